@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged KV-cache path (one GPU).
+
+Default workload: a Llama-3-8B-shaped layer (32 query heads, 8 KV heads,
+head_dim 128, f16 KV, 16-token blocks), 64 sequences with contexts drawn
+uniformly from [2048, 4096], block tables over a permuted pool sized to the
+sequences plus 10% free. One step = append one token per sequence (slot-mapped
+write, kernel 1) + one GQA paged decode-attention pass (kernel 4); contexts
+grow by one per step. Inputs are synthetic (seeded N(0,1)) and resident in HBM
+before the timed region.
+
+Prints one JSON line: the metric, µs per step, the attention kernel's roofline
+(algorithmic bytes / HIP-event time vs 8 TB/s), and the CPU baseline (the
+oracle's restatement of the reference CPU path, timed on this host's cores on
+the same state).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged decode attn µs/step + KV append GB/s (% of HBM roofline), 1 GPU"
+PEAK_HBM_GBPS = 8000.0
+BLOCK = 16
+
+
+def _args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--partition", type=int, default=0, help="attention partition tokens (0 = default)")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0 = host share, max 16)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return p.parse_args()
+
+
+def _cpu_threads(req: int) -> int:
+    if req > 0:
+        return req
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+class Llama3Decode:
+    """The Llama-3-8B decode workload, built through the product's own API."""
+
+    n_heads, n_kv, head_dim, batch = 32, 8, 128, 64
+
+    def __init__(self, steps: int, seed: int, partition: int):
+        import torch
+
+        from langtrain_studio_amd import KvCache
+
+        self.torch = torch
+        dev = torch.device("cuda", 0)
+        self.dev = dev
+        rng = np.random.default_rng(seed)
+        B, kvd = self.batch, self.n_kv * self.head_dim
+        self.kvd = kvd
+        self.steps = steps
+        self.ctx = rng.integers(2048, 4097, B)
+        need = sum(math.ceil((int(c) + steps) / BLOCK) for c in self.ctx)
+        self.n_blocks = int(math.ceil(need * 1.1))
+        stream = torch.cuda.current_stream(dev)
+        self.kv = KvCache(1, kvd, self.n_blocks * BLOCK, dtype="f16", device=0, stream=stream)
+        if partition:
+            self.kv.set_attention_partition(partition)
+        self.order = rng.permutation(self.n_blocks)
+        self.kv.init_free_order(self.order)
+
+        # Prefill: every sequence's positions, claimed through the allocator.
+        self.pre_seqs = np.repeat(np.arange(B, dtype=np.uint32), self.ctx)
+        self.pre_pos = np.concatenate([np.arange(int(c), dtype=np.uint64) for c in self.ctx])
+        sm = self.kv.append_batch(self.pre_seqs, self.pre_pos)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        chunk = 1 << 15
+        for i in range(0, sm.size, chunk):
+            n = min(chunk, sm.size - i)
+            k = torch.randn((n, kvd), generator=gen, device=dev)
+            v = torch.randn((n, kvd), generator=gen, device=dev)
+            self.kv.write_batch(0, torch.from_numpy(sm[i:i + n]).to(dev), k, v)
+        torch.cuda.synchronize()
+
+        # Decode steps: claim every step's cell up front (host bookkeeping is
+        # not part of the device timed region), tables cover the final length.
+        seqs = np.arange(B, dtype=np.uint32)
+        self.step_sm = np.stack([self.kv.append_batch(seqs, (self.ctx + s).astype(np.uint64))
+                                 for s in range(steps)])
+        self.stride = int(math.ceil((int(self.ctx.max()) + steps) / BLOCK))
+        self.tables = self.kv.block_tables(seqs, self.stride)
+        self.lens = np.stack([(self.ctx + s + 1).astype(np.int32) for s in range(steps)])
+        self.d_sm = torch.from_numpy(self.step_sm).to(dev)
+        self.d_tables = torch.from_numpy(self.tables).to(dev)
+        self.d_lens = torch.from_numpy(self.lens).to(dev)
+        rs = np.random.default_rng(seed + 1)
+        self.q = rs.standard_normal((steps, B, self.n_heads * self.head_dim), dtype=np.float32)
+        self.k_new = rs.standard_normal((steps, B, kvd), dtype=np.float32)
+        self.v_new = rs.standard_normal((steps, B, kvd), dtype=np.float32)
+        self.d_q = torch.from_numpy(self.q).to(dev)
+        self.d_k = torch.from_numpy(self.k_new).to(dev)
+        self.d_v = torch.from_numpy(self.v_new).to(dev)
+        self.d_out = torch.empty((B, self.n_heads * self.head_dim), device=dev)
+        torch.cuda.synchronize()
+
+    def append(self, s: int):
+        self.kv.write_batch(0, self.d_sm[s], self.d_k[s], self.d_v[s])
+
+    def attend(self, s: int):
+        self.kv.decode_attention(0, self.d_q[s], self.d_tables, self.d_lens[s], self.n_heads, self.head_dim,
+                                 out=self.d_out)
+
+    # Algorithmic bytes of one launch at step s.
+    def attention_bytes(self, s: int) -> float:
+        lens = self.lens[s].astype(np.int64)
+        kv = lens.sum() * 2 * self.kvd * 2
+        qo = 2 * self.batch * self.n_heads * self.head_dim * 4
+        tables = (-(-lens // BLOCK)).sum() * 4 + self.batch * 4
+        return float(kv + qo + tables)
+
+    def append_bytes(self) -> float:
+        return float(self.batch * self.kvd * (4 + 4 + 2 + 2) + self.batch * 4)
+
+
+def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
+    """The oracle (C++ restatement of kv.rs + model.rs attention + pool.rs)
+    running the same decode steps on the same cache state."""
+    from oracle import OracleKv
+
+    o = OracleKv(1, w.kvd, w.n_blocks * BLOCK, dtype="f16")
+    o.init_free_order(w.order)
+    o.append_batch(w.pre_seqs, w.pre_pos)
+    k, v = w.kv.read_pool(0)  # device state after the GPU run (same cells; the
+    o.load_pool(0, k, v)      # timed steps rewrite the decode cells identically)
+    seqs = np.arange(w.batch, dtype=np.uint32)
+
+    def step(s):
+        sm = o.append_batch(seqs, (w.ctx + s).astype(np.uint64))
+        o.write_batch(0, sm, w.k_new[s], w.v_new[s])
+        o.attention(0, seqs, (w.ctx + s).astype(np.uint64), w.q[s], w.n_heads, w.head_dim, threads=threads)
+
+    times = []
+    t_end = time.perf_counter() + budget_s
+    s = 0
+    while s < w.steps and (s < 2 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        step(s)
+        times.append(time.perf_counter() - t0)
+        s += 1
+    return float(np.mean(times) * 1e6), s
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                          "(the path shards by sequence across GPUs with no exchange, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    steps, warmup = args.steps, args.warmup
+    w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition)
+
+    for s in range(warmup):  # rewrites the same cells with the same data: state unchanged
+        w.append(s)
+        w.attend(s)
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        ev[s][0].record()
+        w.append(s)
+        ev[s][1].record()
+        w.attend(s)
+        ev[s][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = ev[0][0].elapsed_time(ev[-1][2])
+    app_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
+    att_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
+
+    us_step = total_ms * 1e3 / steps
+    att_us = float(att_ms.mean() * 1e3)
+    app_us = float(app_ms.mean() * 1e3)
+    att_bytes = float(np.mean([w.attention_bytes(s) for s in range(steps)]))
+    att_gbps = att_bytes / (att_us * 1e-6) / 1e9
+    app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9
+    roofline_us = att_bytes / (PEAK_HBM_GBPS * 1e9) * 1e6
+
+    cpu = None
+    if not args.no_cpu:
+        threads = _cpu_threads(args.cpu_threads)
+        cpu_us, n = cpu_baseline(w, threads, args.cpu_seconds)
+        cpu = {"value": round(cpu_us, 1), "unit": "µs/step", "cores": threads, "kind": "port",
+               "sample": f"{n} decode steps of the same workload (64 seqs, append+write+attention, "
+                         f"same cache state), oracle C++ restatement, {threads} threads"}
+
+    out = {
+        "metric": METRIC,
+        "value": round(us_step, 2),
+        "unit": "µs/step",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, permuted block pool)",
+        "config": {"workload": "llama3-8b-layer decode: 32q/8kv heads, head_dim 128, f16 KV, block 16, "
+                               "64 seqs ctx U[2048,4096], 1 append + 1 decode attention per step",
+                   "global_batch": 64, "seq_len": "2048-4096", "parallelism": "none (1 GPU)"},
+        "attention_us": round(att_us, 2),
+        "attention_roofline_us": round(roofline_us, 2),
+        "append_us": round(app_us, 2),
+        "append_GBps": round(app_gbps, 1),
+        "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(att_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "attn_kernel + attn_merge_kernel (one decode-attention launch)",
+                     "bytes_per_launch": round(att_bytes)},
+        "wall_s": round(wall, 3),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,193 @@
+/*
+ * ltkv.h - C ABI of the MI355X-native paged KV cache.
+ *
+ * Drop-in for the Langtrain engine's paged KV-cache path. The reference is
+ * Rust: the cache type langtrain_native::kv::KvCache
+ * (engine/crates/native/src/kv.rs:15-188) and its callers, the KV segment of
+ * Model::forward (engine/crates/native/src/model.rs:380-475) and
+ * NativeBackend::decode / kv_remove / kv_copy
+ * (engine/crates/native/src/lib.rs:163-198, behind the Backend trait of
+ * engine/crates/engine/src/backend.rs:17-45). Each entry point below names
+ * the reference item it replaces.
+ *
+ * Model:
+ *  - Host metadata (block allocator, block tables, refcounts) lives in the
+ *    library and has the exact semantics of kv.rs: 16-token blocks, a LIFO
+ *    free stack handing out blocks 0,1,2,... on a fresh cache, refcounted
+ *    prefix sharing and copy-on-write on the first write into a shared block.
+ *  - K and V pools live in device memory (HBM) and are owned by the cache.
+ *    Layout: [layer][block][slot][kv_dim] per pool, as kv.rs:20-22.
+ *  - Device work is enqueued, in call order, on the cache's stream
+ *    (ltkv_set_stream; default: the null stream of the cache's device).
+ *    Device pointers passed in must be valid on that stream.
+ *  - One thread mutates a cache at a time, like KvCache's &mut self methods.
+ *
+ * Status codes: every int-returning call returns LTKV_OK or an LTKV_ERR_*
+ * code and sets a thread-local message readable with ltkv_last_error(). The
+ * messages of the two reference errors are reproduced verbatim:
+ *   LTKV_ERR_FULL       "KV cache full"                               (kv.rs:71)
+ *   LTKV_ERR_NONCONTIG  "seq S: position P is not contiguous (length L)" (kv.rs:88-91)
+ */
+#ifndef LTKV_H
+#define LTKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define LTKV_API __attribute__((visibility("default")))
+#else
+#define LTKV_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTKV_BLOCK 16 /* tokens per block: kv.rs:13 `pub const BLOCK: usize = 16` */
+
+typedef struct ltkv_cache ltkv_cache;
+
+enum {
+  LTKV_OK = 0,
+  LTKV_ERR_FULL = 1,      /* allocator exhausted (kv.rs:67-74) */
+  LTKV_ERR_NONCONTIG = 2, /* append at pos != len (kv.rs:87-92) */
+  LTKV_ERR_RANGE = 3,     /* index out of range (the reference panics: kv.rs:147) */
+  LTKV_ERR_HIP = 4,       /* a HIP runtime call or kernel launch failed */
+  LTKV_ERR_ARG = 5        /* invalid argument */
+};
+
+/* ltkv_create device argument for a metadata-only cache: allocator, tables
+ * and refcounts with no device pools. Every device op on it fails with
+ * LTKV_ERR_ARG (there is no host compute path). */
+#define LTKV_NO_DEVICE (-1)
+
+/* Storage element type. F16 is the reference's (kv.rs:5-6); F32 stores the
+ * f32 input unrounded (same algorithm without the rounding step). */
+enum { LTKV_F16 = 0, LTKV_F32 = 1 };
+
+/* Thread-local message of the last failing call on this thread. */
+LTKV_API const char *ltkv_last_error(void);
+
+/* ---- lifecycle ---------------------------------------------------------- */
+
+/* KvCache::new(n_layers, kv_dim, n_tokens) (kv.rs:35-48): ceil(n_tokens/16)
+ * blocks, zero-filled K and V pools on HIP device `device` (or none for
+ * LTKV_NO_DEVICE), free stack (0..n_blocks).rev(). kv_dim must be a
+ * multiple of 8. */
+LTKV_API int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int device,
+                ltkv_cache **out);
+LTKV_API void ltkv_destroy(ltkv_cache *c);
+
+/* Stream on which all device work of this cache is enqueued (hipStream_t). */
+LTKV_API int ltkv_set_stream(ltkv_cache *c, void *hip_stream);
+
+/* ---- queries (kv.rs:50-60,185-187) ------------------------------------- */
+
+LTKV_API size_t ltkv_capacity(const ltkv_cache *c);    /* KvCache::capacity: n_blocks*16 */
+LTKV_API size_t ltkv_bytes(const ltkv_cache *c);       /* KvCache::bytes: K+V pool bytes */
+LTKV_API size_t ltkv_len(const ltkv_cache *c, uint32_t seq); /* KvCache::len (0 if unknown) */
+LTKV_API size_t ltkv_free_blocks(const ltkv_cache *c); /* KvCache::free_blocks */
+LTKV_API size_t ltkv_n_blocks(const ltkv_cache *c);
+LTKV_API size_t ltkv_kv_dim(const ltkv_cache *c);      /* KvCache::kv_dim */
+LTKV_API uint32_t ltkv_refcount(const ltkv_cache *c, uint32_t block); /* refs[block]; 0 if out of range */
+LTKV_API uint64_t ltkv_cow_copies(const ltkv_cache *c); /* copy-on-write block copies made so far */
+
+/* ---- block management (host; copy-on-write copies go to the stream) ----- */
+
+/* KvCache::append(seq, pos) (kv.rs:85-121): reserve the cell for pos (must
+ * equal len(seq)); returns (block, slot). A copy-on-write of the sequence's
+ * shared last block is enqueued on the stream before returning. */
+LTKV_API int ltkv_append(ltkv_cache *c, uint32_t seq, size_t pos, uint32_t *block, uint32_t *slot);
+
+/* The cell claim of Model::forward (model.rs:380-383) for a whole batch:
+ * append(seqs[i], pos[i]) in order, writing slot_mapping[i] = block*16+slot
+ * (host array). All copy-on-write copies of the batch are enqueued as one
+ * launch before returning, so they precede any later write. On error the
+ * claims before the failing entry stay made (as collect::<Result<_>>()),
+ * their copies are still enqueued, and *n_done (optional) says how many. */
+LTKV_API int ltkv_append_batch(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint64_t *pos,
+                      int32_t *slot_mapping, size_t *n_done);
+
+/* KvCache::truncate(seq, from) (kv.rs:153-169): keep ceil(from/16) blocks;
+ * from == 0 drops the sequence; unknown seq is a no-op. Backend::kv_remove. */
+LTKV_API void ltkv_truncate(ltkv_cache *c, uint32_t seq, size_t from);
+
+/* KvCache::share(src, dst, len) (kv.rs:172-183): dst becomes the first
+ * min(len, len(src)) tokens of src, sharing blocks. Backend::kv_copy. */
+LTKV_API void ltkv_share(ltkv_cache *c, uint32_t src, uint32_t dst, size_t len);
+
+/* Block table of seq (the Seq::blocks of kv.rs:28-32). Writes up to cap
+ * entries; *n_blocks gets the table length. LTKV_ERR_RANGE if cap is short. */
+LTKV_API int ltkv_block_table(const ltkv_cache *c, uint32_t seq, int32_t *out, size_t cap, size_t *n_blocks);
+
+/* Row-major [n][stride] tables for n sequences (host array), for the device
+ * ops below; entries past a table's end are set to -1. */
+LTKV_API int ltkv_block_tables(const ltkv_cache *c, size_t n, const uint32_t *seqs, int32_t *out,
+                      size_t stride);
+
+/* Seed the free stack of a fresh cache (no sequences) so that successive
+ * allocations return order[0], order[1], ...; order is a permutation of
+ * 0..n_blocks-1. The reference's own order is 0,1,2,... (kv.rs:45). */
+LTKV_API int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n);
+
+/* ---- device ops (enqueued on the cache's stream) ----------------------- */
+
+/* Kernel 1, slot-mapped append: KvCache::write (kv.rs:123-131) for n rows,
+ * as the per-token loop of model.rs:414-429. Row i of d_k/d_v (f32, row
+ * stride src_stride >= kv_dim elements) goes to cell d_slot_mapping[i] =
+ * block*16+slot of `layer`, rounded f32->f16 RNE (F16) or stored as is
+ * (F32). Negative or out-of-range slots are skipped. */
+LTKV_API int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+               const float *d_k, const float *d_v, size_t src_stride);
+
+/* Kernel 2, block copy: the copy-on-write body of kv.rs:99-110 (all layers,
+ * K and V) for n pairs d_pairs[2i] = src block, d_pairs[2i+1] = dst block.
+ * ltkv_append and ltkv_append_batch launch it themselves; exposed for bulk
+ * use. Pairs with an out-of-range block are skipped. */
+LTKV_API int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs);
+
+/* Kernel 3, gather: KvCache::rows(layer, seq, len) collected (kv.rs:133-150)
+ * for n sequences. Sequence i has table d_tables[i*table_stride ...] and
+ * length d_lens[i] <= table_stride*16; its rows go to row d_out_offsets[i]
+ * onward of d_k_out / d_v_out ([rows][kv_dim], cache dtype), bit-exact. */
+LTKV_API int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
+                size_t table_stride, const int32_t *d_lens, const int64_t *d_out_offsets,
+                void *d_k_out, void *d_v_out);
+
+/* Kernel 4, GQA paged decode attention: the attention closure of
+ * model.rs:431-475 for n queries. Query i (d_q row i, [n_heads*head_dim] f32)
+ * attends over positions 0..d_lens[i]-1 of the table at
+ * d_tables[i*table_stride]; query head h uses kv head h/(n_heads/n_kv_heads).
+ * Softmax of q.k*scale over the positions, times V; d_out is
+ * [n][n_heads*head_dim] f32. head_dim in {64,128}; group size <= 8.
+ * d_lens[i] == 0 yields zeros. */
+LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
+                          float scale, const float *d_q, const int32_t *d_tables,
+                          size_t table_stride, const int32_t *d_lens, float *d_out);
+
+/* Tokens per context partition of the decode attention split (multiple of
+ * 64; 0 = the default, 256). Results depend on it only through summation
+ * order; they never depend on the other queries of a batch. Tuning knob. */
+LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
+
+/* ---- host conveniences (synchronous on the stream) --------------------- */
+
+/* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */
+LTKV_API int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v);
+
+/* KvCache::rows(layer, seq, n) collected to host [n][kv_dim] buffers. */
+LTKV_API int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v);
+
+/* KvCache::write(layer, block, slot, k, v) (kv.rs:123-131) from host rows. */
+LTKV_API int ltkv_write_row(ltkv_cache *c, size_t layer, uint32_t block, uint32_t slot, const float *h_k,
+                   const float *h_v);
+
+/* Wait for all work enqueued on the cache's stream. */
+LTKV_API int ltkv_synchronize(ltkv_cache *c);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTKV_H */

@@ -1,0 +1,619 @@
+// Host side of the MI355X paged KV cache: block allocator, block tables,
+// refcounted prefix sharing with copy-on-write, and the C ABI of ltkv.h.
+//
+// Metadata semantics follow engine/crates/native/src/kv.rs:15-187 exactly
+// (same allocation order, same refcount rule for copy-on-write, same error
+// messages), so block tables are identical to the reference's for the same
+// call sequence. The K/V pools live in HBM; every device op is enqueued on
+// the cache's stream, in call order.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ltkv.h"
+#include "ltkv_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(LTKV_ERR_HIP, "HIP error in %s: %s", what, hipGetErrorString(e));
+}
+
+int no_device() {
+  return fail(LTKV_ERR_ARG, "metadata-only cache (LTKV_NO_DEVICE): device ops are unavailable");
+}
+
+#define HIP_TRY(call, what)              \
+  do {                                   \
+    hipError_t e_ = (call);              \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+struct Seq {
+  std::vector<int32_t> blocks;  // kv.rs:30
+  size_t len = 0;               // kv.rs:31
+};
+
+// Switches to the cache's device for the scope of a call.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// Context tokens per decode-attention work-group (16 blocks, 4 per wave).
+constexpr size_t kDefaultPartition = 256;
+
+}  // namespace
+
+struct ltkv_cache {
+  int device = 0;
+  int dtype = LTKV_F16;
+  size_t n_layers = 0, kv_dim = 0, n_blocks = 0, elem = 2;
+  ltkv::PoolGeom geom{};
+  void *k = nullptr, *v = nullptr;  // [layer][block][slot][kv_dim]
+  hipStream_t stream = nullptr;
+
+  std::vector<uint32_t> refs;   // kv.rs:23
+  std::vector<int32_t> free;    // kv.rs:24, back() pops first
+  std::unordered_map<uint32_t, Seq> seqs;  // kv.rs:25
+  uint64_t cow_copies = 0;
+
+  // Copy-on-write pair staging: pinned host buffer -> device buffer.
+  std::vector<int32_t> pending;  // (src, dst) pairs of the current claim
+  int32_t *h_pairs = nullptr, *d_pairs = nullptr;
+  size_t pairs_cap = 0;  // pairs
+  hipEvent_t pairs_done = nullptr;
+  bool pairs_in_flight = false;
+
+  // Attention workspace (partition partials), grown on demand.
+  float *ws = nullptr;
+  size_t ws_floats = 0;
+  size_t attn_part_tokens = 0;  // 0 = automatic
+
+  int device_count_cu = 256;
+
+  size_t layer_elems() const { return n_blocks * LTKV_BLOCK * kv_dim; }
+  uint8_t *k_layer(size_t l) const { return (uint8_t *)k + l * layer_elems() * elem; }
+  uint8_t *v_layer(size_t l) const { return (uint8_t *)v + l * layer_elems() * elem; }
+
+  bool alloc(int32_t *b) {  // kv.rs:67-74
+    if (free.empty()) return false;
+    *b = free.back();
+    free.pop_back();
+    refs[*b] = 1;
+    return true;
+  }
+  void release(int32_t b) {  // kv.rs:76-81
+    refs[b] -= 1;
+    if (refs[b] == 0) free.push_back(b);
+  }
+
+  // kv.rs:85-121 without the device copy: a copy-on-write is recorded in
+  // `pending` and launched by the caller before any later device work.
+  int append_meta(uint32_t seq, size_t pos, uint32_t *block, uint32_t *slot) {
+    Seq &s = seqs[seq];  // entry(seq).or_default()
+    if (pos != s.len)
+      return fail(LTKV_ERR_NONCONTIG, "seq %u: position %zu is not contiguous (length %zu)", seq,
+                  pos, s.len);
+    const size_t sl = pos % LTKV_BLOCK;
+    if (sl == 0) {
+      int32_t b;
+      if (!alloc(&b)) return fail(LTKV_ERR_FULL, "KV cache full");
+      s.blocks.push_back(b);
+    } else {
+      const int32_t last = s.blocks.back();
+      if (refs[last] > 1) {  // the sequence diverges from a shared prefix
+        int32_t nb;
+        if (!alloc(&nb)) return fail(LTKV_ERR_FULL, "KV cache full");
+        pending.push_back(last);
+        pending.push_back(nb);
+        release(last);
+        s.blocks.back() = nb;
+        ++cow_copies;
+      }
+    }
+    s.len = pos + 1;
+    *block = (uint32_t)s.blocks.back();
+    *slot = (uint32_t)sl;
+    return LTKV_OK;
+  }
+
+  // Enqueue the pending copy-on-write copies (kernel 2) on the stream.
+  int flush_pending() {
+    if (pending.empty()) return LTKV_OK;
+    if (device == LTKV_NO_DEVICE) {  // no pools: only the metadata changes
+      pending.clear();
+      return LTKV_OK;
+    }
+    const size_t n = pending.size() / 2;
+    DeviceGuard dg(device);
+    if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+    if (pairs_in_flight) {  // the staging buffer may still be read by the last copy
+      HIP_TRY(hipEventSynchronize(pairs_done), "hipEventSynchronize");
+      pairs_in_flight = false;
+    }
+    if (n > pairs_cap) {
+      size_t cap = std::max<size_t>(n, 2 * pairs_cap);
+      cap = std::max<size_t>(cap, 256);
+      if (h_pairs) (void)hipHostFree(h_pairs);
+      if (d_pairs) (void)hipFree(d_pairs);
+      h_pairs = nullptr;
+      d_pairs = nullptr;
+      pairs_cap = 0;
+      HIP_TRY(hipHostMalloc((void **)&h_pairs, cap * 2 * sizeof(int32_t), hipHostMallocDefault),
+              "hipHostMalloc(copy pairs)");
+      HIP_TRY(hipMalloc((void **)&d_pairs, cap * 2 * sizeof(int32_t)), "hipMalloc(copy pairs)");
+      pairs_cap = cap;
+    }
+    std::memcpy(h_pairs, pending.data(), n * 2 * sizeof(int32_t));
+    pending.clear();
+    HIP_TRY(hipMemcpyAsync(d_pairs, h_pairs, n * 2 * sizeof(int32_t), hipMemcpyHostToDevice, stream),
+            "hipMemcpyAsync(copy pairs)");
+    HIP_TRY(hipEventRecord(pairs_done, stream), "hipEventRecord");
+    pairs_in_flight = true;
+    HIP_TRY(ltkv::launch_copy_blocks(geom, (int)n_layers, k, v, d_pairs, (int64_t)n, stream),
+            "copy_blocks launch");
+    return LTKV_OK;
+  }
+
+  void truncate(uint32_t seq, size_t from) {  // kv.rs:153-169
+    auto it = seqs.find(seq);
+    if (it == seqs.end()) return;
+    Seq &s = it->second;
+    if (from >= s.len) return;
+    const size_t keep = (from + LTKV_BLOCK - 1) / LTKV_BLOCK;
+    for (size_t i = keep; i < s.blocks.size(); ++i) release(s.blocks[i]);
+    s.blocks.resize(keep);
+    s.len = from;
+    if (from == 0) seqs.erase(it);
+  }
+
+  void share(uint32_t src, uint32_t dst, size_t len) {  // kv.rs:172-183
+    truncate(dst, 0);
+    auto it = seqs.find(src);
+    if (it == seqs.end()) return;
+    len = std::min(len, it->second.len);
+    const size_t nb = (len + LTKV_BLOCK - 1) / LTKV_BLOCK;
+    std::vector<int32_t> blocks(it->second.blocks.begin(), it->second.blocks.begin() + nb);
+    for (int32_t b : blocks) refs[b] += 1;
+    if (len > 0) seqs[dst] = Seq{std::move(blocks), len};
+  }
+};
+
+extern "C" {
+
+const char *ltkv_last_error(void) { return g_err.c_str(); }
+
+int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int device,
+                ltkv_cache **out) {
+  if (!out) return fail(LTKV_ERR_ARG, "out is null");
+  *out = nullptr;
+  if (n_layers == 0 || kv_dim == 0 || kv_dim % 8 != 0)
+    return fail(LTKV_ERR_ARG, "n_layers must be > 0 and kv_dim a positive multiple of 8");
+  if (dtype != LTKV_F16 && dtype != LTKV_F32) return fail(LTKV_ERR_ARG, "dtype must be F16 or F32");
+  const size_t n_blocks = (n_tokens + LTKV_BLOCK - 1) / LTKV_BLOCK;  // kv.rs:36
+  if (n_blocks > (size_t)INT32_MAX / LTKV_BLOCK)
+    return fail(LTKV_ERR_ARG, "n_tokens too large for 32-bit cell indices");
+  if (device != LTKV_NO_DEVICE) {
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    if (device < 0 || device >= ndev)
+      return fail(LTKV_ERR_ARG, "device %d out of range (%d HIP devices)", device, ndev);
+  }
+
+  ltkv_cache *c = new (std::nothrow) ltkv_cache();
+  if (!c) return fail(LTKV_ERR_ARG, "out of host memory");
+  c->device = device;
+  c->dtype = dtype;
+  c->n_layers = n_layers;
+  c->kv_dim = kv_dim;
+  c->n_blocks = n_blocks;
+  c->elem = dtype == LTKV_F16 ? 2 : 4;
+  c->geom.n_blocks = (int64_t)n_blocks;
+  c->geom.block_stride = (int64_t)(LTKV_BLOCK * kv_dim);
+  c->geom.slot_stride = (int64_t)kv_dim;
+  c->geom.head_stride = 0;  // token-major: set per call from head_dim
+  c->geom.kv_dim = (int)kv_dim;
+  c->geom.elem = (int)c->elem;
+  c->refs.assign(n_blocks, 0);
+  c->free.reserve(n_blocks);
+  for (size_t b = n_blocks; b-- > 0;) c->free.push_back((int32_t)b);  // (0..n).rev()
+
+  if (device == LTKV_NO_DEVICE) {
+    *out = c;
+    return LTKV_OK;
+  }
+  DeviceGuard dg(device);
+  if (!dg.ok) {
+    delete c;
+    return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    c->device_count_cu = prop.multiProcessorCount;
+
+  const size_t bytes = n_layers * c->layer_elems() * c->elem;
+  int rc = LTKV_OK;
+  hipError_t e;
+  if (bytes > 0) {
+    if ((e = hipMalloc(&c->k, bytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(K pool)");
+    else if ((e = hipMalloc(&c->v, bytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(V pool)");
+    else if ((e = hipMemset(c->k, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K pool)");
+    else if ((e = hipMemset(c->v, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
+  }
+  if (rc == LTKV_OK && (e = hipEventCreateWithFlags(&c->pairs_done, hipEventDisableTiming)) != hipSuccess)
+    rc = hip_fail(e, "hipEventCreate");
+  if (rc != LTKV_OK) {
+    ltkv_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return LTKV_OK;
+}
+
+void ltkv_destroy(ltkv_cache *c) {
+  if (!c) return;
+  if (c->device != LTKV_NO_DEVICE) {
+    DeviceGuard dg(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    else (void)hipDeviceSynchronize();
+    if (c->pairs_done) (void)hipEventDestroy(c->pairs_done);
+    if (c->h_pairs) (void)hipHostFree(c->h_pairs);
+    if (c->d_pairs) (void)hipFree(c->d_pairs);
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->k) (void)hipFree(c->k);
+    if (c->v) (void)hipFree(c->v);
+  }
+  delete c;
+}
+
+int ltkv_set_stream(ltkv_cache *c, void *hip_stream) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  c->stream = (hipStream_t)hip_stream;
+  return LTKV_OK;
+}
+
+size_t ltkv_capacity(const ltkv_cache *c) { return c ? c->n_blocks * LTKV_BLOCK : 0; }
+size_t ltkv_bytes(const ltkv_cache *c) {
+  return c ? 2 * c->n_layers * c->layer_elems() * c->elem : 0;
+}
+size_t ltkv_len(const ltkv_cache *c, uint32_t seq) {
+  if (!c) return 0;
+  auto it = c->seqs.find(seq);
+  return it == c->seqs.end() ? 0 : it->second.len;
+}
+size_t ltkv_free_blocks(const ltkv_cache *c) { return c ? c->free.size() : 0; }
+size_t ltkv_n_blocks(const ltkv_cache *c) { return c ? c->n_blocks : 0; }
+size_t ltkv_kv_dim(const ltkv_cache *c) { return c ? c->kv_dim : 0; }
+uint32_t ltkv_refcount(const ltkv_cache *c, uint32_t block) {
+  return (c && block < c->n_blocks) ? c->refs[block] : 0;
+}
+uint64_t ltkv_cow_copies(const ltkv_cache *c) { return c ? c->cow_copies : 0; }
+
+int ltkv_append(ltkv_cache *c, uint32_t seq, size_t pos, uint32_t *block, uint32_t *slot) {
+  if (!c || !block || !slot) return fail(LTKV_ERR_ARG, "null argument");
+  const int rc = c->append_meta(seq, pos, block, slot);
+  const int frc = c->flush_pending();
+  return rc != LTKV_OK ? rc : frc;
+}
+
+int ltkv_append_batch(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint64_t *pos,
+                      int32_t *slot_mapping, size_t *n_done) {
+  if (n_done) *n_done = 0;
+  if (!c || (n && (!seqs || !pos || !slot_mapping))) return fail(LTKV_ERR_ARG, "null argument");
+  int rc = LTKV_OK;
+  size_t i = 0;
+  for (; i < n; ++i) {
+    uint32_t b, s;
+    rc = c->append_meta(seqs[i], (size_t)pos[i], &b, &s);
+    if (rc != LTKV_OK) break;
+    slot_mapping[i] = (int32_t)(b * LTKV_BLOCK + s);
+  }
+  if (n_done) *n_done = i;
+  const std::string err = g_err;
+  const int frc = c->flush_pending();
+  if (rc != LTKV_OK) {
+    g_err = err;
+    return rc;
+  }
+  return frc;
+}
+
+void ltkv_truncate(ltkv_cache *c, uint32_t seq, size_t from) {
+  if (c) c->truncate(seq, from);
+}
+
+void ltkv_share(ltkv_cache *c, uint32_t src, uint32_t dst, size_t len) {
+  if (c) c->share(src, dst, len);
+}
+
+int ltkv_block_table(const ltkv_cache *c, uint32_t seq, int32_t *out, size_t cap, size_t *n_blocks) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  auto it = c->seqs.find(seq);
+  const size_t nb = it == c->seqs.end() ? 0 : it->second.blocks.size();
+  if (n_blocks) *n_blocks = nb;
+  if (nb > cap) return fail(LTKV_ERR_RANGE, "table of seq %u has %zu blocks, capacity %zu", seq, nb, cap);
+  if (nb && !out) return fail(LTKV_ERR_ARG, "out is null");
+  if (nb) std::memcpy(out, it->second.blocks.data(), nb * sizeof(int32_t));
+  return LTKV_OK;
+}
+
+int ltkv_block_tables(const ltkv_cache *c, size_t n, const uint32_t *seqs, int32_t *out,
+                      size_t stride) {
+  if (!c || (n && (!seqs || !out))) return fail(LTKV_ERR_ARG, "null argument");
+  for (size_t i = 0; i < n; ++i) {
+    auto it = c->seqs.find(seqs[i]);
+    const size_t nb = it == c->seqs.end() ? 0 : it->second.blocks.size();
+    if (nb > stride)
+      return fail(LTKV_ERR_RANGE, "table of seq %u has %zu blocks, stride %zu", seqs[i], nb, stride);
+    int32_t *row = out + i * stride;
+    if (nb) std::memcpy(row, it->second.blocks.data(), nb * sizeof(int32_t));
+    std::fill(row + nb, row + stride, -1);
+  }
+  return LTKV_OK;
+}
+
+int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n) {
+  if (!c || (n && !order)) return fail(LTKV_ERR_ARG, "null argument");
+  if (!c->seqs.empty() || c->free.size() != c->n_blocks)
+    return fail(LTKV_ERR_ARG, "init_free_order needs a cache with no sequences");
+  if (n != c->n_blocks) return fail(LTKV_ERR_ARG, "order has %zu entries, cache has %zu blocks", n, c->n_blocks);
+  std::vector<uint8_t> seen(n, 0);
+  for (size_t i = 0; i < n; ++i) {
+    if (order[i] >= n || seen[order[i]]) return fail(LTKV_ERR_ARG, "order is not a permutation");
+    seen[order[i]] = 1;
+  }
+  c->free.clear();
+  for (size_t i = n; i-- > 0;) c->free.push_back((int32_t)order[i]);
+  return LTKV_OK;
+}
+
+int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+               const float *d_k, const float *d_v, size_t src_stride) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (n == 0) return LTKV_OK;
+  if (!d_slot_mapping || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (src_stride < c->kv_dim || src_stride % 4 != 0)
+    return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
+  if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0) return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
+  if ((uint64_t)n * (c->kv_dim / 8) >= (1ull << 32) - 256)
+    return fail(LTKV_ERR_ARG, "too many rows for one launch");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  HIP_TRY(ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping, d_k,
+                             d_v, (int64_t)n, (int64_t)src_stride, c->stream),
+          "write launch");
+  return LTKV_OK;
+}
+
+int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (n == 0) return LTKV_OK;
+  if (!d_pairs) return fail(LTKV_ERR_ARG, "null device pointer");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  HIP_TRY(ltkv::launch_copy_blocks(c->geom, (int)c->n_layers, c->k, c->v, d_pairs, (int64_t)n, c->stream),
+          "copy_blocks launch");
+  return LTKV_OK;
+}
+
+int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
+                size_t table_stride, const int32_t *d_lens, const int64_t *d_out_offsets,
+                void *d_k_out, void *d_v_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (n == 0 || table_stride == 0) return LTKV_OK;
+  if (!d_tables || !d_lens || !d_out_offsets || !d_k_out || !d_v_out)
+    return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_k_out | (uintptr_t)d_v_out) % 16 != 0)
+    return fail(LTKV_ERR_ARG, "outputs must be 16-byte aligned");
+  if ((uint64_t)n * table_stride * 256 >= (1ull << 32))
+    return fail(LTKV_ERR_ARG, "n * table_stride too large for one launch");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  HIP_TRY(ltkv::launch_gather(c->geom, c->k_layer(layer), c->v_layer(layer), d_tables,
+                              (int64_t)table_stride, d_lens, d_out_offsets, (int64_t)n, d_k_out,
+                              d_v_out, c->stream),
+          "gather launch");
+  return LTKV_OK;
+}
+
+int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (tokens % 64 != 0) return fail(LTKV_ERR_ARG, "partition must be a multiple of 64 tokens");
+  c->attn_part_tokens = tokens;
+  return LTKV_OK;
+}
+
+int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
+                          float scale, const float *d_q, const int32_t *d_tables,
+                          size_t table_stride, const int32_t *d_lens, float *d_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (head_dim == 0 || c->kv_dim % head_dim != 0)
+    return fail(LTKV_ERR_ARG, "head_dim %zu does not divide kv_dim %zu", head_dim, c->kv_dim);
+  const size_t n_kv_heads = c->kv_dim / head_dim;
+  if (n_heads == 0 || n_heads % n_kv_heads != 0)
+    return fail(LTKV_ERR_ARG, "n_heads %zu is not a multiple of n_kv_heads %zu", n_heads, n_kv_heads);
+  const size_t group = n_heads / n_kv_heads;
+  if (!ltkv::attention_supported((int)c->elem, (int)head_dim, (int)group))
+    return fail(LTKV_ERR_ARG, "unsupported shape: head_dim %zu (64 or 128), group %zu (1..8)", head_dim, group);
+  if (n == 0) return LTKV_OK;
+  if (table_stride == 0) return fail(LTKV_ERR_ARG, "table_stride must be > 0");
+  if (!d_q || !d_tables || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
+
+  // The partition size never depends on the batch, so a query's result is
+  // bit-identical whatever else is in the batch (the reference's property,
+  // engine/README.md:102). table_stride only bounds the grid.
+  const size_t max_tokens = table_stride * LTKV_BLOCK;
+  const size_t part = c->attn_part_tokens ? c->attn_part_tokens : kDefaultPartition;
+  const size_t max_parts = (max_tokens + part - 1) / part;
+  if ((uint64_t)n * n_kv_heads * max_parts * 256 >= (1ull << 32))
+    return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
+
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  const int64_t need = ltkv::attention_workspace_floats((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
+  if ((size_t)need > c->ws_floats) {
+    if (c->ws) {
+      // The old workspace may still be read by enqueued work.
+      HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+      HIP_TRY(hipFree(c->ws), "hipFree(workspace)");
+      c->ws = nullptr;
+      c->ws_floats = 0;
+    }
+    HIP_TRY(hipMalloc((void **)&c->ws, (size_t)need * sizeof(float)), "hipMalloc(workspace)");
+    c->ws_floats = (size_t)need;
+  }
+  ltkv::PoolGeom g = c->geom;
+  g.head_stride = (int64_t)head_dim;  // token-major: heads are adjacent in a row
+  ltkv::AttnArgs a{};
+  a.k_layer = c->k_layer(layer);
+  a.v_layer = c->v_layer(layer);
+  a.q = d_q;
+  a.tables = d_tables;
+  a.table_stride = (int64_t)table_stride;
+  a.lens = d_lens;
+  a.out = d_out;
+  a.part_o = c->ws;
+  a.part_ml = c->ws ? c->ws + n * n_heads * max_parts * head_dim : nullptr;
+  a.n = (int64_t)n;
+  a.n_heads = (int)n_heads;
+  a.n_kv_heads = (int)n_kv_heads;
+  a.head_dim = (int)head_dim;
+  a.scale = scale;
+  a.part_tokens = (int)part;
+  a.max_parts = (int)max_parts;
+  HIP_TRY(ltkv::launch_decode_attention(g, a, c->stream), "decode attention launch");
+  return LTKV_OK;
+}
+
+int ltkv_synchronize(ltkv_cache *c) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  return LTKV_OK;
+}
+
+int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (!h_k || !h_v) return fail(LTKV_ERR_ARG, "null host pointer");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  const size_t bytes = c->layer_elems() * c->elem;
+  HIP_TRY(hipMemcpyAsync(h_k, c->k_layer(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read K pool");
+  HIP_TRY(hipMemcpyAsync(h_v, c->v_layer(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read V pool");
+  HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  return LTKV_OK;
+}
+
+int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (n == 0) return LTKV_OK;
+  if (!h_k || !h_v) return fail(LTKV_ERR_ARG, "null host pointer");
+  auto it = c->seqs.find(seq);
+  const size_t nb = it == c->seqs.end() ? 0 : it->second.blocks.size();
+  if ((n + LTKV_BLOCK - 1) / LTKV_BLOCK > nb)
+    return fail(LTKV_ERR_RANGE, "rows(%u, %zu): sequence has %zu blocks", seq, n, nb);
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  // Staging: [table | len | offset] then K and V rows, in one device buffer.
+  const size_t tb = (n + LTKV_BLOCK - 1) / LTKV_BLOCK;
+  const size_t row_bytes = c->kv_dim * c->elem;
+  const size_t off_pos = (tb * 4 + 4 + 7) / 8 * 8;  // int64 output offset, 8-aligned
+  const size_t meta = (off_pos + 8 + 255) / 256 * 256;
+  const size_t total = meta + 2 * n * row_bytes;
+  uint8_t *d = nullptr;
+  HIP_TRY(hipMalloc((void **)&d, total), "hipMalloc(rows staging)");
+  std::vector<uint8_t> h(meta, 0);
+  std::memcpy(h.data(), it->second.blocks.data(), tb * 4);
+  const int32_t len = (int32_t)n;
+  const int64_t off = 0;
+  std::memcpy(h.data() + tb * 4, &len, 4);
+  std::memcpy(h.data() + off_pos, &off, 8);
+  hipError_t e = hipMemcpyAsync(d, h.data(), meta, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess)
+    e = ltkv::launch_gather(c->geom, c->k_layer(layer), c->v_layer(layer), (const int32_t *)d,
+                            (int64_t)tb, (const int32_t *)(d + tb * 4), (const int64_t *)(d + off_pos),
+                            1, d + meta, d + meta + n * row_bytes, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(h_k, d + meta, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(h_v, d + meta + n * row_bytes, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "rows");
+  return LTKV_OK;
+}
+
+int ltkv_write_row(ltkv_cache *c, size_t layer, uint32_t block, uint32_t slot, const float *h_k,
+                   const float *h_v) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (block >= c->n_blocks || slot >= LTKV_BLOCK)
+    return fail(LTKV_ERR_RANGE, "cell (%u, %u) out of range", block, slot);
+  if (!h_k || !h_v) return fail(LTKV_ERR_ARG, "null host pointer");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  // Staging: [slot mapping (16 bytes) | K row | V row].
+  const size_t row = c->kv_dim * sizeof(float);
+  const size_t total = 16 + 2 * row;
+  std::vector<uint8_t> h(total, 0);
+  const int32_t cell = (int32_t)(block * LTKV_BLOCK + slot);
+  std::memcpy(h.data(), &cell, 4);
+  std::memcpy(h.data() + 16, h_k, row);
+  std::memcpy(h.data() + 16 + row, h_v, row);
+  uint8_t *d = nullptr;
+  HIP_TRY(hipMalloc((void **)&d, total), "hipMalloc(row staging)");
+  hipError_t e = hipMemcpyAsync(d, h.data(), total, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess)
+    e = ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), (const int32_t *)d,
+                           (const float *)(d + 16), (const float *)(d + 16 + row), 1,
+                           (int64_t)c->kv_dim, c->stream);
+  if (e == hipSuccess) e = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "write_row");
+  return LTKV_OK;
+}
+
+}  // extern "C"

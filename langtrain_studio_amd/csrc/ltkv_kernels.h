@@ -1,0 +1,55 @@
+// Internal launcher interface between the host block manager (ltkv_cache.cpp)
+// and the gfx950 kernels (ltkv_kernels.hip). Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace ltkv {
+
+constexpr int kBlock = 16;  // tokens per block (kv.rs:13)
+
+// Geometry of one layer of a pool: element (block, slot, head, i) lives at
+// block*block_stride + head*head_stride + slot*slot_stride + i.
+struct PoolGeom {
+  int64_t n_blocks;
+  int64_t block_stride;  // elements per block (16 * kv_dim)
+  int64_t slot_stride;   // elements between consecutive slots of a block
+  int64_t head_stride;   // elements between consecutive kv heads of a block
+  int kv_dim;
+  int elem;              // bytes per element: 2 (f16) or 4 (f32)
+};
+
+hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
+                        const float *k, const float *v, int64_t n, int64_t src_stride,
+                        hipStream_t s);
+
+hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
+                              const int32_t *pairs, int64_t n_pairs, hipStream_t s);
+
+hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_layer,
+                         const int32_t *tables, int64_t table_stride, const int32_t *lens,
+                         const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
+                         hipStream_t s);
+
+struct AttnArgs {
+  const void *k_layer, *v_layer;
+  const float *q;
+  const int32_t *tables;
+  int64_t table_stride;
+  const int32_t *lens;
+  float *out;
+  float *part_o;   // [n][n_heads][max_parts][head_dim] partial numerators
+  float *part_ml;  // [n][n_heads][max_parts][2] partial (max, sum), log2 domain
+  int64_t n;
+  int n_heads, n_kv_heads, head_dim;
+  float scale;
+  int part_tokens, max_parts;
+};
+
+// Workspace floats needed by launch_decode_attention for these arguments.
+int64_t attention_workspace_floats(int64_t n, int n_heads, int head_dim, int max_parts);
+bool attention_supported(int elem, int head_dim, int group);
+hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
+
+}  // namespace ltkv

@@ -1,0 +1,574 @@
+// gfx950 (MI355X, CDNA4) kernels of the paged KV-cache path.
+//
+//   write_kernel       slot-mapped K/V append   (kv.rs:123-131 write, per model.rs:414-429)
+//   copy_blocks_kernel copy-on-write block copy (kv.rs:99-110)
+//   gather_kernel      block-table gather       (kv.rs:133-150 rows, collected)
+//   attn_kernel        GQA paged decode attention, split over context partitions
+//   attn_merge_kernel  log-sum-exp merge of the partitions (model.rs:431-475 semantics)
+//
+// Every kernel is HBM-bandwidth bound: the data-movement kernels move each
+// byte once with 16-byte (dwordx4) accesses, and decode attention does ~4
+// flop per KV byte, far below the vector-ALU ridge point, so no MFMA is used.
+// Wavefronts are 64 lanes; reductions use DPP row permutations within a wave.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ltkv_kernels.h"
+
+namespace ltkv {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ----------------------------------------------------------------------------
+// f32 -> f16, IEEE round-to-nearest-even (the conversion of f16::from_f32).
+// v_cvt_f16_f32 rounds to nearest even in the default mode; NaN is rewritten
+// explicitly so the result is sign | 0x7e00 | top payload bits on every part.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+  const _Float16 h = (_Float16)x;
+  uint32_t b = (uint32_t)__builtin_bit_cast(uint16_t, h);
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) b = ((u >> 16) & 0x8000u) | 0x7e00u | ((u >> 13) & 0x3ffu);
+  return b;
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return f16_bits(a) | (f16_bits(b) << 16);
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 1: slot-mapped append. One thread moves 8 consecutive elements of
+// one token row of K and of V: two 32-byte f32 reads each, one 16-byte f16
+// write each (or two 16-byte f32 writes).
+// ----------------------------------------------------------------------------
+template <int ELEM>
+__global__ void __launch_bounds__(256)
+write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
+             const int32_t *__restrict__ slots, const float *__restrict__ k,
+             const float *__restrict__ v, int64_t n, int64_t src_stride, int kv_dim,
+             int64_t n_slots) {
+  const int chunks = kv_dim >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / chunks;
+  if (row >= n) return;
+  const int c = (int)(gid - row * chunks);
+  const int32_t s = slots[row];
+  if (s < 0 || (int64_t)s >= n_slots) return;
+  const int col = c << 3;
+  const int64_t dst = (int64_t)s * kv_dim + col;  // cell block*16+slot, token-major row
+
+  const f32x4 *ks = reinterpret_cast<const f32x4 *>(k + row * src_stride + col);
+  const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
+  const f32x4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+  if constexpr (ELEM == 2) {
+    u32x4 ko, vo;
+    ko.x = pack_f16x2(k0.x, k0.y);
+    ko.y = pack_f16x2(k0.z, k0.w);
+    ko.z = pack_f16x2(k1.x, k1.y);
+    ko.w = pack_f16x2(k1.z, k1.w);
+    vo.x = pack_f16x2(v0.x, v0.y);
+    vo.y = pack_f16x2(v0.z, v0.w);
+    vo.z = pack_f16x2(v1.x, v1.y);
+    vo.w = pack_f16x2(v1.z, v1.w);
+    *reinterpret_cast<u32x4 *>(kpool + dst * 2) = ko;
+    *reinterpret_cast<u32x4 *>(vpool + dst * 2) = vo;
+  } else {
+    f32x4 *kd = reinterpret_cast<f32x4 *>(kpool + dst * 4);
+    f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
+    kd[0] = k0;
+    kd[1] = k1;
+    vd[0] = v0;
+    vd[1] = v1;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 2: block copy. Work item = (pair, layer, tensor, 16 KiB chunk); 256
+// threads each move 4 x 16 bytes, all loads issued before the stores.
+// ----------------------------------------------------------------------------
+constexpr int kCopyUnroll = 4;
+constexpr int64_t kCopyChunk = 256 * 16 * kCopyUnroll;  // bytes per work-group
+
+__global__ void __launch_bounds__(256)
+copy_blocks_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
+                   const int32_t *__restrict__ pairs, int64_t n_blocks, int n_layers,
+                   int64_t block_bytes, int64_t layer_bytes, int chunks_per_block) {
+  int64_t wg = blockIdx.x;
+  const int chunk = (int)(wg % chunks_per_block);
+  wg /= chunks_per_block;
+  const int tensor = (int)(wg & 1);
+  wg >>= 1;
+  const int layer = (int)(wg % n_layers);
+  const int64_t pair = wg / n_layers;
+  const int32_t src = pairs[2 * pair], dst = pairs[2 * pair + 1];
+  if (src < 0 || dst < 0 || src >= n_blocks || dst >= n_blocks || src == dst) return;
+  uint8_t *base = (tensor ? vpool : kpool) + (int64_t)layer * layer_bytes;
+  const u32x4 *s = reinterpret_cast<const u32x4 *>(base + (int64_t)src * block_bytes);
+  u32x4 *d = reinterpret_cast<u32x4 *>(base + (int64_t)dst * block_bytes);
+  const int64_t n16 = block_bytes >> 4;
+  const int64_t i0 = chunk * (kCopyChunk >> 4) + threadIdx.x;
+  u32x4 r[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = i0 + u * 256;
+    if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
+  }
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = i0 + u * 256;
+    if (i < n16) d[i] = r[u];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 3: gather. Work item = (sequence, table entry): the valid rows of
+// one block of K and of V are copied to their contiguous place. A row of the
+// token-major layout is contiguous, so the block's valid prefix is one
+// contiguous run in source and destination.
+// ----------------------------------------------------------------------------
+constexpr int kGatherUnroll = 8;
+
+__device__ __forceinline__ void copy_run(const u32x4 *__restrict__ s, u32x4 *__restrict__ d,
+                                         int64_t n16) {
+  for (int64_t base = 0; base < n16; base += 256 * kGatherUnroll) {
+    u32x4 r[kGatherUnroll];
+#pragma unroll
+    for (int u = 0; u < kGatherUnroll; ++u) {
+      const int64_t i = base + u * 256 + threadIdx.x;
+      if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kGatherUnroll; ++u) {
+      const int64_t i = base + u * 256 + threadIdx.x;
+      if (i < n16) __builtin_nontemporal_store(r[u], d + i);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpool,
+              const int32_t *__restrict__ tables, int64_t table_stride,
+              const int32_t *__restrict__ lens, const int64_t *__restrict__ out_offsets,
+              uint8_t *__restrict__ kout, uint8_t *__restrict__ vout, int64_t n_blocks,
+              int64_t row_bytes) {
+  const int64_t wg = blockIdx.x;
+  const int64_t seq = wg / table_stride;
+  const int64_t j = wg - seq * table_stride;
+  int64_t len = lens[seq];
+  if (len > table_stride * 16) len = table_stride * 16;
+  const int64_t start = j * 16;
+  if (start >= len) return;
+  const int64_t rows = len - start < 16 ? len - start : 16;
+  const int32_t blk = tables[seq * table_stride + j];
+  if (blk < 0 || blk >= n_blocks) return;
+  const int64_t n16 = (rows * row_bytes) >> 4;
+  const int64_t src = (int64_t)blk * 16 * row_bytes;
+  const int64_t dst = (out_offsets[seq] + start) * row_bytes;
+  copy_run(reinterpret_cast<const u32x4 *>(kpool + src), reinterpret_cast<u32x4 *>(kout + dst), n16);
+  copy_run(reinterpret_cast<const u32x4 *>(vpool + src), reinterpret_cast<u32x4 *>(vout + dst), n16);
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 4: GQA paged decode attention.
+//
+// Work-group = 4 waves on (query, kv head, context partition). The waves take
+// the partition's blocks round-robin. For one block a wave reads the head's
+// 16 x head_dim K tile and V tile with 16-byte loads: L lanes cover one row,
+// so a wave load covers 64/L rows. Each lane keeps the g query heads of its
+// column slice in registers (pre-scaled by scale*log2 e) and computes partial
+// dots; a DPP butterfly over the L lanes finishes each score. Online softmax
+// (exp2 domain) runs per row group, so no cross-row-group traffic happens in
+// the block loop; row groups, then waves (through LDS) are merged once at the
+// end. With one partition the work-group writes the normalised output, else
+// it writes (numerator, max, sum) for attn_merge_kernel.
+// ----------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each aligned group of L lanes (L in 4..32); every lane gets it.
+template <int L>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp<0xB1>(x);  // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);  // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) x += dpp<0x141>(x);  // row_half_mirror
+  if constexpr (L >= 16) x += dpp<0x140>(x); // row_mirror
+  if constexpr (L >= 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+template <typename T>
+struct Tile;
+
+template <>
+struct Tile<_Float16> {
+  static constexpr int E = 8;  // elements per 16-byte load
+  __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[8]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = __builtin_bit_cast(h2, u.x), b = __builtin_bit_cast(h2, u.y);
+    const h2 c = __builtin_bit_cast(h2, u.z), d = __builtin_bit_cast(h2, u.w);
+    f[0] = (float)a.x; f[1] = (float)a.y; f[2] = (float)b.x; f[3] = (float)b.y;
+    f[4] = (float)c.x; f[5] = (float)c.y; f[6] = (float)d.x; f[7] = (float)d.y;
+  }
+};
+
+template <>
+struct Tile<float> {
+  static constexpr int E = 4;
+  __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[4]) {
+    f[0] = __builtin_bit_cast(float, u.x);
+    f[1] = __builtin_bit_cast(float, u.y);
+    f[2] = __builtin_bit_cast(float, u.z);
+    f[3] = __builtin_bit_cast(float, u.w);
+  }
+};
+
+constexpr int kAttnWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T, int HD, int G>
+__global__ void __launch_bounds__(256)
+attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
+            const int32_t *__restrict__ tables, int64_t table_stride,
+            const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
+            float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
+            int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
+            int max_parts) {
+  constexpr int E = Tile<T>::E;
+  constexpr int L = HD / E;        // lanes per row
+  constexpr int RPL = 64 / L;      // rows per wave load
+  constexpr int LOADS = 16 / RPL;  // wave loads per 16-row tile
+  static_assert(L >= 4 && L <= 32 && LOADS >= 1, "unsupported head_dim / dtype");
+
+  // 1-D grid, kv head fastest: the work-groups reading the same blocks of a
+  // query (one per kv head) are dispatched together.
+  const int kvh = (int)(blockIdx.x % n_kv_heads);
+  const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
+  const int64_t qi = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane % L, rg = lane / L;
+  const int n_heads = n_kv_heads * G;
+
+  int64_t len = lens[qi];
+  if (len < 0) len = 0;
+  if (len > table_stride * 16) len = table_stride * 16;
+  const int64_t tok0 = (int64_t)part * part_tokens;
+  if (part > 0 && tok0 >= len) return;  // uniform over the work-group
+  const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
+  const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
+
+  float qv[G][E];
+  {
+    const float *qp = q + qi * (int64_t)n_heads * HD + (int64_t)kvh * G * HD + c * E;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const f32x4 t = *reinterpret_cast<const f32x4 *>(qp + h * HD + e);
+        qv[h][e] = t.x * qscale;
+        qv[h][e + 1] = t.y * qscale;
+        qv[h][e + 2] = t.z * qscale;
+        qv[h][e + 3] = t.w * qscale;
+      }
+  }
+
+  float m[G], l[G], acc[G][E];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+  }
+
+  const int32_t *tab = tables + qi * table_stride;
+  const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
+  const int64_t head_off = (int64_t)kvh * head_stride;
+
+  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
+    int32_t blk = tab[b];
+    if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
+    const int64_t base = (int64_t)blk * block_stride + head_off + lane_off;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int64_t o = base + (int64_t)j * RPL * slot_stride;
+      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kpool + o));
+      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vpool + o));
+    }
+  };
+
+  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
+    const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
+    float s[LOADS][G];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      float kf[E];
+      Tile<T>::unpack(kr[j], kf);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) a = __builtin_fmaf(qv[h][e], kf[e], a);
+        s[j][h] = group_sum<L>(a);
+      }
+    }
+    if (valid < 16) {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j)
+        if (rg + j * RPL >= valid)
+#pragma unroll
+          for (int h = 0; h < G; ++h) s[j][h] = -INFINITY;
+    }
+    float p[LOADS][G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float bm = s[0][h];
+#pragma unroll
+      for (int j = 1; j < LOADS; ++j) bm = __builtin_fmaxf(bm, s[j][h]);
+      const float mn = __builtin_fmaxf(m[h], bm);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m[h] - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        p[j][h] = __builtin_amdgcn_exp2f(s[j][h] - mref);
+        ps += p[j][h];
+      }
+      l[h] = l[h] * alpha + ps;
+      m[h] = mn;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[h][e] *= alpha;
+    }
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      float vf[E];
+      Tile<T>::unpack(vr[j], vf);
+      if (valid < 16 && rg + j * RPL >= valid) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) vf[e] = 0.f;  // stale slots may hold non-finite bits
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(p[j][h], vf[e], acc[h][e]);
+    }
+  };
+
+  // Software pipeline: the next tile's loads are in flight while the current
+  // one is computed. Past the end the prefetch re-reads the current tile
+  // (cache hit) so the wait counts stay static.
+  {
+    u32x4 ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
+    int b = b0 + wave;
+    if (b < b1) load_tile(b, ka, va);
+    while (b < b1) {
+      const int bn = b + kAttnWaves < b1 ? b + kAttnWaves : b;
+      load_tile(bn, kb, vb);
+      compute_tile(b, ka, va);
+      b += kAttnWaves;
+      if (b >= b1) break;
+      const int bn2 = b + kAttnWaves < b1 ? b + kAttnWaves : b;
+      load_tile(bn2, ka, va);
+      compute_tile(b, kb, vb);
+      b += kAttnWaves;
+    }
+  }
+
+  // Merge the row groups of the wave (lanes L, 2L, .. apart hold the same column).
+#pragma unroll
+  for (int off = L; off < 64; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mo = __shfl_xor(m[h], off);
+      const float lo = __shfl_xor(l[h], off);
+      const float mn = __builtin_fmaxf(m[h], mo);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float as = __builtin_amdgcn_exp2f(m[h] - mref);
+      const float ao = __builtin_amdgcn_exp2f(mo - mref);
+      l[h] = l[h] * as + lo * ao;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float other = __shfl_xor(acc[h][e], off);
+        acc[h][e] = acc[h][e] * as + other * ao;
+      }
+      m[h] = mn;
+    }
+  }
+
+  // Merge the waves through LDS.
+  __shared__ float sm_acc[kAttnWaves][G][HD];
+  __shared__ float sm_m[kAttnWaves][G], sm_l[kAttnWaves][G];
+  if (rg == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) sm_acc[wave][h][c * E + e] = acc[h][e];
+      if (c == 0) {
+        sm_m[wave][h] = m[h];
+        sm_l[wave][h] = l[h];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
+    const int h = idx / HD, d = idx - h * HD;
+    float mx = sm_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float a = __builtin_amdgcn_exp2f(sm_m[w][h] - mref);
+      lsum += sm_l[w][h] * a;
+      o += sm_acc[w][h][d] * a;
+    }
+    const int64_t qh = qi * n_heads + (int64_t)kvh * G + h;
+    if (max_parts == 1) {
+      out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+    } else {
+      const int64_t pi = qh * max_parts + part;
+      part_o[pi * HD + d] = o;
+      if (d == 0) {
+        part_ml[2 * pi] = mx;
+        part_ml[2 * pi + 1] = lsum;
+      }
+    }
+  }
+}
+
+// Merge of the context partitions of one (query, head): O = sum_p o_p 2^(m_p-M),
+// L = sum_p l_p 2^(m_p-M), out = O / L. One thread per output element.
+template <int HD>
+__global__ void __launch_bounds__(HD)
+attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
+                  const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
+                  int part_tokens, int max_parts, int64_t max_len) {
+  const int h = (int)(blockIdx.x % n_heads);
+  const int64_t qi = blockIdx.x / n_heads;
+  const int d = threadIdx.x;
+  int64_t len = lens[qi];
+  if (len < 0) len = 0;
+  if (len > max_len) len = max_len;
+  int np = (int)((len + part_tokens - 1) / part_tokens);
+  if (np < 1) np = 1;
+  const int64_t qh = qi * n_heads + h;
+  const float *ml = part_ml + qh * max_parts * 2;
+  float mx = -INFINITY;
+  for (int p = 0; p < np; ++p) mx = __builtin_fmaxf(mx, ml[2 * p]);
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  float lsum = 0.f, o = 0.f;
+  for (int p = 0; p < np; ++p) {
+    const float a = __builtin_amdgcn_exp2f(ml[2 * p] - mref);
+    lsum += ml[2 * p + 1] * a;
+    o += part_o[(qh * max_parts + p) * HD + d] * a;
+  }
+  out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+}
+
+template <typename T, int HD, int G>
+hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
+  attn_kernel<T, HD, G><<<grid, 256, 0, s>>>(
+      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
+      a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
+      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.max_parts == 1) return e;
+  const unsigned mgrid = (unsigned)(a.n * a.n_heads);
+  attn_merge_kernel<HD><<<mgrid, HD, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
+                                             a.part_tokens, a.max_parts, a.table_stride * 16);
+  return hipGetLastError();
+}
+
+template <typename T, int HD>
+hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  switch (a.n_heads / a.n_kv_heads) {
+    case 1: return launch_attn_t<T, HD, 1>(g, a, s);
+    case 2: return launch_attn_t<T, HD, 2>(g, a, s);
+    case 3: return launch_attn_t<T, HD, 3>(g, a, s);
+    case 4: return launch_attn_t<T, HD, 4>(g, a, s);
+    case 5: return launch_attn_t<T, HD, 5>(g, a, s);
+    case 6: return launch_attn_t<T, HD, 6>(g, a, s);
+    case 7: return launch_attn_t<T, HD, 7>(g, a, s);
+    case 8: return launch_attn_t<T, HD, 8>(g, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
+                        const float *k, const float *v, int64_t n, int64_t src_stride,
+                        hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t threads = n * (g.kv_dim >> 3);
+  const int64_t blocks = (threads + 255) / 256;
+  if (g.elem == 2)
+    write_kernel<2><<<(unsigned)blocks, 256, 0, s>>>(
+        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n,
+        src_stride, g.kv_dim, g.n_blocks * 16);
+  else
+    write_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(
+        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n,
+        src_stride, g.kv_dim, g.n_blocks * 16);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
+                              const int32_t *pairs, int64_t n_pairs, hipStream_t s) {
+  if (n_pairs <= 0) return hipSuccess;
+  const int64_t block_bytes = g.block_stride * g.elem;
+  const int64_t layer_bytes = g.n_blocks * block_bytes;
+  const int chunks = (int)((block_bytes + kCopyChunk - 1) / kCopyChunk);
+  const int64_t wgs = n_pairs * n_layers * 2 * chunks;
+  copy_blocks_kernel<<<(unsigned)wgs, 256, 0, s>>>(static_cast<uint8_t *>(k_pool),
+                                                   static_cast<uint8_t *>(v_pool), pairs,
+                                                   g.n_blocks, n_layers, block_bytes,
+                                                   layer_bytes, chunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_layer,
+                         const int32_t *tables, int64_t table_stride, const int32_t *lens,
+                         const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
+                         hipStream_t s) {
+  if (n <= 0 || table_stride <= 0) return hipSuccess;
+  const int64_t wgs = n * table_stride;
+  gather_kernel<<<(unsigned)wgs, 256, 0, s>>>(
+      static_cast<const uint8_t *>(k_layer), static_cast<const uint8_t *>(v_layer), tables,
+      table_stride, lens, out_offsets, static_cast<uint8_t *>(k_out),
+      static_cast<uint8_t *>(v_out), g.n_blocks, (int64_t)g.kv_dim * g.elem);
+  return hipGetLastError();
+}
+
+int64_t attention_workspace_floats(int64_t n, int n_heads, int head_dim, int max_parts) {
+  if (max_parts <= 1) return 0;
+  return n * n_heads * (int64_t)max_parts * (head_dim + 2);
+}
+
+bool attention_supported(int elem, int head_dim, int group) {
+  return (elem == 2 || elem == 4) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
+         group <= 8;
+}
+
+hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  if (g.elem == 2) {
+    if (a.head_dim == 64) return launch_attn_hd<_Float16, 64>(g, a, s);
+    if (a.head_dim == 128) return launch_attn_hd<_Float16, 128>(g, a, s);
+  } else {
+    if (a.head_dim == 64) return launch_attn_hd<float, 64>(g, a, s);
+    if (a.head_dim == 128) return launch_attn_hd<float, 128>(g, a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ltkv

@@ -1,0 +1,436 @@
+"""Parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bar: bit-exact for append (write), copy-on-write/block copy, gather and block
+tables; attention within max abs 1e-3 (f32 KV) / 2e-2 (f16 KV) and relative
+L2 1e-3 of the oracle's restatement of model.rs:431-475.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import BLOCK, attention_close, fill_sequences, tables_and_lens
+
+pytestmark = pytest.mark.gpu
+
+
+def _caches(n_layers, kv_dim, n_tokens, dtype, order=None):
+    from langtrain_studio_amd import KvCache
+    from oracle import OracleKv
+
+    g = KvCache(n_layers, kv_dim, n_tokens, dtype=dtype, device=0)
+    o = OracleKv(n_layers, kv_dim, n_tokens, dtype=dtype)
+    if order is not None:
+        g.init_free_order(order)
+        o.init_free_order(order)
+    return g, o
+
+
+def _bits(a):
+    return a.view(np.uint16) if a.dtype == np.uint16 else a.view(np.uint32)
+
+
+def _assert_pools_equal(g, o, layers):
+    for layer in layers:
+        gk, gv = g.read_pool(layer)
+        ok, ov = o.pool(layer)
+        np.testing.assert_array_equal(_bits(gk), _bits(ok), err_msg=f"K pool, layer {layer}")
+        np.testing.assert_array_equal(_bits(gv), _bits(ov), err_msg=f"V pool, layer {layer}")
+
+
+# ---------------------------------------------------------------------------- write (kernel 1)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_write_bitexact_special_values(gpu, dtype):
+    rng = np.random.default_rng(1)
+    kv_dim, n_blocks = 256, 64
+    order = rng.permutation(n_blocks)
+    g, o = _caches(2, kv_dim, n_blocks * BLOCK, dtype, order)
+    fill_sequences([("gpu", g), ("oracle", o)], {0: 37, 5: 16, 9: 100, 3: 1}, rng, kv_dim,
+                   layers=(0, 1), special=True)
+    g.synchronize()
+    _assert_pools_equal(g, o, (0, 1))
+
+
+def test_write_skips_negative_and_out_of_range_slots(gpu):
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    g = KvCache(1, 64, 4 * BLOCK, device=0)
+    sm = torch.tensor([-1, 3, 4 * BLOCK, 5, -7], dtype=torch.int32, device=gpu)
+    k = torch.full((5, 64), 2.0, device=gpu)
+    g.write_batch(0, sm, k, k)
+    pk, pv = g.read_pool(0)
+    flat = pk.reshape(-1, 64)
+    written = {3, 5}
+    for cell in range(4 * BLOCK):
+        want = 0x4000 if cell in written else 0  # 2.0 in f16 is 0x4000
+        assert (flat[cell] == want).all(), cell
+
+
+def test_write_row_strided_source(gpu):
+    import torch
+
+    from langtrain_studio_amd import KvCache
+    from oracle import OracleKv
+
+    rng = np.random.default_rng(2)
+    g = KvCache(1, 128, 8 * BLOCK, device=0)
+    o = OracleKv(1, 128, 8 * BLOCK)
+    sm = g.append_batch([0] * 20, np.arange(20))
+    o.append_batch([0] * 20, np.arange(20))
+    src = rng.standard_normal((20, 160), dtype=np.float32)  # row stride 160 > kv_dim
+    g.write_batch(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(src).to(gpu), torch.from_numpy(src).to(gpu))
+    o.write_batch(0, sm, src[:, :128], src[:, :128])
+    _assert_pools_equal(g, o, (0,))
+
+
+# ---------------------------------------------------------------------------- kv.rs tests, on the GPU cache
+def test_share_then_diverge_copies_on_write(gpu):
+    """kv.rs:202-217 with the K/V data living in HBM (kv_dim 8: the ABI needs a multiple of 8)."""
+    from langtrain_studio_amd import KvCache
+    from oracle import f16_to_f32
+
+    kv = KvCache(1, 8, 256, device=0)
+
+    def fill(seq, n, base):
+        for p in range(kv.len(seq), n):
+            b, s = kv.append(seq, p)
+            x = np.full(kv.kv_dim, base + p, dtype=np.float32)
+            kv.write(0, b, s, x, x)
+
+    fill(0, 20, 0.0)
+    kv.share(0, 1, 20)
+    free_before = kv.free_blocks()
+    b, s = kv.append(1, 20)
+    kv.write(0, b, s, np.full(8, 1000.0, np.float32), np.full(8, 1000.0, np.float32))
+    assert kv.free_blocks() == free_before - 1
+    a = f16_to_f32(kv.rows(0, 0, 20)[0][:, 0])
+    c = f16_to_f32(kv.rows(0, 1, 21)[0][:, 0])
+    np.testing.assert_array_equal(a, c[:20])
+    assert c[20] == 1000.0
+    assert kv.len(0) == 20
+
+
+def test_truncate_frees_blocks(gpu):
+    """kv.rs:219-229 on the GPU cache."""
+    from langtrain_studio_amd import KvCache, NonContiguous
+
+    kv = KvCache(1, 8, 64, device=0)
+    for p in range(40):
+        b, s = kv.append(3, p)
+        x = np.full(8, float(p), np.float32)
+        kv.write(0, b, s, x, x)
+    assert kv.free_blocks() == 1
+    kv.truncate(3, 10)
+    assert kv.free_blocks() == 3
+    kv.truncate(3, 0)
+    assert kv.free_blocks() == 4
+    with pytest.raises(NonContiguous):
+        kv.append(3, 5)
+
+
+# ---------------------------------------------------------------------------- copy-on-write / copy (kernel 2)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_copy_on_write_matches_oracle(gpu, dtype):
+    """Prefix sharing, divergence and truncation, three layers: pools and
+    tables stay bit-identical to the oracle after every step."""
+    import torch
+
+    rng = np.random.default_rng(3)
+    kv_dim, n_blocks, layers = 64, 96, (0, 1, 2)
+    g, o = _caches(3, kv_dim, n_blocks * BLOCK, dtype, rng.permutation(n_blocks))
+    fill_sequences([("gpu", g), ("oracle", o)], {0: 45, 1: 16}, rng, kv_dim, layers=layers)
+    for dst in (2, 3, 4, 5):
+        g.share(0, dst, 45)
+        o.share(0, dst, 45)
+    g.share(1, 6, 16)
+    o.share(1, 6, 16)
+    g.share(0, 7, 30)  # shares a partially used block in the middle of seq 0
+    o.share(0, 7, 30)
+    for step in range(6):
+        seqs = [0, 2, 3, 4, 5, 6, 7]
+        pos = [g.len(s) for s in seqs]
+        sm_g = g.append_batch(seqs, pos)
+        sm_o = o.append_batch(seqs, pos)
+        np.testing.assert_array_equal(sm_g, sm_o)
+        for layer in layers:
+            k = rng.standard_normal((len(seqs), kv_dim), dtype=np.float32)
+            v = rng.standard_normal((len(seqs), kv_dim), dtype=np.float32)
+            g.write_batch(layer, torch.from_numpy(sm_g).to(gpu), torch.from_numpy(k).to(gpu),
+                          torch.from_numpy(v).to(gpu))
+            o.write_batch(layer, sm_o, k, v)
+        if step == 2:
+            g.truncate(3, 20)
+            o.truncate(3, 20)
+            g.share(5, 3, 40)
+            o.share(5, 3, 40)
+        assert g.cow_copies() == o.cow_copies()
+        assert g.free_blocks() == o.free_blocks()
+        for s in range(8):
+            np.testing.assert_array_equal(g.block_table(s), o.block_table(s))
+        _assert_pools_equal(g, o, layers)
+    assert g.cow_copies() >= 6
+
+
+def test_copy_blocks_bulk(gpu):
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    rng = np.random.default_rng(4)
+    kv_dim, n_blocks = 1024, 300
+    g = KvCache(2, kv_dim, n_blocks * BLOCK, device=0)
+    seq_lens = {0: n_blocks * BLOCK}
+    fill_sequences([("gpu", g)], seq_lens, rng, kv_dim, layers=(0, 1))
+    before = [g.read_pool(l) for l in (0, 1)]
+    perm = rng.permutation(n_blocks)
+    src, dst = perm[:100], perm[100:200]
+    pairs = torch.from_numpy(np.stack([src, dst], 1).astype(np.int32)).to(gpu)
+    g.copy_blocks(pairs)
+    for l in (0, 1):
+        k, v = g.read_pool(l)
+        wk, wv = before[l][0].copy(), before[l][1].copy()
+        wk[dst] = before[l][0][src]
+        wv[dst] = before[l][1][src]
+        np.testing.assert_array_equal(k, wk)
+        np.testing.assert_array_equal(v, wv)
+
+
+# ---------------------------------------------------------------------------- gather (kernel 3)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gather_ragged_matches_rows(gpu, dtype):
+    import torch
+
+    rng = np.random.default_rng(5)
+    kv_dim, n_blocks = 512, 256
+    g, o = _caches(1, kv_dim, n_blocks * BLOCK, dtype, rng.permutation(n_blocks))
+    lens = {0: 1, 1: 15, 2: 16, 3: 17, 4: 333, 5: 1000, 6: 64}
+    fill_sequences([("gpu", g), ("oracle", o)], lens, rng, kv_dim)
+    seqs = [0, 1, 2, 3, 4, 5, 6, 9]  # seq 9 is unknown: length 0
+    want_lens = [lens.get(s, 0) for s in seqs]
+    tables, lens_arr = tables_and_lens(g, seqs, want_lens, stride=70)
+    offs = np.concatenate([[0], np.cumsum(want_lens)[:-1]]).astype(np.int64)
+    total = int(sum(want_lens))
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    k_out = torch.full((total + 3, kv_dim), -1.0, dtype=tdt, device=gpu)
+    v_out = torch.full((total + 3, kv_dim), -1.0, dtype=tdt, device=gpu)
+    g.gather(0, torch.from_numpy(tables).to(gpu), torch.from_numpy(lens_arr).to(gpu),
+             torch.from_numpy(offs).to(gpu), k_out, v_out)
+    kh = k_out.cpu().numpy()
+    vh = v_out.cpu().numpy()
+    npdt = np.uint16 if dtype == "f16" else np.uint32
+    for s, n, off in zip(seqs, want_lens, offs):
+        if n == 0:
+            continue
+        wk, wv = o.rows(0, s, n)
+        np.testing.assert_array_equal(kh[off:off + n].view(npdt), _bits(wk))
+        np.testing.assert_array_equal(vh[off:off + n].view(npdt), _bits(wv))
+    # rows past the gathered total are untouched
+    assert (kh[total:] == -1).all() and (vh[total:] == -1).all()
+
+
+def test_rows_host_convenience(gpu):
+    rng = np.random.default_rng(6)
+    g, o = _caches(2, 128, 64 * BLOCK, "f16", rng.permutation(64))
+    fill_sequences([("gpu", g), ("oracle", o)], {4: 77, 8: 3}, rng, 128, layers=(0, 1))
+    for layer in (0, 1):
+        for s, n in ((4, 77), (4, 50), (8, 3)):
+            gk, gv = g.rows(layer, s, n)
+            ok, ov = o.rows(layer, s, n)
+            np.testing.assert_array_equal(gk, ok)
+            np.testing.assert_array_equal(gv, ov)
+
+
+# ---------------------------------------------------------------------------- attention (kernel 4)
+def _attention_case(gpu, dtype, head_dim, group, n_kv_heads, lens, partition, seed):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    kv_dim = n_kv_heads * head_dim
+    n_heads = group * n_kv_heads
+    blocks = sum(-(-n // BLOCK) for n in lens) + 8
+    g, o = _caches(1, kv_dim, blocks * BLOCK, dtype, rng.permutation(blocks))
+    if partition:
+        g.set_attention_partition(partition)
+    fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, kv_dim)
+    seqs = list(range(len(lens)))
+    tables, lens_arr = tables_and_lens(g, seqs, lens)
+    q = rng.standard_normal((len(lens), n_heads * head_dim), dtype=np.float32)
+    out = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(lens_arr).to(gpu), n_heads, head_dim).cpu().numpy()
+    want = o.attention_tables(0, tables, lens_arr, q, n_heads, head_dim, threads=8)
+    return out, want
+
+
+@pytest.mark.parametrize("dtype,head_dim", [("f16", 128), ("f16", 64), ("f32", 64), ("f32", 128)])
+@pytest.mark.parametrize("group", [1, 4, 7, 8])
+def test_attention_shapes(gpu, dtype, head_dim, group):
+    lens = [1, 2, 15, 16, 17, 63, 300, 1031]
+    out, want = _attention_case(gpu, dtype, head_dim, group, 2, lens, 0, seed=group * 10 + head_dim)
+    attention_close(out, want, dtype)
+
+
+@pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
+def test_attention_partitions(gpu, partition):
+    lens = [5, 64, 65, 257, 700, 2049]
+    out, want = _attention_case(gpu, "f16", 128, 4, 8, lens, partition, seed=partition)
+    attention_close(out, want, "f16")
+
+
+def test_attention_config_tinyllama_f32(gpu):
+    """TinyLlama-shaped layer, f32 KV: 32 q heads, 4 kv heads, head_dim 64;
+    4 sequences with contexts U[128,512] over a permuted 1024-block pool;
+    append one token per sequence, then one decode step (scale 1/8)."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+    from oracle import OracleKv
+
+    rng = np.random.default_rng(11)
+    n_heads, n_kv, hd = 32, 4, 64
+    kv_dim = n_kv * hd
+    g = KvCache(1, kv_dim, 1024 * BLOCK, dtype="f32", device=0)
+    o = OracleKv(1, kv_dim, 1024 * BLOCK, dtype="f32")
+    order = rng.permutation(1024)
+    g.init_free_order(order)
+    o.init_free_order(order)
+    ctx = rng.integers(128, 513, 4)
+    fill_sequences([("gpu", g), ("oracle", o)], {s: int(n) for s, n in enumerate(ctx)}, rng, kv_dim)
+    seqs = np.arange(4, dtype=np.uint32)
+    pos = ctx.astype(np.uint64)
+    sm = g.append_batch(seqs, pos)
+    np.testing.assert_array_equal(sm, o.append_batch(seqs, pos))
+    k = rng.standard_normal((4, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((4, kv_dim), dtype=np.float32)
+    g.write_batch(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu))
+    o.write_batch(0, sm, k, v)
+    q = rng.standard_normal((4, n_heads * hd), dtype=np.float32)
+    tables, lens = tables_and_lens(g, seqs, pos + 1)
+    out = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(lens).to(gpu), n_heads, hd, scale=0.125).cpu().numpy()
+    want = o.attention(0, seqs, pos, q, n_heads, hd, scale=0.125, threads=8)
+    attention_close(out, want, "f32")
+    _assert_pools_equal(g, o, (0,))
+
+
+def test_attention_single_position_returns_v_row(gpu):
+    """len == 1: the softmax weight is exactly 1, so the output is the V row."""
+    import torch
+
+    from oracle import f16_to_f32
+
+    rng = np.random.default_rng(12)
+    g, o = _caches(1, 256, 8 * BLOCK, "f16")
+    _, rows = fill_sequences([("gpu", g), ("oracle", o)], {0: 1, 1: 1}, rng, 256)
+    tables, lens = tables_and_lens(g, [0, 1], [1, 1])
+    q = rng.standard_normal((2, 8 * 128), dtype=np.float32)
+    out = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(lens).to(gpu), 8, 128).cpu().numpy()
+    vrow = f16_to_f32(o.rows(0, 0, 1)[1][0]), f16_to_f32(o.rows(0, 1, 1)[1][0])
+    for i in range(2):
+        want = np.concatenate([np.tile(vrow[i][h * 128:(h + 1) * 128], 4) for h in range(2)])
+        np.testing.assert_array_equal(out[i], want)
+
+
+def test_attention_equal_keys_average_values(gpu):
+    """All K rows equal: uniform weights, so the output is the mean of V."""
+    import torch
+
+    from oracle import f16_to_f32
+
+    rng = np.random.default_rng(13)
+    kv_dim, n = 128, 200
+    g, o = _caches(1, kv_dim, 16 * BLOCK, "f16")
+    sm = g.append_batch([0] * n, np.arange(n))
+    o.append_batch([0] * n, np.arange(n))
+    k = np.tile(rng.standard_normal((1, kv_dim), dtype=np.float32), (n, 1))
+    v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    g.write_batch(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu))
+    tables, lens = tables_and_lens(g, [0], [n])
+    q = rng.standard_normal((1, 4 * 128), dtype=np.float32)
+    out = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(lens).to(gpu), 4, 128).cpu().numpy()
+    vm = f16_to_f32(g.rows(0, 0, n)[1]).astype(np.float64).mean(0)
+    np.testing.assert_allclose(out[0], np.tile(vm, 4), atol=2e-5, rtol=0)
+
+
+def test_attention_physical_placement_invariance(gpu):
+    """The same logical contents under two different block placements give
+    bit-identical outputs (the kernel depends only on the block table)."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    rng = np.random.default_rng(14)
+    lens = [700, 33, 1500, 16]
+    kv_dim, blocks = 1024, 256
+    outs = []
+    q = rng.standard_normal((4, 32 * 128), dtype=np.float32)
+    data_seed = 99
+    for order_seed in (1, 2):
+        g = KvCache(1, kv_dim, blocks * BLOCK, device=0)
+        g.init_free_order(np.random.default_rng(order_seed).permutation(blocks))
+        fill_sequences([("gpu", g)], dict(enumerate(lens)), np.random.default_rng(data_seed), kv_dim)
+        tables, la = tables_and_lens(g, range(4), lens)
+        outs.append(g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                                       torch.from_numpy(la).to(gpu), 32, 128).cpu().numpy())
+        assert not np.array_equal(tables[:, 0], np.arange(4))  # placements really differ
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_attention_batch_independence(gpu):
+    """A query's output is bit-identical alone and inside a batch (the
+    reference's batching property, engine/README.md:102)."""
+    import torch
+
+    rng = np.random.default_rng(15)
+    lens = [2000, 9, 513, 4096, 77]
+    g, _ = _caches(1, 1024, 1000 * BLOCK, "f16", rng.permutation(1000))
+    fill_sequences([("gpu", g)], dict(enumerate(lens)), rng, 1024)
+    q = rng.standard_normal((5, 32 * 128), dtype=np.float32)
+    tables, la = tables_and_lens(g, range(5), lens)
+    dq, dt, dl = (torch.from_numpy(x).to(gpu) for x in (q, tables, la))
+    full = g.decode_attention(0, dq, dt, dl, 32, 128).cpu().numpy()
+    for i in range(5):
+        one = g.decode_attention(0, dq[i:i + 1].contiguous(), dt[i:i + 1, :-(-lens[i] // BLOCK)].contiguous(),
+                                 dl[i:i + 1].contiguous(), 32, 128).cpu().numpy()
+        np.testing.assert_array_equal(one[0], full[i])
+
+
+def test_attention_stale_nonfinite_slots_are_ignored(gpu):
+    """Cells past a sequence's length may hold stale non-finite data; they
+    must not leak into the output."""
+    import torch
+
+    rng = np.random.default_rng(16)
+    kv_dim = 128
+    g, o = _caches(1, kv_dim, 8 * BLOCK, "f16")
+    sm = g.append_batch([0] * 16, np.arange(16))
+    o.append_batch([0] * 16, np.arange(16))
+    k = rng.standard_normal((16, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((16, kv_dim), dtype=np.float32)
+    k[9:] = np.inf
+    v[9:] = np.nan
+    g.write_batch(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu))
+    o.write_batch(0, sm, k, v)
+    g.truncate(0, 9)
+    o.truncate(0, 9)
+    tables, lens = tables_and_lens(g, [0], [9])
+    q = rng.standard_normal((1, 128), dtype=np.float32)
+    out = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(lens).to(gpu), 1, 128).cpu().numpy()
+    want = o.attention_tables(0, tables, lens, q, 1, 128)
+    attention_close(out, want, "f16")
+
+
+def test_attention_zero_length_gives_zeros(gpu):
+    import torch
+
+    g, _ = _caches(1, 128, 8 * BLOCK, "f16")
+    q = torch.ones((2, 256), device=gpu)
+    tables = torch.full((2, 4), -1, dtype=torch.int32, device=gpu)
+    lens = torch.zeros(2, dtype=torch.int32, device=gpu)
+    out = g.decode_attention(0, q, tables, lens, 2, 128)
+    assert (out.cpu().numpy() == 0).all()
