@@ -206,15 +206,17 @@ __device__ __forceinline__ float group_sum(float x) {
 template <typename T>
 struct Tile;
 
+// The whole 16-byte vector is bit-cast at once: this clang drops a
+// __builtin_bit_cast whose operand is a single ext-vector element (u.y).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
 template <>
 struct Tile<_Float16> {
   static constexpr int E = 8;  // elements per 16-byte load
   __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[8]) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 a = __builtin_bit_cast(h2, u.x), b = __builtin_bit_cast(h2, u.y);
-    const h2 c = __builtin_bit_cast(h2, u.z), d = __builtin_bit_cast(h2, u.w);
-    f[0] = (float)a.x; f[1] = (float)a.y; f[2] = (float)b.x; f[3] = (float)b.y;
-    f[4] = (float)c.x; f[5] = (float)c.y; f[6] = (float)d.x; f[7] = (float)d.y;
+    const f16x8 h = __builtin_bit_cast(f16x8, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
   }
 };
 
@@ -222,10 +224,9 @@ template <>
 struct Tile<float> {
   static constexpr int E = 4;
   __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[4]) {
-    f[0] = __builtin_bit_cast(float, u.x);
-    f[1] = __builtin_bit_cast(float, u.y);
-    f[2] = __builtin_bit_cast(float, u.z);
-    f[3] = __builtin_bit_cast(float, u.w);
+    const f32x4 v = __builtin_bit_cast(f32x4, u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = v[i];
   }
 };
 
