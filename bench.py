@@ -44,6 +44,9 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0 = host share, max 16)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--workload", default="decode",
+                   choices=["decode", "copy", "append-sweep", "long-context"],
+                   help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
 
@@ -166,6 +169,112 @@ def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
     return float(np.mean(times) * 1e6), s
 
 
+def _time_op(fn, reps: int, warmup: int = 2) -> float:
+    """Mean µs of fn() over reps, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / reps
+
+
+def bench_copy(args):
+    """A plain device-to-device copy of known size: the calibration for the
+    FETCH_SIZE / WRITE_SIZE counters (bytes the counters report per byte moved)."""
+    import torch
+
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+    src.fill_(1.0)
+    dst = torch.empty_like(src)
+    us = _time_op(lambda: dst.copy_(src), reps=max(args.steps, 1))
+    print(json.dumps({"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
+                      "GBps": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
+def bench_append_sweep(args):
+    """Bulk slot-mapped append at the Llama-3-8B layer shape (kv_dim 1024, f16):
+    512 sequences x 512 tokens claimed through the allocator over a permuted
+    pool; the first n slots of that mapping are written for each size."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    kvd, n_seqs, per_seq = 1024, 512, 512
+    total = n_seqs * per_seq
+    rng = np.random.default_rng(args.seed)
+    n_blocks = total // BLOCK + 64
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(n_blocks))
+    sm = kv.append_batch(np.repeat(np.arange(n_seqs, dtype=np.uint32), per_seq),
+                         np.tile(np.arange(per_seq, dtype=np.uint64), n_seqs))
+    d_sm = torch.from_numpy(sm).cuda()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    k = torch.randn((total, kvd), generator=gen, device="cuda")
+    v = torch.randn((total, kvd), generator=gen, device="cuda")
+    rows = []
+    for n in (64, 256, 1024, 4096, 16384, 65536, 262144):
+        us = _time_op(lambda: kv.write_batch(0, d_sm[:n], k[:n], v[:n]), reps=20)
+        nbytes = n * kvd * (4 + 4 + 2 + 2) + n * 4
+        rows.append({"tokens": n, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)})
+    print(json.dumps({"workload": "append-sweep", "shape": "kv_dim 1024 f32->f16", "rows": rows}), flush=True)
+
+
+def bench_long_context(args):
+    """Long-context stress at the Llama-3-8B layer shape: 32 sequences x 32768
+    tokens over a fully permuted pool (worst-case scatter). Times the gather
+    of every sequence to contiguous K/V and one decode-attention pass."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    B, ctx, n_heads, n_kv, hd = 32, 32768, 32, 8, 128
+    kvd = n_kv * hd
+    rng = np.random.default_rng(args.seed)
+    n_blocks = B * ctx // BLOCK + 64
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    if args.partition:
+        kv.set_attention_partition(args.partition)
+    kv.init_free_order(rng.permutation(n_blocks))
+    sm = kv.append_batch(np.repeat(np.arange(B, dtype=np.uint32), ctx),
+                         np.tile(np.arange(ctx, dtype=np.uint64), B))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    chunk = 1 << 16
+    for i in range(0, sm.size, chunk):
+        kk = torch.randn((chunk, kvd), generator=gen, device="cuda")
+        vv = torch.randn((chunk, kvd), generator=gen, device="cuda")
+        kv.write_batch(0, torch.from_numpy(sm[i:i + chunk]).cuda(), kk, vv)
+    del kk, vv
+    tables = torch.from_numpy(kv.block_tables(np.arange(B, dtype=np.uint32), ctx // BLOCK)).cuda()
+    lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    offs = torch.arange(B, dtype=torch.int64, device="cuda") * ctx
+    k_out = torch.empty((B * ctx, kvd), dtype=torch.float16, device="cuda")
+    v_out = torch.empty_like(k_out)
+    g_us = _time_op(lambda: kv.gather(0, tables, lens, offs, k_out, v_out), reps=10)
+    g_bytes = 2 * 2 * B * ctx * kvd * 2 + tables.numel() * 4
+    q = torch.randn((B, n_heads * hd), generator=gen, device="cuda")
+    out = torch.empty_like(q)
+    a_us = _time_op(lambda: kv.decode_attention(0, q, tables, lens, n_heads, hd, out=out), reps=10)
+    a_bytes = B * ctx * 2 * kvd * 2 + 2 * q.numel() * 4 + tables.numel() * 4 + B * 4
+    print(json.dumps({
+        "workload": "long-context 32x32768 llama3-8b f16, random tables",
+        "gather_us": round(g_us, 1), "gather_GBps": round(g_bytes / (g_us * 1e-6) / 1e9, 1),
+        "gather_frac": round(g_bytes / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "gather_bytes": g_bytes,
+        "attention_us": round(a_us, 1), "attention_GBps": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
+        "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "attention_bytes": a_bytes,
+    }), flush=True)
+
+
 def main():
     args = _args()
     if args.gpus != 1:
@@ -177,6 +286,10 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
+    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context}
+    if args.workload in extra:
+        extra[args.workload](args)
+        return
     steps, warmup = args.steps, args.warmup
     w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition)
 
