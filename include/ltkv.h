@@ -167,7 +167,7 @@ LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t
                           size_t table_stride, const int32_t *d_lens, float *d_out);
 
 /* Tokens per context partition of the decode attention split (multiple of
- * 64; 0 = the default, 256). Results depend on it only through summation
+ * 64; 0 = the default, 1024). Results depend on it only through summation
  * order; they never depend on the other queries of a batch. Tuning knob. */
 LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
 

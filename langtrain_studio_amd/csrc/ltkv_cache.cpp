@@ -69,8 +69,8 @@ struct DeviceGuard {
   }
 };
 
-// Context tokens per decode-attention work-group (16 blocks, 4 per wave).
-constexpr size_t kDefaultPartition = 256;
+// Context tokens per decode-attention work-group (64 blocks, 16 per wave).
+constexpr size_t kDefaultPartition = 1024;
 
 }  // namespace
 
@@ -95,8 +95,8 @@ struct ltkv_cache {
   bool pairs_in_flight = false;
 
   // Attention workspace (partition partials), grown on demand.
-  float *ws = nullptr;
-  size_t ws_floats = 0;
+  uint8_t *ws = nullptr;
+  size_t ws_bytes = 0;
   size_t attn_part_tokens = 0;  // 0 = automatic
 
   int device_count_cu = 256;
@@ -488,17 +488,18 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
 
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  const int64_t need = ltkv::attention_workspace_floats((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
-  if ((size_t)need > c->ws_floats) {
+  const ltkv::AttnWorkspace ws =
+      ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
+  if ((size_t)ws.bytes > c->ws_bytes) {
     if (c->ws) {
       // The old workspace may still be read by enqueued work.
       HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
       HIP_TRY(hipFree(c->ws), "hipFree(workspace)");
       c->ws = nullptr;
-      c->ws_floats = 0;
+      c->ws_bytes = 0;
     }
-    HIP_TRY(hipMalloc((void **)&c->ws, (size_t)need * sizeof(float)), "hipMalloc(workspace)");
-    c->ws_floats = (size_t)need;
+    HIP_TRY(hipMalloc((void **)&c->ws, (size_t)ws.bytes), "hipMalloc(workspace)");
+    c->ws_bytes = (size_t)ws.bytes;
   }
   ltkv::PoolGeom g = c->geom;
   g.head_stride = (int64_t)head_dim;  // token-major: heads are adjacent in a row
@@ -510,8 +511,8 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   a.table_stride = (int64_t)table_stride;
   a.lens = d_lens;
   a.out = d_out;
-  a.part_o = c->ws;
-  a.part_ml = c->ws ? c->ws + n * n_heads * max_parts * head_dim : nullptr;
+  a.part_o = ws.bytes ? (float *)(c->ws + ws.part_o_off) : nullptr;
+  a.part_ml = ws.bytes ? (float *)(c->ws + ws.part_ml_off) : nullptr;
   a.n = (int64_t)n;
   a.n_heads = (int)n_heads;
   a.n_kv_heads = (int)n_kv_heads;

@@ -47,8 +47,12 @@ struct AttnArgs {
   int part_tokens, max_parts;
 };
 
-// Workspace floats needed by launch_decode_attention for these arguments.
-int64_t attention_workspace_floats(int64_t n, int n_heads, int head_dim, int max_parts);
+// Workspace of launch_decode_attention: partition partials (bytes == 0 when
+// one partition covers every query).
+struct AttnWorkspace {
+  int64_t part_o_off, part_ml_off, bytes;
+};
+AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts);
 bool attention_supported(int elem, int head_dim, int group);
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
 

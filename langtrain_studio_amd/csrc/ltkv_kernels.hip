@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "ltkv_kernels.h"
 
@@ -260,8 +261,9 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > table_stride * 16) len = table_stride * 16;
+  const int np = len > 0 ? (int)((len + part_tokens - 1) / part_tokens) : 1;
+  if (part >= np) return;  // uniform over the work-group
   const int64_t tok0 = (int64_t)part * part_tokens;
-  if (part > 0 && tok0 >= len) return;  // uniform over the work-group
   const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
@@ -432,7 +434,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
       o += sm_acc[w][h][d] * a;
     }
     const int64_t qh = qi * n_heads + (int64_t)kvh * G + h;
-    if (max_parts == 1) {
+    if (np == 1) {
       out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
     } else {
       const int64_t pi = qh * max_parts + part;
@@ -458,8 +460,8 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
-  int np = (int)((len + part_tokens - 1) / part_tokens);
-  if (np < 1) np = 1;
+  const int np = (int)((len + part_tokens - 1) / part_tokens);
+  if (np <= 1) return;  // a single partition wrote its output directly
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
   float mx = -INFINITY;
@@ -474,13 +476,10 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
 }
 
-template <typename T, int HD, int G>
-hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
-  attn_kernel<T, HD, G><<<grid, 256, 0, s>>>(
-      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
-      a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
-      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+// Launch check of the attention kernel, then the partition merge when some
+// query may span several partitions.
+template <int HD>
+hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.max_parts == 1) return e;
   const unsigned mgrid = (unsigned)(a.n * a.n_heads);
@@ -489,17 +488,439 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ----------------------------------------------------------------------------
+// Kernel 4, 16-lane form (f16 head_dim 128 and f32 head_dim 64: one 16-byte
+// load per lane covers a row across 16 lanes, a DPP row).
+//
+// Differences from attn_kernel, all aimed at VALU count per KV byte:
+//  * the rows x heads partial dots of a tile are reduce-scattered over the 16
+//    lanes of the row, so each lane ends with distinct scores instead of every
+//    lane holding all of them. The head bits of the score index are split
+//    with plain v[r] += dpp(v[r + n/2]) exchanges, with no per-lane selects,
+//    because each lane's q registers are permuted once so that every DPP
+//    partner map (mirror, half-mirror) flips exactly the head bit being
+//    split; the two row bits take select steps, so K and V rows keep their
+//    natural, coalesced lane order;
+//  * the online softmax is distributed accordingly: each lane owns one head's
+//    (max, sum) for its row group and evaluates one exp2 per score it holds;
+//    the V pass fetches the weights it needs with row_newbcast;
+//  * the accumulators are rescaled only when some running max grew (a
+//    wave-uniform branch), which after the first tiles is rare;
+//  * loads take a scalar per-tile base plus a 32-bit per-lane offset fixed
+//    for the whole loop, and the tile pipeline is peeled (no tile is fetched
+//    twice).
+// ----------------------------------------------------------------------------
+// The four DPP partner maps of the scatter: lane ^ 15, ^ 7, ^ 2, ^ 1.
+template <int T>
+__device__ __forceinline__ float partner16(float x) {
+  if constexpr (T == 0) return dpp<0x140>(x);       // row_mirror: lane ^ 15
+  else if constexpr (T == 1) return dpp<0x141>(x);  // row_half_mirror: lane ^ 7
+  else if constexpr (T == 2) return dpp<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  else return dpp<0xB1>(x);                         // quad_perm [1,0,3,2]: lane ^ 1
+}
+
+template <int K>
+__device__ __forceinline__ float bcast16(float x) {
+  // row_newbcast:K, lane K of each 16-lane row (every lane is written).
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + K, 0xf, 0xf, false));
+}
+
+// The score layout of a tile with N = padded_group * 4 partial dots per lane,
+// index h*4 + j (head h, row slot j). The scatter splits index bits from the
+// top; head bits are split select-free (lane i keeps index r ^ g(i) in
+// register r, g linear over GF(2) with g(lane ^ mask_t) = g(lane) ^ split_t,
+// realised by permuting the lane's q registers), the two row bits with
+// selects, so K rows stay in natural (coalesced) lane order.
+template <int N>
+struct Scatter16 {
+  static constexpr int NPL = N > 16 ? N / 16 : 1;            // scores per lane after the scatter
+  static constexpr int T = N >= 16 ? 4 : (N == 8 ? 3 : 2);   // scatter steps (then all-reduce)
+  static constexpr int half(int t) { return (N >> t) / 2; }  // index value of the bit split at t
+  static constexpr bool free_step(int t) { return t < T && half(t) >= 4; }  // head bit
+  static constexpr int gm(int t) { return free_step(t) ? half(t) : 0; }
+  // g on the lane-bit basis e0..e3 (the masks 1, 2, 7, 15 span GF(2)^4).
+  static constexpr int col(int b) {
+    return b == 0 ? gm(3) : b == 1 ? gm(2) : b == 2 ? (gm(1) ^ gm(3) ^ gm(2)) : (gm(0) ^ gm(1));
+  }
+  static constexpr int g(int lane) {
+    int r = 0;
+    for (int b = 0; b < 4; ++b)
+      if ((lane >> b) & 1) r ^= col(b);
+    return r;
+  }
+  static constexpr int lane_bit(int t) { return 8 >> t; }  // lane bit told apart by partner map t
+  // Score index held by lane `lane` in register r (r < NPL) after the scatter.
+  static constexpr int held(int lane, int r) {
+    int idx = g(lane) ^ r;
+    for (int t = 0; t < T; ++t)
+      if (!free_step(t) && (lane & lane_bit(t))) idx += half(t);
+    return idx;
+  }
+  // A lane of the row holding score index idx (in register idx & (NPL-1)).
+  static constexpr int src(int idx) {
+    for (int i = 0; i < 16; ++i)
+      if (held(i, idx & (NPL - 1)) == idx) return i;
+    return 0;
+  }
+};
+
+// In-place reduce-scatter over the 16 lanes of a row; afterwards v[r],
+// r < NPL, holds the row-wide sum of index held(lane, r).
+template <int N, int n, int t>
+__device__ __forceinline__ void reduce_scatter16(float (&v)[N], int lane) {
+  using S = Scatter16<N>;
+  if constexpr (t < 4) {
+    if constexpr (S::free_step(t)) {
+#pragma unroll
+      for (int r = 0; r < n / 2; ++r) v[r] += partner16<t>(v[r + n / 2]);
+      reduce_scatter16<N, n / 2, t + 1>(v, lane);
+    } else if constexpr (t < S::T) {
+      const bool up = (lane & S::lane_bit(t)) != 0;
+#pragma unroll
+      for (int r = 0; r < n / 2; ++r) {
+        const float send = up ? v[r] : v[r + n / 2];
+        const float keep = up ? v[r + n / 2] : v[r];
+        v[r] = keep + partner16<t>(send);
+      }
+      reduce_scatter16<N, n / 2, t + 1>(v, lane);
+    } else {
+      v[0] += partner16<t>(v[0]);
+      reduce_scatter16<N, n, t + 1>(v, lane);
+    }
+  }
+}
+
+// Max or sum over aligned groups of LANES lanes; steps below SKIP (lanes
+// holding replicas of one value) are left out of a sum.
+template <int LANES, int SKIP, bool MAX>
+__device__ __forceinline__ float head_reduce(float x) {
+  auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : a + b; };
+  if constexpr (LANES > 1 && SKIP <= 1) x = op(x, dpp<0xB1>(x));
+  if constexpr (LANES > 2 && SKIP <= 2) x = op(x, dpp<0x4E>(x));
+  if constexpr (LANES > 4 && SKIP <= 4) x = op(x, dpp<0x141>(x));
+  if constexpr (LANES > 8 && SKIP <= 8) x = op(x, dpp<0x140>(x));
+  return x;
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <typename T, int HD, int G>
+__global__ void __launch_bounds__(256)
+attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
+              const int32_t *__restrict__ tables, int64_t table_stride,
+              const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
+              float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
+              int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
+              int max_parts) {
+  constexpr int E = Tile<T>::E;
+  static_assert(HD / E == 16, "16 lanes per row");
+  constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
+  constexpr int GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;  // group padded to a power of two
+  constexpr int N = GP * LOADS;                                 // partial dots per lane per tile
+  using S = Scatter16<N>;
+  constexpr int NPL = S::NPL;                                   // scores per lane after the scatter
+  constexpr int R = N < 16 ? 16 / N : 1;                        // lanes holding the same score
+  constexpr int LPH = 16 / GP;                                  // lanes per head
+
+  const int kvh = (int)(blockIdx.x % n_kv_heads);
+  const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
+  const int64_t qi = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, rg = lane >> 4;
+  const int n_heads = n_kv_heads * G;
+
+  int64_t len = lens[qi];
+  if (len < 0) len = 0;
+  if (len > table_stride * 16) len = table_stride * 16;
+  const int np = len > 0 ? (int)((len + part_tokens - 1) / part_tokens) : 1;
+  if (part >= np) return;  // uniform over the work-group
+  const int64_t tok0 = (int64_t)part * part_tokens;
+  const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
+  const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
+
+  // Lane permutation of the head bits: register r of the partial dots holds
+  // head (r / 4) ^ (gl / 4), row slot r % 4, so q slot u holds head u ^ (gl / 4).
+  // Heads past G are zero queries (padding).
+  int gl = 0;
+#pragma unroll
+  for (int bit = 0; bit < 4; ++bit)
+    if ((c >> bit) & 1) gl ^= S::col(bit);
+
+  float qv[GP][E];
+  {
+    const float *qp = q + qi * (int64_t)n_heads * HD + (int64_t)kvh * G * HD + c * E;
+#pragma unroll
+    for (int u = 0; u < GP; ++u) {
+      const int h = u ^ (gl >> 2);
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        if (h < G) t = *reinterpret_cast<const f32x4 *>(qp + h * HD + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[u][e + i] = t[i] * qscale;
+      }
+    }
+  }
+
+  // Per-lane byte offsets inside a head tile, fixed for the whole loop.
+  const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
+  const uint32_t col_off = (uint32_t)(c * 16);
+  uint32_t roff[LOADS];
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) roff[j] = (uint32_t)(rg + RPL * j) * row_bytes + col_off;
+  int my_row[NPL];  // tile rows of this lane's scores after the scatter
+  static_for<0, NPL>([&](auto rc) {
+    constexpr int r = decltype(rc)::value;
+    int row = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (c == i) row = rg + RPL * (S::held(i, r) & 3);
+    my_row[r] = row;
+  });
+  const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh * head_stride);
+  const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh * head_stride);
+  const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
+
+  float m_own = -INFINITY, l_own = 0.f;  // softmax state of this lane's head, row group rg
+  float acc[G][E];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+
+  const int32_t *tab = tables + qi * table_stride;
+
+  // Rows of a tile past the context read row 0 of the tile instead (always
+  // inside the context, so finite); their weights are exactly 0.
+  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
+    int32_t blk = tab[b];
+    if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
+    const char *tk = kbase + (int64_t)blk * block_bytes;
+    const char *tv = vbase + (int64_t)blk * block_bytes;
+    const int valid = (int)(tok1 - (int64_t)b * 16);
+    if (valid >= 16) {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tk + roff[j]));
+        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tv + roff[j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t o = rg + RPL * j < valid ? roff[j] : col_off;
+        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tk + o));
+        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tv + o));
+      }
+    }
+  };
+
+  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
+    const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
+    float v[N];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      float kf[E];
+      Tile<T>::unpack(kr[j], kf);
+#pragma unroll
+      for (int u = 0; u < GP; ++u) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) a = __builtin_fmaf(qv[u][e], kf[e], a);
+        v[u * LOADS + j] = a;
+      }
+    }
+    reduce_scatter16<N, N, 0>(v, lane);
+    if (valid < 16) {
+#pragma unroll
+      for (int k = 0; k < NPL; ++k)
+        if (my_row[k] >= valid) v[k] = -INFINITY;
+    }
+    // Online softmax of this lane's head over the tile's rows of this row group.
+    float bm = v[0];
+#pragma unroll
+    for (int k = 1; k < NPL; ++k) bm = __builtin_fmaxf(bm, v[k]);
+    bm = head_reduce<LPH, 1, true>(bm);
+    const float mn = __builtin_fmaxf(m_own, bm);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m_own - mref);
+    float p[NPL];
+    float ps = 0.f;
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) {
+      p[k] = __builtin_amdgcn_exp2f(v[k] - mref);
+      ps += p[k];
+    }
+    ps = head_reduce<LPH, R, false>(ps);
+    l_own = l_own * alpha + ps;
+    const bool grew = mn > m_own;
+    m_own = mn;
+    if (__builtin_amdgcn_ballot_w64(grew)) {  // wave-uniform: some head's max grew
+      static_for<0, G>([&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        const float a = bcast16<S::src(h * LOADS)>(alpha);
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] *= a;
+      });
+    }
+    static_for<0, LOADS>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      float vf[E];
+      Tile<T>::unpack(vr[j], vf);
+      static_for<0, G>([&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        constexpr int idx = h * LOADS + j;  // score index of (head h, row slot j)
+        const float w = bcast16<S::src(idx)>(p[idx & (NPL - 1)]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
+      });
+    });
+  };
+
+  // Peeled software pipeline: tile b+4 loads while tile b is computed; the
+  // last tile of a wave is computed without a prefetch.
+  {
+    u32x4 ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
+    int b = b0 + wave;
+    if (b < b1) {
+      load_tile(b, ka, va);
+      for (;;) {
+        if (b + kAttnWaves >= b1) {
+          compute_tile(b, ka, va);
+          break;
+        }
+        load_tile(b + kAttnWaves, kb, vb);
+        compute_tile(b, ka, va);
+        b += kAttnWaves;
+        if (b + kAttnWaves >= b1) {
+          compute_tile(b, kb, vb);
+          break;
+        }
+        load_tile(b + kAttnWaves, ka, va);
+        compute_tile(b, kb, vb);
+        b += kAttnWaves;
+      }
+    }
+  }
+
+  // Every lane takes the (max, sum) of all heads of its row group, then the
+  // four row groups of the wave are merged (lanes 16 and 32 apart).
+  float m[G], l[G];
+  static_for<0, G>([&](auto hc) {
+    constexpr int h = decltype(hc)::value;
+    m[h] = bcast16<S::src(h * LOADS)>(m_own);
+    l[h] = bcast16<S::src(h * LOADS)>(l_own);
+  });
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mo = __shfl_xor(m[h], off);
+      const float lo = __shfl_xor(l[h], off);
+      const float mn = __builtin_fmaxf(m[h], mo);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float as = __builtin_amdgcn_exp2f(m[h] - mref);
+      const float ao = __builtin_amdgcn_exp2f(mo - mref);
+      l[h] = l[h] * as + lo * ao;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[h][e] = acc[h][e] * as + __shfl_xor(acc[h][e], off) * ao;
+      m[h] = mn;
+    }
+  }
+
+  // Merge the waves through LDS.
+  __shared__ float sm_acc[kAttnWaves][G][HD];
+  __shared__ float sm_m[kAttnWaves][G], sm_l[kAttnWaves][G];
+  if (rg == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) sm_acc[wave][h][c * E + e] = acc[h][e];
+      if (c == 0) {
+        sm_m[wave][h] = m[h];
+        sm_l[wave][h] = l[h];
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t qh0 = qi * n_heads + (int64_t)kvh * G;
+  for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
+    const int h = idx / HD, d = idx - h * HD;
+    float mx = sm_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float a = __builtin_amdgcn_exp2f(sm_m[w][h] - mref);
+      lsum += sm_l[w][h] * a;
+      o += sm_acc[w][h][d] * a;
+    }
+    if (np == 1) {
+      out[(qh0 + h) * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+    } else {
+      const int64_t pi = (qh0 + h) * max_parts + part;
+      part_o[pi * HD + d] = o;
+      if (d == 0) {
+        part_ml[2 * pi] = mx;
+        part_ml[2 * pi + 1] = lsum;
+      }
+    }
+  }
+}
+
+template <typename T, int HD, int G>
+hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
+  attn16_kernel<T, HD, G><<<grid, 256, 0, s>>>(
+      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
+      a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
+      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+  return launch_merge<HD>(a, s);
+}
+
+template <typename T, int HD, int G>
+hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
+  attn_kernel<T, HD, G><<<grid, 256, 0, s>>>(
+      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
+      a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
+      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+  return launch_merge<HD>(a, s);
+}
+
+// 16 lanes per row (f16 x 128, f32 x 64) take attn16_kernel; the other
+// shapes (8 or 32 lanes per row) take attn_kernel + attn_merge_kernel.
+template <typename T, int HD>
+constexpr bool kRow16 = HD / Tile<T>::E == 16;
+
+template <typename T, int HD, int G>
+hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  if constexpr (kRow16<T, HD>)
+    return launch_attn16_t<T, HD, G>(g, a, s);
+  else
+    return launch_attn_t<T, HD, G>(g, a, s);
+}
+
 template <typename T, int HD>
 hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   switch (a.n_heads / a.n_kv_heads) {
-    case 1: return launch_attn_t<T, HD, 1>(g, a, s);
-    case 2: return launch_attn_t<T, HD, 2>(g, a, s);
-    case 3: return launch_attn_t<T, HD, 3>(g, a, s);
-    case 4: return launch_attn_t<T, HD, 4>(g, a, s);
-    case 5: return launch_attn_t<T, HD, 5>(g, a, s);
-    case 6: return launch_attn_t<T, HD, 6>(g, a, s);
-    case 7: return launch_attn_t<T, HD, 7>(g, a, s);
-    case 8: return launch_attn_t<T, HD, 8>(g, a, s);
+    case 1: return launch_attn_g<T, HD, 1>(g, a, s);
+    case 2: return launch_attn_g<T, HD, 2>(g, a, s);
+    case 3: return launch_attn_g<T, HD, 3>(g, a, s);
+    case 4: return launch_attn_g<T, HD, 4>(g, a, s);
+    case 5: return launch_attn_g<T, HD, 5>(g, a, s);
+    case 6: return launch_attn_g<T, HD, 6>(g, a, s);
+    case 7: return launch_attn_g<T, HD, 7>(g, a, s);
+    case 8: return launch_attn_g<T, HD, 8>(g, a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -550,9 +971,14 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
   return hipGetLastError();
 }
 
-int64_t attention_workspace_floats(int64_t n, int n_heads, int head_dim, int max_parts) {
-  if (max_parts <= 1) return 0;
-  return n * n_heads * (int64_t)max_parts * (head_dim + 2);
+AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts) {
+  AttnWorkspace w{};
+  if (max_parts <= 1) return w;
+  const int64_t parts = n * n_heads * (int64_t)max_parts;
+  w.part_o_off = 0;
+  w.part_ml_off = parts * head_dim * 4;
+  w.bytes = w.part_ml_off + parts * 2 * 4;
+  return w;
 }
 
 bool attention_supported(int elem, int head_dim, int group) {

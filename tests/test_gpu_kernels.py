@@ -399,6 +399,25 @@ def test_attention_batch_independence(gpu):
         np.testing.assert_array_equal(one[0], full[i])
 
 
+def test_attention_workspace_reuse_across_shapes(gpu):
+    """Calls of different batch sizes and table widths alternate on one cache
+    (its partition workspace and counters are reused); each must match."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    lens = [3000, 40, 700, 1500, 5, 2222]
+    g, o = _caches(1, 1024, 800 * BLOCK, "f16", rng.permutation(800))
+    fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, 1024)
+    q = rng.standard_normal((6, 32 * 128), dtype=np.float32)
+    for pick in ([0, 1, 2, 3, 4, 5], [1], [3, 0], [4], [5, 2, 1], [0, 1, 2, 3, 4, 5], [2]):
+        tables, la = tables_and_lens(g, pick, [lens[i] for i in pick])
+        qq = q[pick]
+        out = g.decode_attention(0, torch.from_numpy(qq).to(gpu), torch.from_numpy(tables).to(gpu),
+                                 torch.from_numpy(la).to(gpu), 32, 128).cpu().numpy()
+        want = o.attention_tables(0, tables, la, qq, 32, 128, threads=8)
+        attention_close(out, want, "f16")
+
+
 def test_attention_stale_nonfinite_slots_are_ignored(gpu):
     """Cells past a sequence's length may hold stale non-finite data; they
     must not leak into the output."""
