@@ -45,7 +45,8 @@ def _args():
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0 = host share, max 16)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "copy", "append-sweep", "long-context"],
+                   choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
+                            "mixed"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -275,6 +276,217 @@ def bench_long_context(args):
     }), flush=True)
 
 
+def _fill_pool_random(kv, kvd, n_blocks, seed):
+    """Write N(0,1) rows into every cell of a pool (device-only, outside timing),
+    so blocks that arrivals inherit hold finite data."""
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    cells = np.arange(n_blocks * BLOCK, dtype=np.int32)
+    chunk = 1 << 16
+    for i in range(0, cells.size, chunk):
+        sm = torch.from_numpy(cells[i:i + chunk]).cuda()
+        k = torch.randn((sm.numel(), kvd), generator=gen, device="cuda")
+        v = torch.randn((sm.numel(), kvd), generator=gen, device="cuda")
+        kv.write_batch(0, sm, k, v)
+    torch.cuda.synchronize()
+
+
+def bench_tinyllama(args):
+    """TinyLlama-shaped layer, f32 KV (32 q heads, 4 kv heads, head_dim 64): 4
+    sequences with contexts U[128,512] over a permuted 1024-block pool; one
+    append of one token per sequence, then one decode step (scale 1/8)."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    rng = np.random.default_rng(args.seed)
+    n_heads, n_kv, hd, B = 32, 4, 64, 4
+    kvd = n_kv * hd
+    kv = KvCache(1, kvd, 1024 * BLOCK, dtype="f32", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(1024))
+    ctx = rng.integers(128, 513, B)
+    sm = kv.append_batch(np.repeat(np.arange(B, dtype=np.uint32), ctx),
+                         np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx]))
+    k = torch.randn((sm.size, kvd), device="cuda")
+    kv.write_batch(0, torch.from_numpy(sm).cuda(), k, k)
+    seqs = np.arange(B, dtype=np.uint32)
+    d_sm = torch.from_numpy(kv.append_batch(seqs, ctx.astype(np.uint64))).cuda()
+    tables = torch.from_numpy(kv.block_tables(seqs)).cuda()
+    lens = torch.from_numpy((ctx + 1).astype(np.int32)).cuda()
+    kn = torch.randn((B, kvd), device="cuda")
+    q = torch.randn((B, n_heads * hd), device="cuda")
+    out = torch.empty_like(q)
+
+    def step():
+        kv.write_batch(0, d_sm, kn, kn)
+        kv.decode_attention(0, q, tables, lens, n_heads, hd, scale=0.125, out=out)
+
+    us = _time_op(step, reps=max(args.steps, 10))
+    a_us = _time_op(lambda: kv.decode_attention(0, q, tables, lens, n_heads, hd, scale=0.125, out=out),
+                    reps=max(args.steps, 10))
+    a_bytes = int((ctx + 1).sum()) * 2 * kvd * 4 + 2 * q.numel() * 4
+    print(json.dumps({"workload": "tinyllama f32, 4 seqs ctx U[128,512]", "step_us": round(us, 2),
+                      "attention_us": round(a_us, 2), "attention_bytes": a_bytes,
+                      "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}),
+          flush=True)
+
+
+def bench_prefix_cow(args):
+    """Prefix sharing at the Llama-3-8B layer shape: 256 sequences hold a
+    4088-token prefix (256 blocks, the last holding 8 tokens, refcount 256);
+    step 0 appends a 64-token private suffix to every sequence, which copies
+    the shared partial block 255 times (the last holder writes in place); then
+    32 decode steps. Attention bytes count shared blocks once (unique bytes)."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_heads, n_kv, hd, S, prefix, suffix, steps = 32, 8, 128, 256, 4088, 64, 32
+    kvd = n_kv * hd
+    rng = np.random.default_rng(args.seed)
+    per_seq = -(-(prefix + suffix + steps) // BLOCK) - prefix // BLOCK + 1
+    n_blocks = int((prefix // BLOCK + 1 + S * per_seq) * 1.1)
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(n_blocks))
+    _fill_pool_random(kv, kvd, n_blocks, args.seed)
+    kv.append_batch(np.zeros(prefix, np.uint32), np.arange(prefix, dtype=np.uint64))
+    for d in range(1, S):
+        kv.share(0, d, prefix)
+    # step 0: the suffix append (copy-on-write launched by the claim itself)
+    seqs0 = np.repeat(np.arange(S, dtype=np.uint32), suffix)
+    pos0 = np.tile(np.arange(prefix, prefix + suffix, dtype=np.uint64), S)
+    shared_last = int(kv.block_table(0)[-1])
+    kn = torch.randn((seqs0.size, kvd), device="cuda")
+    sm0 = kv.append_batch(seqs0, pos0)  # launches the 255 copies itself
+    d_sm0 = torch.from_numpy(sm0).cuda()
+    torch.cuda.synchronize()
+    assert kv.cow_copies() == S - 1, kv.cow_copies()
+    app_us = _time_op(lambda: kv.write_batch(0, d_sm0, kn, kn), reps=10)
+    cow_bytes = (S - 1) * 2 * 2 * BLOCK * kvd * 2
+    seqs = np.arange(S, dtype=np.uint32)
+    sms, lens = [], []
+    for s in range(steps):
+        pos = np.full(S, prefix + suffix + s, dtype=np.uint64)
+        sms.append(kv.append_batch(seqs, pos))
+        lens.append((pos + 1).astype(np.int32))
+    tables_h = kv.block_tables(seqs)
+    tables = torch.from_numpy(tables_h).cuda()
+    d_sm = torch.from_numpy(np.stack(sms)).cuda()
+    d_lens = torch.from_numpy(np.stack(lens)).cuda()
+    q = torch.randn((steps, S, n_heads * hd), device="cuda")
+    kd = torch.randn((steps, S, kvd), device="cuda")
+    out = torch.empty((S, n_heads * hd), device="cuda")
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for s in range(steps):
+        kv.write_batch(0, d_sm[s], kd[s], kd[s])
+        ev[s][0].record()
+        kv.decode_attention(0, q[s], tables, d_lens[s], n_heads, hd, out=out)
+        ev[s][1].record()
+    torch.cuda.synchronize()
+    att_us = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]) * 1e3)
+    # The copy-on-write copies of step 0 again, timed alone (same pairs).
+    dst = tables_h[:, prefix // BLOCK]
+    pairs = np.stack([np.full(S, shared_last), dst], 1)[dst != shared_last].astype(np.int32)
+    assert len(pairs) == S - 1
+    d_pairs = torch.from_numpy(pairs).cuda()
+    cow_us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=10)
+    uniq_blocks = len(np.unique(tables_h[tables_h >= 0]))
+    uniq = uniq_blocks * BLOCK * kvd * 2 * 2 + 2 * S * n_heads * hd * 4
+    logical = int(np.mean([l.astype(np.int64).sum() for l in lens])) * 2 * kvd * 2
+    print(json.dumps({
+        "workload": "prefix-cow llama3-8b f16: 256 seqs x 4088 shared + 64 private, 32 decode steps",
+        "cow_copies": S - 1, "cow_us": round(cow_us, 2), "cow_GBps": round(cow_bytes / (cow_us * 1e-6) / 1e9, 1),
+        "suffix_append_us": round(app_us, 2), "attention_us": round(att_us, 2),
+        "attention_unique_bytes": uniq, "attention_logical_bytes": logical,
+        "attention_frac_unique": round(uniq / (att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "attention_logical_GBps": round(logical / (att_us * 1e-6) / 1e9, 1)}), flush=True)
+
+
+def bench_mixed(args):
+    """Continuous batching at the Qwen2.5-7B layer shape (28 q heads, 4 kv
+    heads, head_dim 128, f16): every step appends 8 prefill chunks of 512
+    tokens and one token for each of 120 decode sequences (contexts U[512,
+    8192]), then runs decode attention for the 120. Decode sequences finish
+    with probability 2% per step (their blocks are freed, LIFO) and arrivals
+    take their slot from the fragmented pool; prefill streams restart when
+    their prompt is done. The allocator runs ahead of the timed device loop."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_heads, n_kv, hd, n_dec, n_pre, chunk, steps = 28, 4, 128, 120, 8, 512, max(args.steps, 1)
+    kvd = n_kv * hd
+    rng = np.random.default_rng(args.seed)
+    n_blocks = int((n_dec + n_pre) * 8192 // BLOCK * 1.1) + (n_dec + n_pre) * (steps // BLOCK + 2)
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(n_blocks))
+    _fill_pool_random(kv, kvd, n_blocks, args.seed)
+    next_id = [0]
+
+    def new_seq(ctx):
+        sid = next_id[0]
+        next_id[0] += 1
+        if ctx:
+            kv.append_batch(np.full(ctx, sid, np.uint32), np.arange(ctx, dtype=np.uint64))
+        return sid
+
+    dec = [new_seq(int(rng.integers(512, 8193))) for _ in range(n_dec)]
+    pre = [(new_seq(0), int(rng.integers(512, 8193))) for _ in range(n_pre)]
+    plan_sm, plan_tables, plan_lens = [], [], []
+    stride = (8192 + steps + chunk) // BLOCK + 2
+    for s in range(steps):
+        seqs, pos = [], []
+        for i, (sid, target) in enumerate(pre):
+            start = kv.len(sid)
+            n = min(chunk, target - start)
+            seqs += [sid] * n
+            pos += list(range(start, start + n))
+        for sid in dec:
+            seqs.append(sid)
+            pos.append(kv.len(sid))
+        sm = kv.append_batch(np.array(seqs, np.uint32), np.array(pos, np.uint64))
+        plan_sm.append(np.pad(sm, (0, n_pre * chunk + n_dec - sm.size), constant_values=-1))
+        plan_tables.append(kv.block_tables(np.array(dec, np.uint32), stride))
+        plan_lens.append(np.array([kv.len(sid) for sid in dec], np.int32))
+        for i, (sid, target) in enumerate(pre):  # prompt done: the stream restarts
+            if kv.len(sid) >= target:
+                kv.truncate(sid, 0)
+                pre[i] = (new_seq(0), int(rng.integers(512, 8193)))
+        for i, sid in enumerate(dec):  # 2% finish per step; an arrival takes the slot
+            if rng.random() < 0.02:
+                kv.truncate(sid, 0)
+                dec[i] = new_seq(int(rng.integers(512, 8193)))
+    d_sm = torch.from_numpy(np.stack(plan_sm)).cuda()
+    d_tables = torch.from_numpy(np.stack(plan_tables)).cuda()
+    d_lens = torch.from_numpy(np.stack(plan_lens)).cuda()
+    rows = n_pre * chunk + n_dec
+    kn = torch.randn((rows, kvd), device="cuda")
+    q = torch.randn((n_dec, n_heads * hd), device="cuda")
+    out = torch.empty_like(q)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s in range(steps):
+        ev[s][0].record()
+        kv.write_batch(0, d_sm[s], kn, kn)
+        ev[s][1].record()
+        kv.decode_attention(0, q, d_tables[s], d_lens[s], n_heads, hd, out=out)
+        ev[s][2].record()
+    torch.cuda.synchronize()
+    app_us = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]) * 1e3)
+    att_us = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]) * 1e3)
+    app_bytes = float(np.mean([(p >= 0).sum() for p in plan_sm])) * (kvd * 12 + 4)
+    att_bytes = float(np.mean([l.astype(np.int64).sum() for l in plan_lens])) * 2 * kvd * 2 + 2 * q.numel() * 4
+    print(json.dumps({
+        "workload": "mixed qwen2.5-7b f16: 8x512 prefill append + 120 decode, 2% churn, "
+                    f"{steps} steps", "append_us": round(app_us, 2),
+        "append_GBps": round(app_bytes / (app_us * 1e-6) / 1e9, 1),
+        "attention_us": round(att_us, 2), "attention_bytes": round(att_bytes),
+        "attention_frac": round(att_bytes / (att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "step_us": round(app_us + att_us, 2)}), flush=True)
+
+
 def main():
     args = _args()
     if args.gpus != 1:
@@ -286,7 +498,8 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
-    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context}
+    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
+             "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed}
     if args.workload in extra:
         extra[args.workload](args)
         return

@@ -526,55 +526,51 @@ __device__ __forceinline__ float bcast16(float x) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + K, 0xf, 0xf, false));
 }
 
-// The score layout of a tile with N = padded_group * 4 partial dots per lane,
-// index h*4 + j (head h, row slot j). The scatter splits index bits from the
-// top; head bits are split select-free (lane i keeps index r ^ g(i) in
-// register r, g linear over GF(2) with g(lane ^ mask_t) = g(lane) ^ split_t,
-// realised by permuting the lane's q registers), the two row bits with
-// selects, so K rows stay in natural (coalesced) lane order.
-template <int N>
+// The score layout of one scatter pass: N <= 16 partial dots per lane,
+// index h * 2^RB + j (head h, row j of the pass). The scatter splits index
+// bits from the top; head bits are split select-free (lane i keeps index
+// r ^ g(i) in register r, g linear over GF(2) with g(lane ^ mask_t) =
+// g(lane) ^ split_t, realised by permuting the lane's q registers), row bits
+// with selects, so K rows stay in natural (coalesced) lane order.
+template <int N, int RB>
 struct Scatter16 {
-  static constexpr int NPL = N > 16 ? N / 16 : 1;            // scores per lane after the scatter
-  static constexpr int T = N >= 16 ? 4 : (N == 8 ? 3 : 2);   // scatter steps (then all-reduce)
+  static_assert(N <= 16, "one score per lane at most");
+  static constexpr int T = N == 16 ? 4 : (N == 8 ? 3 : (N == 4 ? 2 : 1));  // scatter steps
   static constexpr int half(int t) { return (N >> t) / 2; }  // index value of the bit split at t
-  static constexpr bool free_step(int t) { return t < T && half(t) >= 4; }  // head bit
+  static constexpr bool free_step(int t) { return t < T && half(t) >= (1 << RB); }  // head bit
   static constexpr int gm(int t) { return free_step(t) ? half(t) : 0; }
   // g on the lane-bit basis e0..e3 (the masks 1, 2, 7, 15 span GF(2)^4).
   static constexpr int col(int b) {
     return b == 0 ? gm(3) : b == 1 ? gm(2) : b == 2 ? (gm(1) ^ gm(3) ^ gm(2)) : (gm(0) ^ gm(1));
   }
-  static constexpr int g(int lane) {
-    int r = 0;
-    for (int b = 0; b < 4; ++b)
-      if ((lane >> b) & 1) r ^= col(b);
-    return r;
-  }
   static constexpr int lane_bit(int t) { return 8 >> t; }  // lane bit told apart by partner map t
-  // Score index held by lane `lane` in register r (r < NPL) after the scatter.
-  static constexpr int held(int lane, int r) {
-    int idx = g(lane) ^ r;
+  // Score index held by lane `lane` after the scatter.
+  static constexpr int held(int lane) {
+    int idx = 0;
+    for (int b = 0; b < 4; ++b)
+      if ((lane >> b) & 1) idx ^= col(b);
     for (int t = 0; t < T; ++t)
       if (!free_step(t) && (lane & lane_bit(t))) idx += half(t);
     return idx;
   }
-  // A lane of the row holding score index idx (in register idx & (NPL-1)).
+  // A lane of the row holding score index idx.
   static constexpr int src(int idx) {
     for (int i = 0; i < 16; ++i)
-      if (held(i, idx & (NPL - 1)) == idx) return i;
+      if (held(i) == idx) return i;
     return 0;
   }
 };
 
-// In-place reduce-scatter over the 16 lanes of a row; afterwards v[r],
-// r < NPL, holds the row-wide sum of index held(lane, r).
-template <int N, int n, int t>
+// In-place reduce-scatter over the 16 lanes of a row; afterwards v[0]
+// holds the row-wide sum of index held(lane).
+template <int N, int RB, int n, int t>
 __device__ __forceinline__ void reduce_scatter16(float (&v)[N], int lane) {
-  using S = Scatter16<N>;
+  using S = Scatter16<N, RB>;
   if constexpr (t < 4) {
     if constexpr (S::free_step(t)) {
 #pragma unroll
       for (int r = 0; r < n / 2; ++r) v[r] += partner16<t>(v[r + n / 2]);
-      reduce_scatter16<N, n / 2, t + 1>(v, lane);
+      reduce_scatter16<N, RB, n / 2, t + 1>(v, lane);
     } else if constexpr (t < S::T) {
       const bool up = (lane & S::lane_bit(t)) != 0;
 #pragma unroll
@@ -583,10 +579,10 @@ __device__ __forceinline__ void reduce_scatter16(float (&v)[N], int lane) {
         const float keep = up ? v[r + n / 2] : v[r];
         v[r] = keep + partner16<t>(send);
       }
-      reduce_scatter16<N, n / 2, t + 1>(v, lane);
+      reduce_scatter16<N, RB, n / 2, t + 1>(v, lane);
     } else {
       v[0] += partner16<t>(v[0]);
-      reduce_scatter16<N, n, t + 1>(v, lane);
+      reduce_scatter16<N, RB, n, t + 1>(v, lane);
     }
   }
 }
@@ -623,11 +619,16 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   static_assert(HD / E == 16, "16 lanes per row");
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
   constexpr int GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;  // group padded to a power of two
-  constexpr int N = GP * LOADS;                                 // partial dots per lane per tile
-  using S = Scatter16<N>;
-  constexpr int NPL = S::NPL;                                   // scores per lane after the scatter
-  constexpr int R = N < 16 ? 16 / N : 1;                        // lanes holding the same score
-  constexpr int LPH = 16 / GP;                                  // lanes per head
+  // Groups of 8 heads scatter the tile in two passes of two row slots, which
+  // keeps 16 (not 32) partial dots live per lane.
+  constexpr int PASSES = GP == 8 ? 2 : 1;
+  constexpr int RPP = LOADS / PASSES;                 // row slots per pass
+  constexpr int RB = RPP == 4 ? 2 : 1;                // log2(RPP)
+  constexpr int N = GP * RPP;                         // partial dots per lane per pass (<= 16)
+  using S = Scatter16<N, RB>;
+  constexpr int NPL = PASSES;                         // scores per lane per tile
+  constexpr int R = N < 16 ? 16 / N : 1;              // lanes holding the same score
+  constexpr int LPH = 16 / GP;                        // lanes per head
 
   const int kvh = (int)(blockIdx.x % n_kv_heads);
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
@@ -646,26 +647,47 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
-  // Lane permutation of the head bits: register r of the partial dots holds
-  // head (r / 4) ^ (gl / 4), row slot r % 4, so q slot u holds head u ^ (gl / 4).
-  // Heads past G are zero queries (padding).
+  // Lane permutation of the head bits: register r of a pass's partial dots
+  // holds head (r >> RB) ^ (gl >> RB), row r % RPP, so q slot u holds head
+  // u ^ (gl >> RB). Heads past G are zero queries (padding).
   int gl = 0;
 #pragma unroll
   for (int bit = 0; bit < 4; ++bit)
     if ((c >> bit) & 1) gl ^= S::col(bit);
 
-  float qv[GP][E];
+  // Eight-head groups keep q in LDS (shared by the four waves and the four
+  // row groups, read per head right before use); smaller groups keep it in
+  // registers.
+  constexpr bool kQInLds = GP == 8;
+  __shared__ f32x4 sm_q[kQInLds ? GP * 16 * (E / 4) : 1];  // [slot u][lane c][E/4]
+  float qv[kQInLds ? 1 : GP][E];
   {
     const float *qp = q + qi * (int64_t)n_heads * HD + (int64_t)kvh * G * HD + c * E;
+    if constexpr (kQInLds) {
+      if (threadIdx.x < 16) {
 #pragma unroll
-    for (int u = 0; u < GP; ++u) {
-      const int h = u ^ (gl >> 2);
+        for (int u = 0; u < GP; ++u) {
+          const int h = u ^ (gl >> RB);
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        if (h < G) t = *reinterpret_cast<const f32x4 *>(qp + h * HD + e);
+          for (int e = 0; e < E; e += 4) {
+            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            if (h < G) t = *reinterpret_cast<const f32x4 *>(qp + h * HD + e);
+            sm_q[(u * 16 + c) * (E / 4) + e / 4] = t * qscale;
+          }
+        }
+      }
+      __syncthreads();
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qv[u][e + i] = t[i] * qscale;
+      for (int u = 0; u < GP; ++u) {
+        const int h = u ^ (gl >> RB);
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+          f32x4 t = {0.f, 0.f, 0.f, 0.f};
+          if (h < G) t = *reinterpret_cast<const f32x4 *>(qp + h * HD + e);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qv[u][e + i] = t[i] * qscale;
+        }
       }
     }
   }
@@ -677,14 +699,14 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) roff[j] = (uint32_t)(rg + RPL * j) * row_bytes + col_off;
   int my_row[NPL];  // tile rows of this lane's scores after the scatter
-  static_for<0, NPL>([&](auto rc) {
-    constexpr int r = decltype(rc)::value;
-    int row = 0;
+  {
+    int jj = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-      if (c == i) row = rg + RPL * (S::held(i, r) & 3);
-    my_row[r] = row;
-  });
+      if (c == i) jj = S::held(i) & (RPP - 1);
+#pragma unroll
+    for (int pass = 0; pass < NPL; ++pass) my_row[pass] = rg + RPL * (pass * RPP + jj);
+  }
   const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh * head_stride);
   const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh * head_stride);
   const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
@@ -724,29 +746,49 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
     const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
-    float v[N];
+    float sc[NPL];  // this lane's scores: one per pass
 #pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      float kf[E];
-      Tile<T>::unpack(kr[j], kf);
+    for (int pass = 0; pass < PASSES; ++pass) {
+      float v[N];
+      // Keeps the LDS reads of q inside the loop (not hoisted into registers).
+      if constexpr (kQInLds) asm volatile("" ::: "memory");
+      float kf[RPP][E];
+#pragma unroll
+      for (int jj = 0; jj < RPP; ++jj) Tile<T>::unpack(kr[pass * RPP + jj], kf[jj]);
 #pragma unroll
       for (int u = 0; u < GP; ++u) {
-        float a = 0.f;
+        float qu[E];
+        if constexpr (kQInLds) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) a = __builtin_fmaf(qv[u][e], kf[e], a);
-        v[u * LOADS + j] = a;
+          for (int e = 0; e < E; e += 4) {
+            const f32x4 t = sm_q[(u * 16 + c) * (E / 4) + e / 4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qu[e + i] = t[i];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) qu[e] = qv[u][e];
+        }
+#pragma unroll
+        for (int jj = 0; jj < RPP; ++jj) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) a = __builtin_fmaf(qu[e], kf[jj][e], a);
+          v[u * RPP + jj] = a;
+        }
       }
+      reduce_scatter16<N, RB, N, 0>(v, lane);
+      sc[pass] = v[0];
     }
-    reduce_scatter16<N, N, 0>(v, lane);
     if (valid < 16) {
 #pragma unroll
       for (int k = 0; k < NPL; ++k)
-        if (my_row[k] >= valid) v[k] = -INFINITY;
+        if (my_row[k] >= valid) sc[k] = -INFINITY;
     }
     // Online softmax of this lane's head over the tile's rows of this row group.
-    float bm = v[0];
+    float bm = sc[0];
 #pragma unroll
-    for (int k = 1; k < NPL; ++k) bm = __builtin_fmaxf(bm, v[k]);
+    for (int k = 1; k < NPL; ++k) bm = __builtin_fmaxf(bm, sc[k]);
     bm = head_reduce<LPH, 1, true>(bm);
     const float mn = __builtin_fmaxf(m_own, bm);
     const float mref = mn == -INFINITY ? 0.f : mn;
@@ -755,7 +797,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     float ps = 0.f;
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
-      p[k] = __builtin_amdgcn_exp2f(v[k] - mref);
+      p[k] = __builtin_amdgcn_exp2f(sc[k] - mref);
       ps += p[k];
     }
     ps = head_reduce<LPH, R, false>(ps);
@@ -765,7 +807,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     if (__builtin_amdgcn_ballot_w64(grew)) {  // wave-uniform: some head's max grew
       static_for<0, G>([&](auto hc) {
         constexpr int h = decltype(hc)::value;
-        const float a = bcast16<S::src(h * LOADS)>(alpha);
+        const float a = bcast16<S::src(h * RPP)>(alpha);
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[h][e] *= a;
       });
@@ -776,8 +818,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
       Tile<T>::unpack(vr[j], vf);
       static_for<0, G>([&](auto hc) {
         constexpr int h = decltype(hc)::value;
-        constexpr int idx = h * LOADS + j;  // score index of (head h, row slot j)
-        const float w = bcast16<S::src(idx)>(p[idx & (NPL - 1)]);
+        // (head h, row slot j): pass j / RPP, index h * RPP + j % RPP of it
+        const float w = bcast16<S::src(h * RPP + j % RPP)>(p[j / RPP]);
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
       });
@@ -815,8 +857,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   float m[G], l[G];
   static_for<0, G>([&](auto hc) {
     constexpr int h = decltype(hc)::value;
-    m[h] = bcast16<S::src(h * LOADS)>(m_own);
-    l[h] = bcast16<S::src(h * LOADS)>(l_own);
+    m[h] = bcast16<S::src(h * RPP)>(m_own);
+    l[h] = bcast16<S::src(h * RPP)>(l_own);
   });
 #pragma unroll
   for (int off = 16; off < 64; off <<= 1) {
