@@ -51,6 +51,22 @@ def _args():
     return p.parse_args()
 
 
+TRAFFIC_PROFILE = "profiles/attn16_llama3_decode.md"
+
+
+def _profiled_traffic():
+    """HBM bytes per attention launch (FETCH_SIZE x 2 + WRITE_SIZE, calibrated
+    against a plain copy) from the committed rocprofv3 summary of this workload."""
+    import re
+
+    try:
+        text = open(os.path.join(ROOT, TRAFFIC_PROFILE)).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", text)
+    return int(m.group(1)) if m else None
+
+
 def _cpu_threads(req: int) -> int:
     if req > 0:
         return req
@@ -564,8 +580,9 @@ def main():
         "append_GBps": round(app_gbps, 1),
         "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(att_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "attn_kernel + attn_merge_kernel (one decode-attention launch)",
+                     "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": _profiled_traffic(),
+                     "traffic_source": TRAFFIC_PROFILE,
+                     "kernel": "attn16_kernel + attn_merge_kernel (one decode-attention launch)",
                      "bytes_per_launch": round(att_bytes)},
         "wall_s": round(wall, 3),
         "cpu_baseline": cpu,
