@@ -167,8 +167,11 @@ LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t
                           size_t table_stride, const int32_t *d_lens, float *d_out);
 
 /* Tokens per context partition of the decode attention split (multiple of
- * 64; 0 = the default, 1024). Results depend on it only through summation
- * order; they never depend on the other queries of a batch. Tuning knob. */
+ * 64), or 0 (the default) for the per-query policy: a query is split into
+ * four partitions of ceil(len/4) rounded up to 64 tokens (at least 64) up to
+ * 4096 tokens, and into 1024-token partitions beyond. Either way a query's
+ * result depends only on its own inputs, never on the rest of the batch.
+ * Tuning knob. */
 LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
 
 /* ---- host conveniences (synchronous on the stream) --------------------- */

@@ -69,9 +69,6 @@ struct DeviceGuard {
   }
 };
 
-// Context tokens per decode-attention work-group (64 blocks, 16 per wave).
-constexpr size_t kDefaultPartition = 1024;
-
 }  // namespace
 
 struct ltkv_cache {
@@ -453,7 +450,8 @@ int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
 
 int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens) {
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
-  if (tokens % 64 != 0) return fail(LTKV_ERR_ARG, "partition must be a multiple of 64 tokens");
+  if (tokens % 64 != 0 || tokens > (size_t{1} << 30))
+    return fail(LTKV_ERR_ARG, "partition must be a multiple of 64 tokens, at most 2^30");
   c->attn_part_tokens = tokens;
   return LTKV_OK;
 }
@@ -477,12 +475,13 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (!d_q || !d_tables || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
   if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
 
-  // The partition size never depends on the batch, so a query's result is
-  // bit-identical whatever else is in the batch (the reference's property,
-  // engine/README.md:102). table_stride only bounds the grid.
+  // A query's partition size depends on its own length only (or is fixed by
+  // ltkv_set_attention_partition), so its result is bit-identical whatever
+  // else is in the batch (the reference's property, engine/README.md:102).
+  // table_stride only bounds the grid.
   const size_t max_tokens = table_stride * LTKV_BLOCK;
-  const size_t part = c->attn_part_tokens ? c->attn_part_tokens : kDefaultPartition;
-  const size_t max_parts = (max_tokens + part - 1) / part;
+  const int part = (int)c->attn_part_tokens;  // 0: per-query policy
+  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)max_tokens, part);
   if ((uint64_t)n * n_kv_heads * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
 
@@ -518,7 +517,7 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   a.n_kv_heads = (int)n_kv_heads;
   a.head_dim = (int)head_dim;
   a.scale = scale;
-  a.part_tokens = (int)part;
+  a.part_tokens = part;
   a.max_parts = (int)max_parts;
   HIP_TRY(ltkv::launch_decode_attention(g, a, c->stream), "decode attention launch");
   return LTKV_OK;

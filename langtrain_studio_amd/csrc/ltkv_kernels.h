@@ -44,8 +44,26 @@ struct AttnArgs {
   int64_t n;
   int n_heads, n_kv_heads, head_dim;
   float scale;
-  int part_tokens, max_parts;
+  int part_tokens, max_parts;  // part_tokens 0: per-query partition_tokens(len)
 };
+
+// Context tokens per attention partition when none is fixed: four
+// partitions of a query up to 4096 tokens (at least 64 tokens each), 1024
+// tokens beyond. It depends on the query's own length only, so a query's
+// result never depends on the rest of the batch.
+__host__ __device__ inline int partition_tokens(int64_t len, int fixed) {
+  if (fixed > 0) return fixed;
+  if (len > 4096) return 1024;
+  const int64_t p = ((len + 3) / 4 + 63) / 64 * 64;
+  return p < 64 ? 64 : (int)p;
+}
+
+// Upper bound of partitions per query for contexts up to max_tokens.
+inline int max_partitions(int64_t max_tokens, int fixed) {
+  if (fixed > 0) return (int)((max_tokens + fixed - 1) / fixed);
+  const int64_t beyond = (max_tokens + 1023) / 1024;
+  return (int)(beyond > 4 ? beyond : 4);
+}
 
 // Workspace of launch_decode_attention: partition partials (bytes == 0 when
 // one partition covers every query).

@@ -232,6 +232,8 @@ struct Tile<float> {
 };
 
 constexpr int kAttnWaves = 4;
+constexpr int kBufferWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9-family raw buffers
+constexpr int kNt = 2;                    // buffer load cache policy: non-temporal
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T, int HD, int G>
@@ -261,10 +263,11 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > table_stride * 16) len = table_stride * 16;
-  const int np = len > 0 ? (int)((len + part_tokens - 1) / part_tokens) : 1;
+  const int pt = partition_tokens(len, part_tokens);
+  const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;  // uniform over the work-group
-  const int64_t tok0 = (int64_t)part * part_tokens;
-  const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
+  const int64_t tok0 = (int64_t)part * pt;
+  const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
   float qv[G][E];
@@ -460,7 +463,8 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
-  const int np = (int)((len + part_tokens - 1) / part_tokens);
+  const int pt = partition_tokens(len, part_tokens);
+  const int np = (int)((len + pt - 1) / pt);
   if (np <= 1) return;  // a single partition wrote its output directly
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
@@ -506,9 +510,11 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
 //    the V pass fetches the weights it needs with row_newbcast;
 //  * the accumulators are rescaled only when some running max grew (a
 //    wave-uniform branch), which after the first tiles is rare;
-//  * loads take a scalar per-tile base plus a 32-bit per-lane offset fixed
-//    for the whole loop, and the tile pipeline is peeled (no tile is fetched
-//    twice).
+//  * loads go through per-tile buffer descriptors (scalar) with 32-bit
+//    per-lane offsets fixed for the whole loop; rows past the context and
+//    prefetches past a wave's last tile fall outside the descriptor's extent
+//    and read zeros without memory traffic, so the 2- or 3-stage tile
+//    pipeline has no conditional loads.
 // ----------------------------------------------------------------------------
 // The four DPP partner maps of the scatter: lane ^ 15, ^ 7, ^ 2, ^ 1.
 template <int T>
@@ -641,10 +647,11 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > table_stride * 16) len = table_stride * 16;
-  const int np = len > 0 ? (int)((len + part_tokens - 1) / part_tokens) : 1;
+  const int pt = partition_tokens(len, part_tokens);
+  const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;  // uniform over the work-group
-  const int64_t tok0 = (int64_t)part * part_tokens;
-  const int64_t tok1 = len < tok0 + part_tokens ? len : tok0 + part_tokens;
+  const int64_t tok0 = (int64_t)part * pt;
+  const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
   // Lane permutation of the head bits: register r of a pass's partial dots
@@ -720,27 +727,25 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   const int32_t *tab = tables + qi * table_stride;
 
-  // Rows of a tile past the context read row 0 of the tile instead (always
-  // inside the context, so finite); their weights are exactly 0.
+  // A tile is read through buffer descriptors whose extent ends at the last
+  // row inside the context: rows past it (and every row of a prefetch past
+  // the wave's last tile, extent 0) read as zeros without touching memory,
+  // so every load is unconditional and the wait counts stay static.
   auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
-    int32_t blk = tab[b];
+    const int bb = b < b1 ? b : b1 - 1;
+    int32_t blk = tab[bb];
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
-    const char *tk = kbase + (int64_t)blk * block_bytes;
-    const char *tv = vbase + (int64_t)blk * block_bytes;
-    const int valid = (int)(tok1 - (int64_t)b * 16);
-    if (valid >= 16) {
+    const int valid = b < b1 ? (int)(tok1 - (int64_t)b * 16) : 0;
+    const int rows = valid < 16 ? valid : 16;
+    const int extent = rows > 0 ? (rows - 1) * (int)row_bytes + HD * (int)sizeof(T) : 0;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(kbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(vbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
 #pragma unroll
-      for (int j = 0; j < LOADS; ++j) {
-        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tk + roff[j]));
-        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tv + roff[j]));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < LOADS; ++j) {
-        const uint32_t o = rg + RPL * j < valid ? roff[j] : col_off;
-        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tk + o));
-        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tv + o));
-      }
+    for (int j = 0; j < LOADS; ++j) {
+      kr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, roff[j], 0, kNt));
+      vr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, roff[j], 0, kNt));
     }
   };
 
@@ -826,28 +831,39 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     });
   };
 
-  // Peeled software pipeline: tile b+4 loads while tile b is computed; the
-  // last tile of a wave is computed without a prefetch.
+  // Software pipeline, STAGES - 1 tiles in flight while one is computed.
+  // Loads past the wave's last tile read nothing (extent 0).
+  constexpr int STAGES = GP <= 4 ? 3 : 2;
   {
-    u32x4 ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
+    constexpr int W = kAttnWaves;
     int b = b0 + wave;
     if (b < b1) {
-      load_tile(b, ka, va);
-      for (;;) {
-        if (b + kAttnWaves >= b1) {
-          compute_tile(b, ka, va);
-          break;
+      if constexpr (STAGES == 3) {
+        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS], k2[LOADS], v2[LOADS];
+        load_tile(b, k0, v0);
+        load_tile(b + W, k1, v1);
+        for (;;) {
+          load_tile(b + 2 * W, k2, v2);
+          compute_tile(b, k0, v0);
+          if ((b += W) >= b1) break;
+          load_tile(b + 2 * W, k0, v0);
+          compute_tile(b, k1, v1);
+          if ((b += W) >= b1) break;
+          load_tile(b + 2 * W, k1, v1);
+          compute_tile(b, k2, v2);
+          if ((b += W) >= b1) break;
         }
-        load_tile(b + kAttnWaves, kb, vb);
-        compute_tile(b, ka, va);
-        b += kAttnWaves;
-        if (b + kAttnWaves >= b1) {
-          compute_tile(b, kb, vb);
-          break;
+      } else {
+        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
+        load_tile(b, k0, v0);
+        for (;;) {
+          load_tile(b + W, k1, v1);
+          compute_tile(b, k0, v0);
+          if ((b += W) >= b1) break;
+          load_tile(b + W, k0, v0);
+          compute_tile(b, k1, v1);
+          if ((b += W) >= b1) break;
         }
-        load_tile(b + kAttnWaves, ka, va);
-        compute_tile(b, kb, vb);
-        b += kAttnWaves;
       }
     }
   }

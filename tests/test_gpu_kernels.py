@@ -279,6 +279,33 @@ def test_attention_partitions(gpu, partition):
     attention_close(out, want, "f16")
 
 
+@pytest.mark.parametrize("lens,fixed", [
+    ([1537, 1600, 1580], 448),     # ceil(len/4) in (384, 448]
+    ([2, 40, 255, 256], 64),       # the 64-token floor
+    ([4097, 9000, 5000], 1024),    # beyond 4096 tokens
+])
+def test_attention_default_policy_is_per_query_partition(gpu, lens, fixed):
+    """With no fixed partition a query of len tokens is split into partitions
+    of roundup64(ceil(len/4)) tokens (at least 64; 1024 past 4096 tokens):
+    the output equals, bit for bit, the one with that partition fixed."""
+    import torch
+
+    rng = np.random.default_rng(fixed)
+    kv_dim = 1024
+    blocks = sum(-(-n // BLOCK) for n in lens) + 4
+    g, o = _caches(1, kv_dim, blocks * BLOCK, "f16", rng.permutation(blocks))
+    fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, kv_dim)
+    tables, la = tables_and_lens(g, list(range(len(lens))), lens)
+    q = torch.from_numpy(rng.standard_normal((len(lens), 32 * 128), dtype=np.float32)).to(gpu)
+    dt, dl = torch.from_numpy(tables).to(gpu), torch.from_numpy(la).to(gpu)
+    auto = g.decode_attention(0, q, dt, dl, 32, 128).cpu().numpy()
+    g.set_attention_partition(fixed)
+    pinned = g.decode_attention(0, q, dt, dl, 32, 128).cpu().numpy()
+    np.testing.assert_array_equal(auto, pinned)
+    want = o.attention_tables(0, tables, la, q.cpu().numpy(), 32, 128, threads=8)
+    attention_close(auto, want, "f16")
+
+
 def test_attention_config_tinyllama_f32(gpu):
     """TinyLlama-shaped layer, f32 KV: 32 q heads, 4 kv heads, head_dim 64;
     4 sequences with contexts U[128,512] over a permuted 1024-block pool;
