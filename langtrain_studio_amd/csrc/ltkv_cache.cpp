@@ -437,7 +437,10 @@ int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
     return fail(LTKV_ERR_ARG, "null device pointer");
   if (((uintptr_t)d_k_out | (uintptr_t)d_v_out) % 16 != 0)
     return fail(LTKV_ERR_ARG, "outputs must be 16-byte aligned");
-  if ((uint64_t)n * table_stride * 256 >= (1ull << 32))
+  // One work-group of 1024 threads per 16 KiB of a block's K or V.
+  const uint64_t row_bytes = (uint64_t)c->kv_dim * c->geom.elem;
+  const uint64_t chunks = (row_bytes + 1023) / 1024;
+  if ((uint64_t)n * table_stride * 2 * chunks * 1024 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "n * table_stride too large for one launch");
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);

@@ -126,39 +126,29 @@ copy_blocks_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 3: gather. Work item = (sequence, table entry): the valid rows of
-// one block of K and of V are copied to their contiguous place. A row of the
-// token-major layout is contiguous, so the block's valid prefix is one
-// contiguous run in source and destination.
+// Kernel 3: gather. Work-group = (sequence, table entry, K or V, 16 KiB chunk
+// of the block): the valid rows of one block are one contiguous run in the
+// token-major layout, in source and destination, so each thread moves one
+// 16-byte vector. Small work-groups with one load per thread keep the most
+// loads in flight across the chip (measured faster than fewer, longer
+// work-groups on this scatter pattern).
 // ----------------------------------------------------------------------------
-constexpr int kGatherUnroll = 8;
+constexpr int kGatherThreads = 1024;
+constexpr int64_t kGatherChunk = kGatherThreads;  // 16-byte vectors per work-group
 
-__device__ __forceinline__ void copy_run(const u32x4 *__restrict__ s, u32x4 *__restrict__ d,
-                                         int64_t n16) {
-  for (int64_t base = 0; base < n16; base += 256 * kGatherUnroll) {
-    u32x4 r[kGatherUnroll];
-#pragma unroll
-    for (int u = 0; u < kGatherUnroll; ++u) {
-      const int64_t i = base + u * 256 + threadIdx.x;
-      if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
-    }
-#pragma unroll
-    for (int u = 0; u < kGatherUnroll; ++u) {
-      const int64_t i = base + u * 256 + threadIdx.x;
-      if (i < n16) __builtin_nontemporal_store(r[u], d + i);
-    }
-  }
-}
-
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kGatherThreads)
 gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpool,
               const int32_t *__restrict__ tables, int64_t table_stride,
               const int32_t *__restrict__ lens, const int64_t *__restrict__ out_offsets,
               uint8_t *__restrict__ kout, uint8_t *__restrict__ vout, int64_t n_blocks,
-              int64_t row_bytes) {
-  const int64_t wg = blockIdx.x;
-  const int64_t seq = wg / table_stride;
-  const int64_t j = wg - seq * table_stride;
+              int64_t row_bytes, int chunks) {
+  const int64_t per_entry = 2 * (int64_t)chunks;
+  const int64_t entry = blockIdx.x / per_entry;
+  const int part = (int)(blockIdx.x - entry * per_entry);
+  const int is_v = part >= chunks;
+  const int chunk = part - is_v * chunks;
+  const int64_t seq = entry / table_stride;
+  const int64_t j = entry - seq * table_stride;
   int64_t len = lens[seq];
   if (len > table_stride * 16) len = table_stride * 16;
   const int64_t start = j * 16;
@@ -166,11 +156,12 @@ gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpo
   const int64_t rows = len - start < 16 ? len - start : 16;
   const int32_t blk = tables[seq * table_stride + j];
   if (blk < 0 || blk >= n_blocks) return;
-  const int64_t n16 = (rows * row_bytes) >> 4;
-  const int64_t src = (int64_t)blk * 16 * row_bytes;
-  const int64_t dst = (out_offsets[seq] + start) * row_bytes;
-  copy_run(reinterpret_cast<const u32x4 *>(kpool + src), reinterpret_cast<u32x4 *>(kout + dst), n16);
-  copy_run(reinterpret_cast<const u32x4 *>(vpool + src), reinterpret_cast<u32x4 *>(vout + dst), n16);
+  const int64_t i = (int64_t)chunk * kGatherChunk + threadIdx.x;
+  if (i >= (rows * row_bytes) >> 4) return;
+  const u32x4 *src = reinterpret_cast<const u32x4 *>((is_v ? vpool : kpool) +
+                                                     (int64_t)blk * 16 * row_bytes);
+  u32x4 *dst = reinterpret_cast<u32x4 *>((is_v ? vout : kout) + (out_offsets[seq] + start) * row_bytes);
+  __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 // ----------------------------------------------------------------------------
@@ -1021,11 +1012,15 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
                          const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
                          hipStream_t s) {
   if (n <= 0 || table_stride <= 0) return hipSuccess;
-  const int64_t wgs = n * table_stride;
-  gather_kernel<<<(unsigned)wgs, 256, 0, s>>>(
+  const int64_t row_bytes = (int64_t)g.kv_dim * g.elem;
+  // A block's K (or V) is 16 rows = row_bytes 16-byte vectors.
+  const int chunks = (int)((row_bytes + kGatherChunk - 1) / kGatherChunk);
+  const int64_t wgs = n * table_stride * 2 * chunks;
+  if (wgs * kGatherThreads >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  gather_kernel<<<(unsigned)wgs, kGatherThreads, 0, s>>>(
       static_cast<const uint8_t *>(k_layer), static_cast<const uint8_t *>(v_layer), tables,
       table_stride, lens, out_offsets, static_cast<uint8_t *>(k_out),
-      static_cast<uint8_t *>(v_out), g.n_blocks, (int64_t)g.kv_dim * g.elem);
+      static_cast<uint8_t *>(v_out), g.n_blocks, row_bytes, chunks);
   return hipGetLastError();
 }
 
