@@ -174,6 +174,40 @@ LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t
  * Tuning knob. */
 LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
 
+/* ---- planned attention (one step descriptor, reused by every layer) ---- */
+
+/* Flags of ltkv_plan_attention. */
+#define LTKV_PLAN_SHARED_PREFIX 1u
+
+/* Plans one batch's attention from the cache's own block tables, the way
+ * NativeBackend::decode hands a batch to Model::forward
+ * (native/src/lib.rs:163-182, model.rs:431-475): query i reads positions
+ * [0, lens[i]) of sequence seqs[i] (lens[i] <= its length; 0 yields zeros).
+ * The tables are built on the host and uploaded once, on the cache stream,
+ * for every layer's ltkv_planned_attention of the step.
+ * With LTKV_PLAN_SHARED_PREFIX, queries whose tables begin with the same
+ * blocks (sequences forked by ltkv_share) form groups: the query rows of a
+ * group attend to its shared full blocks once, together, on the matrix
+ * cores (f16 pools; f32 pools ignore the flag), and each query's own
+ * remaining blocks as in ltkv_decode_attention; the two are merged by their
+ * softmax statistics. Results agree with ltkv_decode_attention within the
+ * attention tolerance (and bit for bit without the flag). A grouped query's
+ * summation order depends on its group, so it is not batch-invariant.
+ * The plan is invalidated by any later append, truncate, share or
+ * init_free_order (ltkv_planned_attention then fails). */
+LTKV_API int ltkv_plan_attention(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *lens,
+                        size_t n_heads, size_t head_dim, unsigned flags);
+
+/* Attention of the planned batch on one layer: q [n][n_heads*head_dim] f32
+ * (16-byte aligned), out [n][n_heads*head_dim] f32, device pointers. */
+LTKV_API int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float *d_q,
+                           float *d_out);
+
+/* Figures of the current plan: out[0] queries, [1] prefix groups, [2]
+ * grouped queries, [3] shared blocks (sum over groups), [4] shared-prefix
+ * work-groups, [5] table width in blocks. */
+LTKV_API int ltkv_plan_stats(const ltkv_cache *c, uint64_t out[6]);
+
 /* ---- host conveniences (synchronous on the stream) --------------------- */
 
 /* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */

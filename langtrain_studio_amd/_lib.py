@@ -46,6 +46,9 @@ SIGNATURES = {
     "ltkv_gather": (_int, [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp]),
     "ltkv_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp]),
     "ltkv_set_attention_partition": (_int, [_vp, _sz]),
+    "ltkv_plan_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _u32]),
+    "ltkv_planned_attention": (_int, [_vp, _sz, _f32, _vp, _vp]),
+    "ltkv_plan_stats": (_int, [_vp, _vp]),
     "ltkv_read_pool": (_int, [_vp, _sz, _vp, _vp]),
     "ltkv_rows": (_int, [_vp, _sz, _u32, _sz, _vp, _vp]),
     "ltkv_write_row": (_int, [_vp, _sz, _u32, _u32, _vp, _vp]),

@@ -55,6 +55,25 @@ struct Seq {
   size_t len = 0;               // kv.rs:31
 };
 
+// Step descriptor of ltkv_plan_attention: host-built tables, uploaded once.
+// Device arrays (int32, each 32-byte aligned inside one buffer): full tables
+// [n][stride], lens [n], suffix tables [n][sstride], suffix lens [n],
+// prefix partials per query [n], members [2 * n_members], jobs [n_jobs].
+struct AttnPlan {
+  bool valid = false;
+  uint64_t gen = 0;
+  size_t n = 0, n_heads = 0, head_dim = 0, stride = 0, sstride = 0;
+  int max_pre_parts = 0, n_jobs = 0;
+  uint64_t groups = 0, grouped = 0, shared_blocks = 0;
+  size_t off_tables = 0, off_lens = 0, off_stables = 0, off_slens = 0, off_pre = 0,
+         off_members = 0, off_jobs = 0, bytes = 0;
+  std::vector<int32_t> host;  // the arrays above, in device layout
+  uint8_t *d = nullptr, *h = nullptr;  // device buffer, pinned staging
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool in_flight = false;
+};
+
 // Switches to the cache's device for the scope of a call.
 struct DeviceGuard {
   int prev = -1;
@@ -96,6 +115,10 @@ struct ltkv_cache {
   size_t ws_bytes = 0;
   size_t attn_part_tokens = 0;  // 0 = automatic
 
+  // Bumped by every metadata change; a plan records the value it was built at.
+  uint64_t gen = 0;
+  AttnPlan plan;
+
   int device_count_cu = 256;
 
   size_t layer_elems() const { return n_blocks * LTKV_BLOCK * kv_dim; }
@@ -117,6 +140,7 @@ struct ltkv_cache {
   // kv.rs:85-121 without the device copy: a copy-on-write is recorded in
   // `pending` and launched by the caller before any later device work.
   int append_meta(uint32_t seq, size_t pos, uint32_t *block, uint32_t *slot) {
+    ++gen;
     Seq &s = seqs[seq];  // entry(seq).or_default()
     if (pos != s.len)
       return fail(LTKV_ERR_NONCONTIG, "seq %u: position %zu is not contiguous (length %zu)", seq,
@@ -183,6 +207,7 @@ struct ltkv_cache {
   }
 
   void truncate(uint32_t seq, size_t from) {  // kv.rs:153-169
+    ++gen;
     auto it = seqs.find(seq);
     if (it == seqs.end()) return;
     Seq &s = it->second;
@@ -195,6 +220,7 @@ struct ltkv_cache {
   }
 
   void share(uint32_t src, uint32_t dst, size_t len) {  // kv.rs:172-183
+    ++gen;
     truncate(dst, 0);
     auto it = seqs.find(src);
     if (it == seqs.end()) return;
@@ -205,6 +231,256 @@ struct ltkv_cache {
     if (len > 0) seqs[dst] = Seq{std::move(blocks), len};
   }
 };
+
+namespace {
+
+int check_attention_shape(const ltkv_cache *c, size_t n_heads, size_t head_dim, size_t *group) {
+  if (head_dim == 0 || c->kv_dim % head_dim != 0)
+    return fail(LTKV_ERR_ARG, "head_dim %zu does not divide kv_dim %zu", head_dim, c->kv_dim);
+  const size_t n_kv_heads = c->kv_dim / head_dim;
+  if (n_heads == 0 || n_heads % n_kv_heads != 0)
+    return fail(LTKV_ERR_ARG, "n_heads %zu is not a multiple of n_kv_heads %zu", n_heads, n_kv_heads);
+  *group = n_heads / n_kv_heads;
+  if (!ltkv::attention_supported((int)c->elem, (int)head_dim, (int)*group))
+    return fail(LTKV_ERR_ARG, "unsupported shape: head_dim %zu (64 or 128), group %zu (1..8)", head_dim,
+                *group);
+  return LTKV_OK;
+}
+
+// Grows the attention workspace to at least `bytes` (device of the cache current).
+int ensure_workspace(ltkv_cache *c, size_t bytes) {
+  if (bytes <= c->ws_bytes) return LTKV_OK;
+  if (c->ws) {
+    // The old workspace may still be read by enqueued work.
+    HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+    HIP_TRY(hipFree(c->ws), "hipFree(workspace)");
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+  }
+  HIP_TRY(hipMalloc((void **)&c->ws, bytes), "hipMalloc(workspace)");
+  c->ws_bytes = bytes;
+  return LTKV_OK;
+}
+
+ltkv::PoolGeom head_geom(const ltkv_cache *c, size_t head_dim) {
+  ltkv::PoolGeom g = c->geom;
+  g.head_stride = (int64_t)head_dim;  // token-major: heads are adjacent in a row
+  return g;
+}
+
+ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
+                         float scale, const float *d_q, float *d_out, const ltkv::AttnWorkspace &ws,
+                         int part, int max_parts) {
+  ltkv::AttnArgs a{};
+  a.k_layer = c->k_layer(layer);
+  a.v_layer = c->v_layer(layer);
+  a.q = d_q;
+  a.out = d_out;
+  a.part_o = ws.bytes ? (float *)(c->ws + ws.part_o_off) : nullptr;
+  a.part_ml = ws.bytes ? (float *)(c->ws + ws.part_ml_off) : nullptr;
+  a.n = (int64_t)n;
+  a.n_heads = (int)n_heads;
+  a.n_kv_heads = (int)(c->kv_dim / head_dim);
+  a.head_dim = (int)head_dim;
+  a.scale = scale;
+  a.part_tokens = part;
+  a.max_parts = max_parts;
+  return a;
+}
+
+// Fewest shared full blocks and members for a prefix group.
+constexpr size_t kMinSharedBlocks = 2;
+// Tokens per shared-prefix partition are at least this (a multiple of the
+// kernel's 32-token staging step).
+constexpr size_t kMinPrefixPart = 256;
+
+size_t align8(size_t x) { return (x + 7) / 8 * 8; }
+
+// Builds the plan's host arrays: tables, prefix groups, suffix tables, jobs.
+int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *lens, size_t n_heads,
+               size_t head_dim, size_t group, unsigned flags) {
+  AttnPlan &P = c->plan;
+  std::vector<const Seq *> sq(n, nullptr);
+  size_t stride = 1;
+  for (size_t i = 0; i < n; ++i) {
+    auto it = c->seqs.find(seqs[i]);
+    const size_t have = it == c->seqs.end() ? 0 : it->second.len;
+    if (lens[i] > have)
+      return fail(LTKV_ERR_RANGE, "query %zu: length %u exceeds the %zu tokens of seq %u", i, lens[i],
+                  have, seqs[i]);
+    if (it != c->seqs.end()) sq[i] = &it->second;
+    stride = std::max<size_t>(stride, (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK);
+  }
+
+  // Prefix groups: queries bucketed by their first block; in a bucket, the
+  // member set and shared length (common leading full blocks) that save the
+  // most block reads, (members - 1) * blocks.
+  struct Group {
+    std::vector<int32_t> members;
+    size_t blocks;
+  };
+  std::vector<Group> groups;
+  std::vector<size_t> pre_blocks(n, 0);
+  const size_t n_kv_heads = c->kv_dim / head_dim;
+  if ((flags & LTKV_PLAN_SHARED_PREFIX) && ltkv::mq_supported((int)c->elem, (int)head_dim, (int)group)) {
+    std::unordered_map<int32_t, size_t> bucket_of;
+    std::vector<std::vector<int32_t>> buckets;
+    for (size_t i = 0; i < n; ++i) {
+      if (lens[i] / LTKV_BLOCK < kMinSharedBlocks) continue;
+      auto ins = bucket_of.emplace(sq[i]->blocks[0], buckets.size());
+      if (ins.second) buckets.emplace_back();
+      buckets[ins.first->second].push_back((int32_t)i);
+    }
+    for (const auto &b : buckets) {
+      if (b.size() < 2) continue;
+      const std::vector<int32_t> &ref = sq[b[0]]->blocks;
+      const size_t ref_full = lens[b[0]] / LTKV_BLOCK;
+      std::vector<std::pair<size_t, int32_t>> lcp;  // (shared full blocks with b[0], query)
+      lcp.reserve(b.size());
+      for (int32_t m : b) {
+        const size_t cap = std::min<size_t>(lens[m] / LTKV_BLOCK, ref_full);
+        size_t k = 0;
+        while (k < cap && sq[m]->blocks[k] == ref[k]) ++k;
+        lcp.emplace_back(k, m);
+      }
+      std::stable_sort(lcp.begin(), lcp.end(),
+                       [](const auto &x, const auto &y) { return x.first > y.first; });
+      size_t best = 0, best_count = 0;
+      for (size_t cnt = 2; cnt <= lcp.size(); ++cnt) {
+        const size_t blocks = lcp[cnt - 1].first;
+        if (blocks < kMinSharedBlocks) break;
+        if ((cnt - 1) * blocks > best) {
+          best = (cnt - 1) * blocks;
+          best_count = cnt;
+        }
+      }
+      if (best_count < 2) continue;
+      Group gr;
+      gr.blocks = lcp[best_count - 1].first;
+      for (size_t k = 0; k < best_count; ++k) gr.members.push_back(lcp[k].second);
+      std::sort(gr.members.begin(), gr.members.end());
+      for (int32_t m : gr.members) pre_blocks[m] = gr.blocks;
+      groups.push_back(std::move(gr));
+    }
+  }
+
+  // Shared-prefix jobs: member tiles of kMqRows query rows; each group's
+  // prefix is split into partitions so the launch has about two work-groups
+  // per CU.
+  const size_t per_job = ltkv::kMqRows / group;  // members per work-group
+  size_t units = 0;
+  for (const auto &gr : groups) units += (gr.members.size() + per_job - 1) / per_job * n_kv_heads;
+  const size_t target = 2 * (size_t)c->device_count_cu;
+  std::vector<ltkv::MqJob> jobs;
+  std::vector<int32_t> members;
+  std::vector<int32_t> pre_parts(n, 0);
+  int max_pre_parts = 0;
+  uint64_t shared_blocks = 0, grouped = 0;
+  for (const auto &gr : groups) {
+    const size_t tokens = gr.blocks * LTKV_BLOCK;
+    const size_t max_split = std::max<size_t>(1, tokens / kMinPrefixPart);
+    const size_t split = std::min(max_split, std::max<size_t>(1, (target + units - 1) / units));
+    const size_t pt = ((tokens + split - 1) / split + 31) / 32 * 32;
+    const size_t parts = (tokens + pt - 1) / pt;
+    const size_t m0 = members.size() / 2;
+    for (int32_t m : gr.members) {
+      members.push_back(m);
+      members.push_back((int32_t)tokens);
+      pre_parts[m] = (int32_t)parts;
+    }
+    const size_t tiles = (gr.members.size() + per_job - 1) / per_job;
+    for (size_t p = 0; p < parts; ++p)
+      for (size_t h = 0; h < n_kv_heads; ++h)
+        for (size_t t = 0; t < tiles; ++t) {
+          ltkv::MqJob j{};
+          j.table = (int32_t)((size_t)gr.members[0] * stride);
+          j.t0 = (int32_t)(p * pt);
+          j.t1 = (int32_t)std::min(tokens, (p + 1) * pt);
+          j.member0 = (int32_t)(m0 + t * per_job);
+          j.n_members = (int32_t)std::min(per_job, gr.members.size() - t * per_job);
+          j.part = (int32_t)p;
+          j.kvh = (int32_t)h;
+          jobs.push_back(j);
+        }
+    max_pre_parts = std::max(max_pre_parts, (int)parts);
+    shared_blocks += gr.blocks;
+    grouped += gr.members.size();
+  }
+
+  size_t sstride = 1;
+  for (size_t i = 0; i < n; ++i)
+    sstride = std::max<size_t>(sstride, (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK - pre_blocks[i]);
+  if ((uint64_t)n * std::max(stride, sstride) > (uint64_t)INT32_MAX / 2)
+    return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
+
+  P.n = n;
+  P.n_heads = n_heads;
+  P.head_dim = head_dim;
+  P.stride = stride;
+  P.sstride = sstride;
+  P.max_pre_parts = max_pre_parts;
+  P.n_jobs = (int)jobs.size();
+  P.groups = groups.size();
+  P.grouped = grouped;
+  P.shared_blocks = shared_blocks;
+  P.off_tables = 0;
+  P.off_lens = align8(P.off_tables + n * stride);
+  P.off_stables = align8(P.off_lens + n);
+  P.off_slens = align8(P.off_stables + n * sstride);
+  P.off_pre = align8(P.off_slens + n);
+  P.off_members = align8(P.off_pre + n);
+  P.off_jobs = align8(P.off_members + members.size());
+  const size_t words = P.off_jobs + jobs.size() * (sizeof(ltkv::MqJob) / 4);
+  P.bytes = words * 4;
+  P.host.assign(words, 0);
+  int32_t *h = P.host.data();
+  for (size_t i = 0; i < n; ++i) {
+    const size_t nb = (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK;
+    int32_t *row = h + P.off_tables + i * stride;
+    int32_t *srow = h + P.off_stables + i * sstride;
+    for (size_t k = 0; k < stride; ++k) row[k] = k < nb ? sq[i]->blocks[k] : -1;
+    for (size_t k = 0; k < sstride; ++k) srow[k] = pre_blocks[i] + k < nb ? sq[i]->blocks[pre_blocks[i] + k] : -1;
+    h[P.off_lens + i] = (int32_t)lens[i];
+    h[P.off_slens + i] = (int32_t)(lens[i] - pre_blocks[i] * LTKV_BLOCK);
+    h[P.off_pre + i] = pre_parts[i];
+  }
+  std::copy(members.begin(), members.end(), h + P.off_members);
+  if (!jobs.empty()) std::memcpy(h + P.off_jobs, jobs.data(), jobs.size() * sizeof(ltkv::MqJob));
+  return LTKV_OK;
+}
+
+// Copies the plan's arrays to the device on the cache stream (pinned staging).
+int upload_plan(ltkv_cache *c) {
+  AttnPlan &P = c->plan;
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (!P.done) HIP_TRY(hipEventCreateWithFlags(&P.done, hipEventDisableTiming), "hipEventCreate");
+  if (P.in_flight) {  // the staging buffer may still be read by the last upload
+    HIP_TRY(hipEventSynchronize(P.done), "hipEventSynchronize");
+    P.in_flight = false;
+  }
+  if (P.bytes > P.cap) {
+    const size_t cap = std::max<size_t>(P.bytes, 2 * P.cap);
+    if (P.d) {  // enqueued attention may still read the old tables
+      HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+      HIP_TRY(hipFree(P.d), "hipFree(plan)");
+      P.d = nullptr;
+    }
+    if (P.h) (void)hipHostFree(P.h);
+    P.h = nullptr;
+    P.cap = 0;
+    HIP_TRY(hipHostMalloc((void **)&P.h, cap, hipHostMallocDefault), "hipHostMalloc(plan)");
+    HIP_TRY(hipMalloc((void **)&P.d, cap), "hipMalloc(plan)");
+    P.cap = cap;
+  }
+  std::memcpy(P.h, P.host.data(), P.bytes);
+  HIP_TRY(hipMemcpyAsync(P.d, P.h, P.bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(plan)");
+  HIP_TRY(hipEventRecord(P.done, c->stream), "hipEventRecord");
+  P.in_flight = true;
+  return LTKV_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -287,6 +563,9 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->h_pairs) (void)hipHostFree(c->h_pairs);
     if (c->d_pairs) (void)hipFree(c->d_pairs);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->plan.done) (void)hipEventDestroy(c->plan.done);
+    if (c->plan.h) (void)hipHostFree(c->plan.h);
+    if (c->plan.d) (void)hipFree(c->plan.d);
     if (c->k) (void)hipFree(c->k);
     if (c->v) (void)hipFree(c->v);
   }
@@ -383,6 +662,7 @@ int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n) {
   if (!c || (n && !order)) return fail(LTKV_ERR_ARG, "null argument");
   if (!c->seqs.empty() || c->free.size() != c->n_blocks)
     return fail(LTKV_ERR_ARG, "init_free_order needs a cache with no sequences");
+  ++c->gen;
   if (n != c->n_blocks) return fail(LTKV_ERR_ARG, "order has %zu entries, cache has %zu blocks", n, c->n_blocks);
   std::vector<uint8_t> seen(n, 0);
   for (size_t i = 0; i < n; ++i) {
@@ -465,14 +745,8 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
-  if (head_dim == 0 || c->kv_dim % head_dim != 0)
-    return fail(LTKV_ERR_ARG, "head_dim %zu does not divide kv_dim %zu", head_dim, c->kv_dim);
-  const size_t n_kv_heads = c->kv_dim / head_dim;
-  if (n_heads == 0 || n_heads % n_kv_heads != 0)
-    return fail(LTKV_ERR_ARG, "n_heads %zu is not a multiple of n_kv_heads %zu", n_heads, n_kv_heads);
-  const size_t group = n_heads / n_kv_heads;
-  if (!ltkv::attention_supported((int)c->elem, (int)head_dim, (int)group))
-    return fail(LTKV_ERR_ARG, "unsupported shape: head_dim %zu (64 or 128), group %zu (1..8)", head_dim, group);
+  size_t group = 0;
+  if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
   if (n == 0) return LTKV_OK;
   if (table_stride == 0) return fail(LTKV_ERR_ARG, "table_stride must be > 0");
   if (!d_q || !d_tables || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
@@ -482,47 +756,113 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   // ltkv_set_attention_partition), so its result is bit-identical whatever
   // else is in the batch (the reference's property, engine/README.md:102).
   // table_stride only bounds the grid.
-  const size_t max_tokens = table_stride * LTKV_BLOCK;
   const int part = (int)c->attn_part_tokens;  // 0: per-query policy
-  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)max_tokens, part);
-  if ((uint64_t)n * n_kv_heads * max_parts * 256 >= (1ull << 32))
+  const size_t max_parts =
+      (size_t)ltkv::max_partitions((int64_t)(table_stride * LTKV_BLOCK), part);
+  if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
 
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   const ltkv::AttnWorkspace ws =
       ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
-  if ((size_t)ws.bytes > c->ws_bytes) {
-    if (c->ws) {
-      // The old workspace may still be read by enqueued work.
-      HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-      HIP_TRY(hipFree(c->ws), "hipFree(workspace)");
-      c->ws = nullptr;
-      c->ws_bytes = 0;
-    }
-    HIP_TRY(hipMalloc((void **)&c->ws, (size_t)ws.bytes), "hipMalloc(workspace)");
-    c->ws_bytes = (size_t)ws.bytes;
-  }
-  ltkv::PoolGeom g = c->geom;
-  g.head_stride = (int64_t)head_dim;  // token-major: heads are adjacent in a row
-  ltkv::AttnArgs a{};
-  a.k_layer = c->k_layer(layer);
-  a.v_layer = c->v_layer(layer);
-  a.q = d_q;
+  if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
+  ltkv::AttnArgs a = attn_args(c, layer, n, n_heads, head_dim, scale, d_q, d_out, ws, part,
+                               (int)max_parts);
   a.tables = d_tables;
   a.table_stride = (int64_t)table_stride;
   a.lens = d_lens;
-  a.out = d_out;
-  a.part_o = ws.bytes ? (float *)(c->ws + ws.part_o_off) : nullptr;
-  a.part_ml = ws.bytes ? (float *)(c->ws + ws.part_ml_off) : nullptr;
-  a.n = (int64_t)n;
-  a.n_heads = (int)n_heads;
-  a.n_kv_heads = (int)n_kv_heads;
-  a.head_dim = (int)head_dim;
-  a.scale = scale;
-  a.part_tokens = part;
-  a.max_parts = (int)max_parts;
+  HIP_TRY(ltkv::launch_decode_attention(head_geom(c, head_dim), a, c->stream),
+          "decode attention launch");
+  return LTKV_OK;
+}
+
+int ltkv_plan_attention(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *lens,
+                        size_t n_heads, size_t head_dim, unsigned flags) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  c->plan.valid = false;
+  size_t group = 0;
+  if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
+  if (n && (!seqs || !lens)) return fail(LTKV_ERR_ARG, "null argument");
+  if (n > (size_t)INT32_MAX / 64) return fail(LTKV_ERR_ARG, "batch of %zu queries is too large", n);
+  if (int rc = build_plan(c, n, seqs, lens, n_heads, head_dim, group, flags)) return rc;
+  if (c->device != LTKV_NO_DEVICE) {
+    if (int rc = upload_plan(c)) return rc;
+  }
+  c->plan.valid = true;
+  c->plan.gen = c->gen;
+  return LTKV_OK;
+}
+
+int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float *d_q, float *d_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  const AttnPlan &P = c->plan;
+  if (!P.valid) return fail(LTKV_ERR_ARG, "no attention plan (ltkv_plan_attention)");
+  if (P.gen != c->gen)
+    return fail(LTKV_ERR_ARG, "the attention plan is stale: block tables changed after ltkv_plan_attention");
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (P.n == 0) return LTKV_OK;
+  if (!d_q || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
+  const size_t group = P.n_heads / (c->kv_dim / P.head_dim);
+  const int part = (int)c->attn_part_tokens;
+  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
+  if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
+    return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
+
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  const bool grouped = P.groups > 0;
+  const ltkv::AttnWorkspace ws = ltkv::attention_workspace(
+      (int64_t)P.n, (int)P.n_heads, (int)P.head_dim, (int)max_parts, grouped);
+  const size_t pre_slots = grouped ? P.n * P.n_heads * (size_t)P.max_pre_parts : 0;
+  const size_t pre_o_off = ((size_t)ws.bytes + 255) / 256 * 256;
+  const size_t pre_ml_off = pre_o_off + pre_slots * P.head_dim * 4;
+  if (int rc = ensure_workspace(c, pre_ml_off + pre_slots * 2 * 4)) return rc;
+  const int32_t *d = reinterpret_cast<const int32_t *>(P.d);
+  const ltkv::PoolGeom g = head_geom(c, P.head_dim);
+  ltkv::AttnArgs a = attn_args(c, layer, P.n, P.n_heads, P.head_dim, scale, d_q, d_out, ws, part,
+                               (int)max_parts);
+  a.tables = d + P.off_stables;
+  a.table_stride = (int64_t)P.sstride;
+  a.lens = d + P.off_slens;
+  if (grouped) {
+    a.pre_parts = d + P.off_pre;
+    a.pre_o = (float *)(c->ws + pre_o_off);
+    a.pre_ml = (float *)(c->ws + pre_ml_off);
+    a.max_pre_parts = P.max_pre_parts;
+    ltkv::MqArgs m{};
+    m.k_layer = a.k_layer;
+    m.v_layer = a.v_layer;
+    m.q = d_q;
+    m.tables = d + P.off_tables;
+    m.jobs = reinterpret_cast<const ltkv::MqJob *>(d + P.off_jobs);
+    m.n_jobs = P.n_jobs;
+    m.members = d + P.off_members;
+    m.pre_o = (float *)a.pre_o;
+    m.pre_ml = (float *)a.pre_ml;
+    m.n_heads = (int)P.n_heads;
+    m.n_kv_heads = a.n_kv_heads;
+    m.head_dim = (int)P.head_dim;
+    m.scale = scale;
+    m.max_pre_parts = P.max_pre_parts;
+    HIP_TRY(ltkv::launch_mq_attention(g, m, c->stream), "shared-prefix attention launch");
+  }
   HIP_TRY(ltkv::launch_decode_attention(g, a, c->stream), "decode attention launch");
+  return LTKV_OK;
+}
+
+int ltkv_plan_stats(const ltkv_cache *c, uint64_t out[6]) {
+  if (!c || !out) return fail(LTKV_ERR_ARG, "null argument");
+  const AttnPlan &P = c->plan;
+  if (!P.valid) return fail(LTKV_ERR_ARG, "no attention plan (ltkv_plan_attention)");
+  out[0] = P.n;
+  out[1] = P.groups;
+  out[2] = P.grouped;
+  out[3] = P.shared_blocks;
+  out[4] = (uint64_t)P.n_jobs;
+  out[5] = P.stride;
   return LTKV_OK;
 }
 

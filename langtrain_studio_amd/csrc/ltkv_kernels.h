@@ -45,6 +45,12 @@ struct AttnArgs {
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int part_tokens, max_parts;  // part_tokens 0: per-query partition_tokens(len)
+  // Shared-prefix partials folded into each query's result (planned
+  // attention), or pre_parts == nullptr: query i has pre_parts[i] partials
+  // at pre_o/pre_ml slot (i * n_heads + head) * max_pre_parts + p.
+  const int32_t *pre_parts;
+  const float *pre_o, *pre_ml;
+  int max_pre_parts;
 };
 
 // Context tokens per attention partition when none is fixed: four
@@ -70,8 +76,39 @@ inline int max_partitions(int64_t max_tokens, int fixed) {
 struct AttnWorkspace {
   int64_t part_o_off, part_ml_off, bytes;
 };
-AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts);
+// always: partials even when one partition covers every query (the planned
+// path merges them with shared-prefix partials).
+AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts,
+                                  bool always = false);
 bool attention_supported(int elem, int head_dim, int group);
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
+
+// One work-group of shared-prefix attention (mq_attn_kernel): the query rows
+// of n_members members of a prefix-sharing group (every query head of kv
+// head kvh) against tokens [t0, t1) of the group's shared blocks.
+struct MqJob {
+  int32_t table;               // offset of the group's block table in the tables array
+  int32_t t0, t1;              // token range
+  int32_t member0, n_members;  // members[2*member0 ...]: (query, token limit) pairs
+  int32_t part;                // partial slot of this token range
+  int32_t kvh;
+  int32_t pad;
+};
+constexpr int kMqRows = 128;  // query rows per work-group
+
+struct MqArgs {
+  const void *k_layer, *v_layer;
+  const float *q;
+  const int32_t *tables;
+  const MqJob *jobs;
+  int n_jobs;
+  const int32_t *members;
+  float *pre_o, *pre_ml;  // partial slots, laid out as AttnArgs::pre_o/pre_ml
+  int n_heads, n_kv_heads, head_dim;
+  float scale;
+  int max_pre_parts;
+};
+bool mq_supported(int elem, int head_dim, int group);
+hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s);
 
 }  // namespace ltkv

@@ -234,7 +234,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
             float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
-            int max_parts) {
+            int max_parts, const int32_t *__restrict__ pre_parts) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
   constexpr int RPL = 64 / L;      // rows per wave load
@@ -428,7 +428,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
       o += sm_acc[w][h][d] * a;
     }
     const int64_t qh = qi * n_heads + (int64_t)kvh * G + h;
-    if (np == 1) {
+    if (np == 1 && !(pre_parts && pre_parts[qi] > 0)) {  // else merged with prefix partials
       out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
     } else {
       const int64_t pi = qh * max_parts + part;
@@ -447,7 +447,9 @@ template <int HD>
 __global__ void __launch_bounds__(HD)
 attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                   const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
-                  int part_tokens, int max_parts, int64_t max_len) {
+                  int part_tokens, int max_parts, int64_t max_len,
+                  const int32_t *__restrict__ pre_parts, const float *__restrict__ pre_o,
+                  const float *__restrict__ pre_ml, int max_pre_parts) {
   const int h = (int)(blockIdx.x % n_heads);
   const int64_t qi = blockIdx.x / n_heads;
   const int d = threadIdx.x;
@@ -455,14 +457,24 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
   const int pt = partition_tokens(len, part_tokens);
-  const int np = (int)((len + pt - 1) / pt);
-  if (np <= 1) return;  // a single partition wrote its output directly
+  const int npre = pre_parts ? pre_parts[qi] : 0;
+  // With prefix partials the context kernels wrote partials even for a
+  // single partition; an empty context left an empty one (max -inf, sum 0).
+  const int np = npre > 0 ? (len > 0 ? (int)((len + pt - 1) / pt) : 1) : (int)((len + pt - 1) / pt);
+  if (np <= 1 && npre == 0) return;  // a single partition wrote its output directly
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
+  const float *pml = npre > 0 ? pre_ml + qh * max_pre_parts * 2 : nullptr;
   float mx = -INFINITY;
   for (int p = 0; p < np; ++p) mx = __builtin_fmaxf(mx, ml[2 * p]);
+  for (int p = 0; p < npre; ++p) mx = __builtin_fmaxf(mx, pml[2 * p]);
   const float mref = mx == -INFINITY ? 0.f : mx;
   float lsum = 0.f, o = 0.f;
+  for (int p = 0; p < npre; ++p) {
+    const float a = __builtin_amdgcn_exp2f(pml[2 * p] - mref);
+    lsum += pml[2 * p + 1] * a;
+    o += pre_o[(qh * max_pre_parts + p) * HD + d] * a;
+  }
   for (int p = 0; p < np; ++p) {
     const float a = __builtin_amdgcn_exp2f(ml[2 * p] - mref);
     lsum += ml[2 * p + 1] * a;
@@ -476,10 +488,11 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
 template <int HD>
 hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.max_parts == 1) return e;
+  if (e != hipSuccess || (a.max_parts == 1 && !a.pre_parts)) return e;
   const unsigned mgrid = (unsigned)(a.n * a.n_heads);
   attn_merge_kernel<HD><<<mgrid, HD, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
-                                             a.part_tokens, a.max_parts, a.table_stride * 16);
+                                             a.part_tokens, a.max_parts, a.table_stride * 16,
+                                             a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts);
   return hipGetLastError();
 }
 
@@ -611,7 +624,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
               float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
-              int max_parts) {
+              int max_parts, const int32_t *__restrict__ pre_parts) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
@@ -913,7 +926,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
       lsum += sm_l[w][h] * a;
       o += sm_acc[w][h][d] * a;
     }
-    if (np == 1) {
+    if (np == 1 && !(pre_parts && pre_parts[qi] > 0)) {  // else merged with prefix partials
       out[(qh0 + h) * HD + d] = lsum > 0.f ? o / lsum : 0.f;
     } else {
       const int64_t pi = (qh0 + h) * max_parts + part;
@@ -932,7 +945,8 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
   attn16_kernel<T, HD, G><<<grid, 256, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
-      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
+      a.pre_parts);
   return launch_merge<HD>(a, s);
 }
 
@@ -942,7 +956,8 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   attn_kernel<T, HD, G><<<grid, 256, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
-      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts);
+      g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
+      a.pre_parts);
   return launch_merge<HD>(a, s);
 }
 
@@ -971,6 +986,259 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
     case 7: return launch_attn_g<T, HD, 7>(g, a, s);
     case 8: return launch_attn_g<T, HD, 8>(g, a, s);
     default: return hipErrorInvalidValue;
+  }
+}
+
+
+// ----------------------------------------------------------------------------
+// Shared-prefix (cascade) attention. The members of a prefix-sharing group
+// read the same leading blocks, so their query rows (every member x every
+// query head of a kv head) attend to those blocks once, together: with
+// hundreds of rows per K/V row the work is GEMM-shaped, and it runs on MFMA
+// (v_mfma_f32_16x16x32_f16) instead of once per member on the VALU:
+//   S^T[token][row] = K Q^T   A = K rows (LDS), B = Q^T (registers)
+//   O^T[d][row]    += V^T P^T A = V^T (LDS transpose reads), B = P^T, whose
+//                             layout is the C layout of S^T
+// Q and P are f32; each is split into f16 hi + lo parts (hi + lo equals the
+// f32 value to about 2^-22 relative) and both products accumulate in f32,
+// so scores and sums keep f32 accuracy over the exact f16 K and V. The
+// result of a work-group is a partial (numerator, max, sum) per row for its
+// token range, folded into each member's output by attn_merge_kernel.
+//
+// Work-group: 4 waves x 32 rows (two 16-row tiles per wave); K and V are
+// staged 32 tokens at a time through double-buffered LDS.
+// Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, j = 0..7, i = 0..3):
+// A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16], D[4 (l / 16) + i][l % 16].
+// ds_read_b64_tr_b16 within each 16-lane group: lane i, element j is element
+// i % 4 of the 8 bytes addressed by lane 4 j + i / 4.
+// ----------------------------------------------------------------------------
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) hf4 lds_hf4;
+typedef __attribute__((address_space(3))) char lds_char;
+
+constexpr int kMqChunk = 32;  // tokens per staging step
+
+__device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const _Float16 h = (_Float16)x[j];
+    hi[j] = h;
+    lo[j] = (_Float16)(x[j] - (float)h);
+  }
+}
+
+__device__ __forceinline__ hf4 lds_read_tr(const char *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4 *)(lds_char *)p);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256, 2)  // two waves per SIMD: at most 256 registers
+mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool,
+               const float *__restrict__ q, const int32_t *__restrict__ tables,
+               const MqJob *__restrict__ jobs, int n_jobs, const int32_t *__restrict__ members,
+               float *__restrict__ pre_o, float *__restrict__ pre_ml, int n_heads, int group,
+               int64_t n_blocks, int64_t block_stride, int64_t slot_stride, float qscale,
+               int max_pre_parts) {
+  constexpr int KS = HD / 32;                // k steps of the score product
+  constexpr int DT = HD / 16;                // 16-wide d tiles of the output
+  constexpr int ROWB = HD * 2 + 16;          // LDS bytes per staged row (pad: no bank conflicts)
+  constexpr int VPR = HD / 8;                // 16-byte vectors per row
+  constexpr int NPT = kMqChunk * VPR / 256;  // vectors per thread per chunk, K and V each
+  static_assert(NPT >= 1 && kMqChunk * VPR % 256 == 0, "chunk must split over 256 threads");
+  __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V]
+
+  // Work-group b runs on XCD b % 8. Each XCD takes a contiguous run of the
+  // job list, in which the jobs of one token range (its member tiles) are
+  // adjacent, so their K/V reads are served by that XCD's L2.
+  const int per_xcd = (n_jobs + 7) / 8;
+  const int j = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (j >= n_jobs) return;
+  const MqJob jb = jobs[j];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lq = lane >> 4;
+  const int rows = jb.n_members * group;
+  const bool active = wave * 32 < rows;  // wave-uniform
+
+  // This lane's query row in each of the wave's two row tiles, as the B
+  // operand Q^T: 8 consecutive d of k step ks at d = 32 ks + 8 lq.
+  h8 qh[2][KS], ql[2][KS];
+  int limit[2];
+  int64_t slot[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = wave * 32 + rt * 16 + lr;
+    float x[KS][8];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[ks][e] = 0.f;
+    limit[rt] = 0;
+    slot[rt] = -1;
+    if (r < rows) {
+      const int m = r / group, hh = r - m * group;
+      const int qi = members[2 * (jb.member0 + m)];
+      limit[rt] = members[2 * (jb.member0 + m) + 1];
+      const int64_t qh_idx = (int64_t)qi * n_heads + (int64_t)jb.kvh * group + hh;
+      slot[rt] = qh_idx * max_pre_parts + jb.part;
+      const float *qp = q + qh_idx * HD + 8 * lq;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[ks][e] = a[e] * qscale;
+          x[ks][4 + e] = b[e] * qscale;
+        }
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) split_hl(x[ks], qh[rt][ks], ql[rt][ks]);
+  }
+
+  // Staging: token tok's row of this kv head is one contiguous HD-element
+  // run; tokens at or past t1 stage as zeros.
+  const int32_t *tab = tables + jb.table;
+  const int64_t head_off = (int64_t)jb.kvh * HD;
+  auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT]) {
+#pragma unroll
+    for (int u = 0; u < NPT; ++u) {
+      const int idx = threadIdx.x + 256 * u;
+      const int row = idx / VPR, col = idx - row * VPR;
+      const int tok = c0 + row;
+      kr[u] = u32x4{0u, 0u, 0u, 0u};
+      vr[u] = kr[u];
+      if (tok < jb.t1) {
+        const int32_t blk = tab[tok >> 4];
+        if (blk >= 0 && blk < n_blocks) {
+          const int64_t off = (int64_t)blk * block_stride + (tok & 15) * slot_stride + head_off + col * 8;
+          kr[u] = *reinterpret_cast<const u32x4 *>(kpool + off);
+          vr[u] = *reinterpret_cast<const u32x4 *>(vpool + off);
+        }
+      }
+    }
+  };
+  auto store_chunk = [&](int st, const u32x4 (&kr)[NPT], const u32x4 (&vr)[NPT]) {
+#pragma unroll
+    for (int u = 0; u < NPT; ++u) {
+      const int idx = threadIdx.x + 256 * u;
+      const int row = idx / VPR, col = idx - row * VPR;
+      *reinterpret_cast<u32x4 *>(&sm[st][0][row * ROWB + col * 16]) = kr[u];
+      *reinterpret_cast<u32x4 *>(&sm[st][1][row * ROWB + col * 16]) = vr[u];
+    }
+  };
+
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  f32x4 o[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int st, int c0) {
+    const char *ks_base = sm[st][0];
+    const char *vs_base = sm[st][1];
+    // Scores of 32 tokens (two 16-token tiles) x 32 rows.
+    f32x4 sc[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) sc[tt][0] = sc[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const h8 a = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWB + (32 * ks + 8 * lq) * 2);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], sc[tt][rt], 0, 0, 0);
+          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], sc[tt][rt], 0, 0, 0);
+        }
+      }
+    }
+    // Online softmax per row. This lane holds tokens 4 lq + i and 16 + 4 lq + i
+    // of its row; k slot j of the P^T operand is token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4.
+    h8 ph[2], pl[2];
+    float alpha[2];
+    bool grew = false;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int lim = (jb.t1 < limit[rt] ? jb.t1 : limit[rt]) - c0;  // visible tokens of the chunk
+      float x[8];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          x[tt * 4 + i] = tt * 16 + 4 * lq + i < lim ? sc[tt][rt][i] : -INFINITY;
+      float mx = x[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) mx = __builtin_fmaxf(mx, x[k]);
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = __builtin_fmaxf(m_run[rt], mx);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - mref);
+      grew |= mn > m_run[rt];
+      m_run[rt] = mn;
+      float p[8], ps = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        p[k] = __builtin_amdgcn_exp2f(x[k] - mref);
+        ps += p[k];
+      }
+      l_run[rt] = l_run[rt] * alpha[rt] + ps;
+      split_hl(p, ph[rt], pl[rt]);
+    }
+    if (__builtin_amdgcn_ballot_w64(grew)) {  // some row's max grew: rescale (the row is lr)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        o[dt][0] *= alpha[0];
+        o[dt][1] *= alpha[1];
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      // V^T operand: d = 16 dt + lr, tokens 4 lq + j (j < 4) and 16 + 4 lq + j - 4.
+      const int col = (dt * 16 + 4 * (lr & 3)) * 2;
+      const u32x2 a0 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (4 * lq + (lr >> 2)) * ROWB + col));
+      const u32x2 a1 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (16 + 4 * lq + (lr >> 2)) * ROWB + col));
+      const h8 a = __builtin_bit_cast(h8, u32x4{a0.x, a0.y, a1.x, a1.y});
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph[rt], o[dt][rt], 0, 0, 0);
+        o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl[rt], o[dt][rt], 0, 0, 0);
+      }
+    }
+  };
+
+  // Double-buffered staging: the next chunk's global loads are in flight
+  // while the current one is computed.
+  const int nch = (jb.t1 - jb.t0 + kMqChunk - 1) / kMqChunk;
+  u32x4 kr[NPT], vr[NPT];
+  load_chunk(jb.t0, kr, vr);
+  store_chunk(0, kr, vr);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const bool more = c + 1 < nch;
+    if (more) load_chunk(jb.t0 + (c + 1) * kMqChunk, kr, vr);
+    if (active) compute(c & 1, jb.t0 + c * kMqChunk);
+    if (more) store_chunk((c + 1) & 1, kr, vr);
+    __syncthreads();
+  }
+
+  // Partial per row: the row's sum is spread over its four lanes (lq).
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = l_run[rt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (slot[rt] >= 0) {
+      float *po = pre_o + slot[rt] * HD + 4 * lq;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(po + dt * 16) = o[dt][rt];
+      if (lq == 0) {
+        pre_ml[2 * slot[rt]] = m_run[rt];
+        pre_ml[2 * slot[rt] + 1] = l;
+      }
+    }
   }
 }
 
@@ -1024,9 +1292,10 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
   return hipGetLastError();
 }
 
-AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts) {
+AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts,
+                                  bool always) {
   AttnWorkspace w{};
-  if (max_parts <= 1) return w;
+  if (max_parts <= 1 && !always) return w;
   const int64_t parts = n * n_heads * (int64_t)max_parts;
   w.part_o_off = 0;
   w.part_ml_off = parts * head_dim * 4;
@@ -1049,6 +1318,30 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
     if (a.head_dim == 128) return launch_attn_hd<float, 128>(g, a, s);
   }
   return hipErrorInvalidValue;
+}
+
+bool mq_supported(int elem, int head_dim, int group) {
+  return elem == 2 && (head_dim == 64 || head_dim == 128) && group >= 1 && group <= kMqRows;
+}
+
+hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s) {
+  if (a.n_jobs <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)(8 * ((a.n_jobs + 7) / 8));
+  const int group = a.n_heads / a.n_kv_heads;
+  const auto *k = static_cast<const _Float16 *>(a.k_layer);
+  const auto *v = static_cast<const _Float16 *>(a.v_layer);
+  const float qscale = a.scale * kLog2e;
+  if (a.head_dim == 128)
+    mq_attn_kernel<128><<<grid, 256, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
+                                             a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
+                                             g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
+  else if (a.head_dim == 64)
+    mq_attn_kernel<64><<<grid, 256, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
+                                            a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
+                                            g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 }  // namespace ltkv

@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
-from typing import Optional
+from typing import Optional, Sequence
 
 import numpy as np
 
@@ -89,6 +89,7 @@ class KvCache:
         self.elem = 2 if dtype == "f16" else 4
         self.device = device
         self.n_blocks = self._lib.ltkv_n_blocks(h)
+        self._plan_shape = None
         if stream is not None:
             self.set_stream(stream)
 
@@ -267,6 +268,47 @@ class KvCache:
             _dev_ptr(q, torch.float32, "q", self.device),
             _dev_ptr(tables, torch.int32, "tables", self.device), tables.shape[1],
             _dev_ptr(lens, torch.int32, "lens", self.device),
+            _dev_ptr(out, torch.float32, "out", self.device)))
+        return out
+
+    def plan_attention(self, seqs: Sequence[int], lens: Sequence[int], n_heads: int, head_dim: int,
+                       shared_prefix: bool = True) -> dict:
+        """Step descriptor for planned_attention: query i reads positions
+        [0, lens[i]) of sequence seqs[i]; with shared_prefix, queries forked
+        from a common prefix attend to its shared blocks once, together.
+        Returns the plan's figures."""
+        seqs_a = np.ascontiguousarray(seqs, dtype=np.uint32)
+        lens_a = np.ascontiguousarray(lens, dtype=np.uint32)
+        if seqs_a.shape != lens_a.shape or seqs_a.ndim != 1:
+            raise ValueError("seqs and lens must be 1-D of equal length")
+        _check(self._lib.ltkv_plan_attention(self._h, len(seqs_a), _np_ptr(seqs_a), _np_ptr(lens_a),
+                                             n_heads, head_dim, 1 if shared_prefix else 0))
+        self._plan_shape = (len(seqs_a), n_heads * head_dim, head_dim)
+        return self.plan_stats()
+
+    def plan_stats(self) -> dict:
+        out = np.zeros(6, dtype=np.uint64)
+        _check(self._lib.ltkv_plan_stats(self._h, _np_ptr(out)))
+        keys = ("queries", "groups", "grouped", "shared_blocks", "prefix_workgroups", "table_width")
+        return {k: int(v) for k, v in zip(keys, out)}
+
+    def planned_attention(self, layer: int, q, scale: Optional[float] = None, out=None):
+        """Attention of the planned batch on one layer; q, out [n][n_heads*head_dim] f32."""
+        import torch
+
+        if self._plan_shape is None:
+            raise KvError(_lib.ERR_ARG, "no attention plan (plan_attention)")
+        n, width, head_dim = self._plan_shape
+        if q.dim() != 2 or q.shape != (n, width):
+            raise ValueError("q must be [n][n_heads*head_dim] of the plan")
+        if out is None:
+            out = torch.empty_like(q)
+        elif out.shape != q.shape:
+            raise ValueError("out must match q")
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)  # model.rs:402
+        _check(self._lib.ltkv_planned_attention(
+            self._h, layer, float(scale), _dev_ptr(q, torch.float32, "q", self.device),
             _dev_ptr(out, torch.float32, "out", self.device)))
         return out
 

@@ -28,10 +28,19 @@ def fill_sequences(caches, seq_lens, rng, kv_dim, layers=(0,), special=False):
     same K/V rows into every cache. `caches` holds (kind, cache) pairs with
     kind "gpu" (langtrain_studio_amd.KvCache) or "oracle" (oracle.OracleKv).
     Returns the f32 K and V rows written, per layer."""
-    import torch
-
     seqs = np.concatenate([np.full(n, s, dtype=np.uint32) for s, n in seq_lens.items()])
     pos = np.concatenate([np.arange(n, dtype=np.uint64) for n in seq_lens.values()])
+    return append_rows(caches, seqs, pos, rng, kv_dim, layers, special)
+
+
+def append_rows(caches, seqs, pos, rng, kv_dim, layers=(0,), special=False):
+    """Claim cells for tokens (seqs[i], pos[i]) in every cache (in order, so
+    copy-on-write happens as the reference's claim loop does) and write the
+    same random K/V rows into them. Returns the slot mapping and the rows."""
+    import torch
+
+    seqs = np.asarray(seqs, dtype=np.uint32)
+    pos = np.asarray(pos, dtype=np.uint64)
     sms = [c.append_batch(seqs, pos) for _, c in caches]
     for sm in sms[1:]:
         np.testing.assert_array_equal(sm, sms[0])

@@ -1,0 +1,163 @@
+"""Planned attention on the GPU (ltkv_plan_attention + ltkv_planned_attention)
+against the oracle's attention closure (model.rs:431-475 over kv.rs tables):
+without prefix groups it is the decode kernel on host-built tables (bit-exact
+with ltkv_decode_attention); with them, the shared blocks of forked sequences
+go through the matrix-core kernel once per group and are merged with each
+query's own blocks (attention tolerance)."""
+
+import numpy as np
+import pytest
+
+from helpers import BLOCK, append_rows, attention_close, fill_sequences, tables_and_lens
+
+pytestmark = pytest.mark.gpu
+
+
+def _caches(n_layers, kv_dim, n_tokens, dtype, rng):
+    from langtrain_studio_amd import KvCache
+    from oracle import OracleKv
+
+    g = KvCache(n_layers, kv_dim, n_tokens, dtype=dtype, device=0)
+    o = OracleKv(n_layers, kv_dim, n_tokens, dtype=dtype)
+    order = rng.permutation(g.n_blocks)
+    g.init_free_order(order)
+    o.init_free_order(order)
+    return g, o
+
+
+def _forked(rng, kv_dim, dtype, spec, singles=(), n_layers=1):
+    """spec: (root, prefix_len, [(child, extra_tokens), ...]) -- the root holds
+    prefix_len tokens, each child shares them (kv.rs:172-183) and appends its
+    own tokens (copy-on-write of the shared partial block, kv.rs:95-110).
+    singles: (seq, len) sequences that share nothing."""
+    need = sum(p + sum(e for _, e in kids) + 16 * (len(kids) + 1) for _, p, kids in spec)
+    need += sum(n + 16 for _, n in singles) + 64 * BLOCK
+    g, o = _caches(n_layers, kv_dim, need, dtype, rng)
+    both = [("gpu", g), ("oracle", o)]
+    layers = tuple(range(n_layers))
+    for root, prefix, kids in spec:
+        append_rows(both, [root] * prefix, np.arange(prefix), rng, kv_dim, layers)
+        for child, extra in kids:
+            g.share(root, child, prefix)
+            o.share(root, child, prefix)
+            if extra:
+                append_rows(both, [child] * extra, np.arange(prefix, prefix + extra), rng, kv_dim, layers)
+    if singles:
+        fill_sequences(both, dict(singles), rng, kv_dim, layers)
+    assert g.cow_copies() == o.cow_copies()
+    return g, o
+
+
+def _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, shared=True, layer=0, dtype="f16"):
+    import torch
+
+    q = rng.standard_normal((len(seqs), n_heads * head_dim), dtype=np.float32)
+    stats = g.plan_attention(seqs, lens, n_heads, head_dim, shared_prefix=shared)
+    out = g.planned_attention(layer, torch.from_numpy(q).to(gpu)).cpu().numpy()
+    tables, la = tables_and_lens(g, seqs, lens)
+    want = o.attention_tables(layer, tables, la, q, n_heads, head_dim, threads=8)
+    attention_close(out, want, dtype)
+    return stats, q, out, tables, la
+
+
+def test_planned_without_groups_is_the_decode_kernel(gpu):
+    """Host-built tables, one upload: bit-identical to ltkv_decode_attention."""
+    import torch
+
+    rng = np.random.default_rng(40)
+    lens = [1, 17, 300, 1031, 2500, 64]
+    g, o = _caches(1, 1024, (sum(lens) // BLOCK + 32) * BLOCK, "f16", rng)
+    fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, 1024)
+    seqs = list(range(len(lens)))
+    _, q, out, tables, la = _run(gpu, g, o, seqs, lens, 32, 128, rng, shared=False)
+    ref = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(la).to(gpu), 32, 128).cpu().numpy()
+    np.testing.assert_array_equal(out, ref)
+
+
+@pytest.mark.parametrize("n_kids,prefix", [(70, 2040), (3, 100), (256, 504)])
+def test_prefix_sharing_forks(gpu, n_kids, prefix):
+    """Sequences forked from one prefix with private suffixes (Llama-3-8B
+    heads, f16): one group over the common full blocks; output within the
+    attention tolerance of the oracle and of the per-query decode kernel."""
+    import torch
+
+    rng = np.random.default_rng(n_kids + prefix)
+    kids = [(1 + i, int(rng.integers(1, 71))) for i in range(n_kids)]
+    g, o = _forked(rng, 1024, "f16", [(0, prefix, kids)])
+    seqs = [s for s, _ in kids]
+    lens = [g.len(s) for s in seqs]
+    stats, q, out, tables, la = _run(gpu, g, o, seqs, lens, 32, 128, rng)
+    assert stats["groups"] == 1 and stats["grouped"] == n_kids
+    assert stats["shared_blocks"] == prefix // BLOCK
+    ref = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(la).to(gpu), 32, 128).cpu().numpy()
+    attention_close(out, ref, "f16")
+
+
+@pytest.mark.parametrize("head_dim,group", [(128, 1), (128, 4), (128, 7), (128, 8), (64, 4), (64, 8)])
+def test_prefix_groups_shapes(gpu, head_dim, group):
+    """Two groups, their roots, sequences sharing nothing, a fork with an
+    empty suffix (its whole context is shared) and an empty read, for each
+    supported head shape."""
+    rng = np.random.default_rng(head_dim * 10 + group)
+    n_kv = 2
+    kv_dim = n_kv * head_dim
+    spec = [(0, 333, [(1, 5), (2, 0), (3, 40), (4, 16)]),
+            (10, 1200, [(11 + i, int(rng.integers(0, 50))) for i in range(20)])]
+    g, o = _forked(rng, kv_dim, "f16", spec, singles=[(50, 700), (51, 3)])
+    seqs = [0, 1, 2, 3, 4, 10] + [11 + i for i in range(20)] + [50, 51, 2]
+    lens = [g.len(s) for s in seqs]
+    lens[-1] = 0  # an empty read of a grouped sequence
+    stats, *_ = _run(gpu, g, o, seqs, lens, group * n_kv, head_dim, rng)
+    assert stats["groups"] == 2
+
+
+def test_plan_serves_every_layer_and_replans(gpu):
+    """One plan for several layers; a second plan of another batch reuses
+    the buffers."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    kids = [(1 + i, int(rng.integers(1, 40))) for i in range(12)]
+    g, o = _forked(rng, 1024, "f16", [(0, 900, kids)], singles=[(40, 2000)], n_layers=3)
+    seqs = [s for s, _ in kids] + [40]
+    lens = [g.len(s) for s in seqs]
+    q = rng.standard_normal((len(seqs), 32 * 128), dtype=np.float32)
+    g.plan_attention(seqs, lens, 32, 128)
+    tables, la = tables_and_lens(g, seqs, lens)
+    for layer in (2, 0, 1):
+        out = g.planned_attention(layer, torch.from_numpy(q).to(gpu)).cpu().numpy()
+        want = o.attention_tables(layer, tables, la, q, 32, 128, threads=8)
+        attention_close(out, want, "f16")
+    _run(gpu, g, o, seqs[:3], lens[:3], 32, 128, rng, layer=1)
+    _run(gpu, g, o, seqs[::-1], lens[::-1], 32, 128, rng, layer=2)
+
+
+def test_stale_plan_is_rejected(gpu):
+    import torch
+
+    from langtrain_studio_amd import KvError
+
+    rng = np.random.default_rng(42)
+    g, o = _forked(rng, 1024, "f16", [(0, 100, [(1, 3), (2, 3)])])
+    g.plan_attention([1, 2], [g.len(1), g.len(2)], 32, 128)
+    g.append(1, g.len(1))
+    q = torch.zeros((2, 32 * 128), dtype=torch.float32, device=gpu)
+    with pytest.raises(KvError, match="stale"):
+        g.planned_attention(0, q)
+
+
+def test_f32_pools_plan_without_groups(gpu):
+    """f32 pools ignore the shared-prefix flag: bit-identical to the decode kernel."""
+    import torch
+
+    rng = np.random.default_rng(43)
+    g, o = _forked(rng, 256, "f32", [(0, 300, [(1, 4), (2, 9)])])
+    seqs = [0, 1, 2]
+    lens = [g.len(s) for s in seqs]
+    stats, q, out, tables, la = _run(gpu, g, o, seqs, lens, 32, 64, rng, dtype="f32")
+    assert stats["groups"] == 0
+    ref = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
+                             torch.from_numpy(la).to(gpu), 32, 64).cpu().numpy()
+    np.testing.assert_array_equal(out, ref)
