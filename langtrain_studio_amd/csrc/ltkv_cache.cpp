@@ -64,6 +64,7 @@ struct AttnPlan {
   uint64_t gen = 0;
   size_t n = 0, n_heads = 0, head_dim = 0, stride = 0, sstride = 0;
   int max_pre_parts = 0, n_jobs = 0;
+  int suffix_part = 0;  // partition tokens of the per-query pass when grouped
   uint64_t groups = 0, grouped = 0, shared_blocks = 0;
   size_t off_tables = 0, off_lens = 0, off_stables = 0, off_slens = 0, off_pre = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
@@ -364,13 +365,14 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     }
   }
 
-  // Shared-prefix jobs: member tiles of kMqRows query rows; each group's
-  // prefix is split into partitions so the launch has about two work-groups
-  // per CU.
-  const size_t per_job = ltkv::kMqRows / group;  // members per work-group
+  // Shared-prefix jobs: member tiles of mq_rows query rows; each group's
+  // prefix is split into partitions so the launch has about two waves per
+  // SIMD.
+  const size_t per_job = (size_t)ltkv::mq_rows((int)head_dim) / group;  // members per work-group
   size_t units = 0;
   for (const auto &gr : groups) units += (gr.members.size() + per_job - 1) / per_job * n_kv_heads;
-  const size_t target = 2 * (size_t)c->device_count_cu;
+  const size_t waves = (size_t)ltkv::mq_rows((int)head_dim) / 32;
+  const size_t target = 8 * (size_t)c->device_count_cu / waves;  // two waves per SIMD
   std::vector<ltkv::MqJob> jobs;
   std::vector<int32_t> members;
   std::vector<int32_t> pre_parts(n, 0);
@@ -408,8 +410,15 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   }
 
   size_t sstride = 1;
-  for (size_t i = 0; i < n; ++i)
+  uint64_t suffix_tokens = 0;
+  for (size_t i = 0; i < n; ++i) {
     sstride = std::max<size_t>(sstride, (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK - pre_blocks[i]);
+    suffix_tokens += lens[i] - pre_blocks[i] * LTKV_BLOCK;
+  }
+  // With groups the per-query pass covers the (usually short) remainders:
+  // single-wave work-groups, about eight per CU, whatever the batch.
+  const uint64_t per_wg = suffix_tokens * n_kv_heads / (8 * (uint64_t)c->device_count_cu) + 1;
+  P.suffix_part = (int)std::min<uint64_t>(1024, std::max<uint64_t>(64, (per_wg + 63) / 64 * 64));
   if ((uint64_t)n * std::max(stride, sstride) > (uint64_t)INT32_MAX / 2)
     return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
 
@@ -806,14 +815,21 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   if (!d_q || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
   if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
   const size_t group = P.n_heads / (c->kv_dim / P.head_dim);
-  const int part = (int)c->attn_part_tokens;
+  const bool grouped = P.groups > 0;
+  // Grouped plans are batch-dependent anyway: their per-query pass takes the
+  // plan's partition and single-wave work-groups unless a partition is fixed.
+  int part = (int)c->attn_part_tokens;
+  int waves = 4;
+  if (grouped && part == 0) {
+    part = P.suffix_part;
+    waves = 1;
+  }
   const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
   if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
 
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  const bool grouped = P.groups > 0;
   const ltkv::AttnWorkspace ws = ltkv::attention_workspace(
       (int64_t)P.n, (int)P.n_heads, (int)P.head_dim, (int)max_parts, grouped);
   const size_t pre_slots = grouped ? P.n * P.n_heads * (size_t)P.max_pre_parts : 0;
@@ -827,6 +843,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
   a.lens = d + P.off_slens;
+  a.waves = waves;
   if (grouped) {
     a.pre_parts = d + P.off_pre;
     a.pre_o = (float *)(c->ws + pre_o_off);
@@ -847,6 +864,8 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
     m.head_dim = (int)P.head_dim;
     m.scale = scale;
     m.max_pre_parts = P.max_pre_parts;
+    // The two passes run one after the other: the shared-prefix kernel's
+    // footprint (two waves per SIMD) leaves no room to overlap them.
     HIP_TRY(ltkv::launch_mq_attention(g, m, c->stream), "shared-prefix attention launch");
   }
   HIP_TRY(ltkv::launch_decode_attention(g, a, c->stream), "decode attention launch");

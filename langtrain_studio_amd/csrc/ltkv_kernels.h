@@ -51,6 +51,7 @@ struct AttnArgs {
   const int32_t *pre_parts;
   const float *pre_o, *pre_ml;
   int max_pre_parts;
+  int waves;  // 1: single-wave work-groups (f16 x 128 only), else four
 };
 
 // Context tokens per attention partition when none is fixed: four
@@ -94,7 +95,7 @@ struct MqJob {
   int32_t kvh;
   int32_t pad;
 };
-constexpr int kMqRows = 128;  // query rows per work-group
+int mq_rows(int head_dim);  // query rows per work-group
 
 struct MqArgs {
   const void *k_layer, *v_layer;

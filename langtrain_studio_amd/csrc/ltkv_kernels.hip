@@ -617,8 +617,8 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-template <typename T, int HD, int G>
-__global__ void __launch_bounds__(256)
+template <typename T, int HD, int G, int NW>
+__global__ void __launch_bounds__(64 * NW)
 attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
               const int32_t *__restrict__ tables, int64_t table_stride,
               const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
@@ -644,7 +644,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
   const int64_t qi = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, rg = lane >> 4;
   const int n_heads = n_kv_heads * G;
 
@@ -839,7 +839,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   // Loads past the wave's last tile read nothing (extent 0).
   constexpr int STAGES = GP <= 4 ? 3 : 2;
   {
-    constexpr int W = kAttnWaves;
+    constexpr int W = NW;
     int b = b0 + wave;
     if (b < b1) {
       if constexpr (STAGES == 3) {
@@ -897,9 +897,35 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     }
   }
 
+  const int64_t qh0 = qi * n_heads + (int64_t)kvh * G;
+  const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
+  if constexpr (NW == 1) {
+    // One wave: the lanes of row group 0 hold the merged numerators.
+    if (rg == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        if (direct) {
+          const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
+          float *o = out + (qh0 + h) * HD + c * E;
+#pragma unroll
+          for (int e = 0; e < E; ++e) o[e] = l[h] > 0.f ? acc[h][e] * inv : 0.f;
+        } else {
+          const int64_t pi = (qh0 + h) * max_parts + part;
+#pragma unroll
+          for (int e = 0; e < E; ++e) part_o[pi * HD + c * E + e] = acc[h][e];
+          if (c == 0) {
+            part_ml[2 * pi] = m[h];
+            part_ml[2 * pi + 1] = l[h];
+          }
+        }
+      }
+    }
+    return;
+  }
+
   // Merge the waves through LDS.
-  __shared__ float sm_acc[kAttnWaves][G][HD];
-  __shared__ float sm_m[kAttnWaves][G], sm_l[kAttnWaves][G];
+  __shared__ float sm_acc[NW][G][HD];
+  __shared__ float sm_m[NW][G], sm_l[NW][G];
   if (rg == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -912,21 +938,20 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     }
   }
   __syncthreads();
-  const int64_t qh0 = qi * n_heads + (int64_t)kvh * G;
-  for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
+  for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW) {
     const int h = idx / HD, d = idx - h * HD;
     float mx = sm_m[0][h];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
+    for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
     const float mref = mx == -INFINITY ? 0.f : mx;
     float lsum = 0.f, o = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float a = __builtin_amdgcn_exp2f(sm_m[w][h] - mref);
       lsum += sm_l[w][h] * a;
       o += sm_acc[w][h][d] * a;
     }
-    if (np == 1 && !(pre_parts && pre_parts[qi] > 0)) {  // else merged with prefix partials
+    if (direct) {
       out[(qh0 + h) * HD + d] = lsum > 0.f ? o / lsum : 0.f;
     } else {
       const int64_t pi = (qh0 + h) * max_parts + part;
@@ -942,7 +967,18 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 template <typename T, int HD, int G>
 hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
-  attn16_kernel<T, HD, G><<<grid, 256, 0, s>>>(
+  // Single-wave work-groups (short per-query contexts) exist for f16 x 128.
+  if constexpr (std::is_same_v<T, _Float16> && HD == 128) {
+    if (a.waves == 1) {
+      attn16_kernel<T, HD, G, 1><<<grid, 64, 0, s>>>(
+          static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
+          a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
+          g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens,
+          a.max_parts, a.pre_parts);
+      return launch_merge<HD>(a, s);
+    }
+  }
+  attn16_kernel<T, HD, G, kAttnWaves><<<grid, 64 * kAttnWaves, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
@@ -1006,7 +1042,9 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 // token range, folded into each member's output by attn_merge_kernel.
 //
 // Work-group: 4 waves x 32 rows (two 16-row tiles per wave); K and V are
-// staged 32 tokens at a time through double-buffered LDS.
+// staged 32 tokens at a time through double-buffered LDS. MFMA and VALU
+// instructions of the waves of a SIMD do not overlap on this chip, so the
+// kernel keeps the VALU count per score low rather than interleaving.
 // Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, j = 0..7, i = 0..3):
 // A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16], D[4 (l / 16) + i][l % 16].
 // ds_read_b64_tr_b16 within each 16-lane group: lane i, element j is element
@@ -1018,7 +1056,8 @@ typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) hf4 lds_hf4;
 typedef __attribute__((address_space(3))) char lds_char;
 
-constexpr int kMqChunk = 32;  // tokens per staging step
+constexpr int kMqChunk = 32;       // tokens per staging step
+constexpr float kMqSlack = 8.f;    // log2 headroom of the softmax reference
 
 __device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
 #pragma unroll
@@ -1033,8 +1072,10 @@ __device__ __forceinline__ hf4 lds_read_tr(const char *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4 *)(lds_char *)p);
 }
 
+constexpr int kMqWaves = 4;  // waves per work-group
+
 template <int HD>
-__global__ void __launch_bounds__(256, 2)  // two waves per SIMD: at most 256 registers
+__global__ void __launch_bounds__(64 * kMqWaves, 2)  // two waves per SIMD: at most 256 registers
 mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool,
                const float *__restrict__ q, const int32_t *__restrict__ tables,
                const MqJob *__restrict__ jobs, int n_jobs, const int32_t *__restrict__ members,
@@ -1045,8 +1086,10 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   constexpr int DT = HD / 16;                // 16-wide d tiles of the output
   constexpr int ROWB = HD * 2 + 16;          // LDS bytes per staged row (pad: no bank conflicts)
   constexpr int VPR = HD / 8;                // 16-byte vectors per row
-  constexpr int NPT = kMqChunk * VPR / 256;  // vectors per thread per chunk, K and V each
-  static_assert(NPT >= 1 && kMqChunk * VPR % 256 == 0, "chunk must split over 256 threads");
+  constexpr int NT = 64 * kMqWaves;     // threads
+  constexpr int NPT = kMqChunk * VPR / NT;   // vectors per thread per chunk, K and V each
+  static_assert(NPT >= 1 && kMqChunk * VPR % NT == 0, "chunk must split over the threads");
+  static_assert(64 / VPR <= 16, "a wave's rows of a chunk must lie in one block");
   __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V]
 
   // Work-group b runs on XCD b % 8. Each XCD takes a contiguous run of the
@@ -1102,98 +1145,155 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   // run; tokens at or past t1 stage as zeros.
   const int32_t *tab = tables + jb.table;
   const int64_t head_off = (int64_t)jb.kvh * HD;
+  // Chunks start on block boundaries (t0 % 32 == 0) and a wave's share of a
+  // chunk lies in one block. The job's block ids (at most 64) sit one per
+  // lane and are read with readlane; K/V rows go through buffer descriptors
+  // whose extent ends at t1, so rows past it load as zeros with no branch.
+  const int jb0 = jb.t0 >> 4;
+  const int jb1 = (jb.t1 + 15) >> 4;  // jb1 - jb0 <= 64
+  int32_t my_blk = jb0 + lane < jb1 ? tab[jb0 + lane] : -1;
+  if (my_blk >= n_blocks) my_blk = -1;
+  const uint32_t row_bytes = (uint32_t)(slot_stride * 2);
   auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT]) {
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
-      const int idx = threadIdx.x + 256 * u;
+      const int idx = threadIdx.x + NT * u;
       const int row = idx / VPR, col = idx - row * VPR;
-      const int tok = c0 + row;
-      kr[u] = u32x4{0u, 0u, 0u, 0u};
-      vr[u] = kr[u];
-      if (tok < jb.t1) {
-        const int32_t blk = tab[tok >> 4];
-        if (blk >= 0 && blk < n_blocks) {
-          const int64_t off = (int64_t)blk * block_stride + (tok & 15) * slot_stride + head_off + col * 8;
-          kr[u] = *reinterpret_cast<const u32x4 *>(kpool + off);
-          vr[u] = *reinterpret_cast<const u32x4 *>(vpool + off);
-        }
-      }
+      const int wrow = __builtin_amdgcn_readfirstlane(row);  // first row of this wave's share
+      const int bi = (c0 + wrow) >> 4;
+      const int rel = bi - jb0 < 63 ? bi - jb0 : 63;
+      const int32_t blk = __builtin_amdgcn_readlane(my_blk, rel);
+      const int valid = jb.t1 - bi * 16;  // rows of the block inside the range
+      const int extent = blk < 0 || valid <= 0 ? 0
+                         : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * 2;
+      const int64_t base = (int64_t)(blk < 0 ? 0 : blk) * block_stride + head_off;
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void *)(kpool + base), (short)0, extent, kBufferWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc((void *)(vpool + base), (short)0, extent, kBufferWord3);
+      const uint32_t voff = (uint32_t)((c0 + row) & 15) * row_bytes + (uint32_t)col * 16;
+      kr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
+      vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
     }
   };
   auto store_chunk = [&](int st, const u32x4 (&kr)[NPT], const u32x4 (&vr)[NPT]) {
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
-      const int idx = threadIdx.x + 256 * u;
+      const int idx = threadIdx.x + NT * u;
       const int row = idx / VPR, col = idx - row * VPR;
       *reinterpret_cast<u32x4 *>(&sm[st][0][row * ROWB + col * 16]) = kr[u];
       *reinterpret_cast<u32x4 *>(&sm[st][1][row * ROWB + col * 16]) = vr[u];
     }
   };
 
+  // Chunks wholly inside every valid row's visible range need no masking
+  // (rows past n_members are never stored and need none).
+  int lim_min = jb.t1;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+    if (slot[rt] >= 0) lim_min = limit[rt] < lim_min ? limit[rt] : lim_min;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int other = __shfl_xor(lim_min, off);
+    lim_min = other < lim_min ? other : lim_min;
+  }
+
+  // Softmax reference per row: p = 2^(s - m_ref) with s <= m_ref + kMqSlack,
+  // so p <= 2^kMqSlack (exact in the f16 hi/lo split). The reference is
+  // raised (and the accumulators rescaled) only when a score exceeds it by
+  // more than the slack, which after the first chunk is rare; the fast path
+  // needs no cross-lane exchange.
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   f32x4 o[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int st, int c0) {
+  // Scores of 32 tokens (two 16-token tiles) x this wave's 32 rows, from the
+  // K rows of LDS stage st. Consecutive MFMAs go to different accumulators.
+  auto score = [&](int st, f32x4 (&sc)[2][2]) {
     const char *ks_base = sm[st][0];
-    const char *vs_base = sm[st][1];
-    // Scores of 32 tokens (two 16-token tiles) x 32 rows.
-    f32x4 sc[2][2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) sc[tt][0] = sc[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      h8 a[2];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const h8 a = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWB + (32 * ks + 8 * lq) * 2);
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], sc[tt][rt], 0, 0, 0);
-          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], sc[tt][rt], 0, 0, 0);
-        }
-      }
-    }
-    // Online softmax per row. This lane holds tokens 4 lq + i and 16 + 4 lq + i
-    // of its row; k slot j of the P^T operand is token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4.
-    h8 ph[2], pl[2];
-    float alpha[2];
-    bool grew = false;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int lim = (jb.t1 < limit[rt] ? jb.t1 : limit[rt]) - c0;  // visible tokens of the chunk
-      float x[8];
+      for (int tt = 0; tt < 2; ++tt)
+        a[tt] = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWB + (32 * ks + 8 * lq) * 2);
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          x[tt * 4 + i] = tt * 16 + 4 * lq + i < lim ? sc[tt][rt][i] : -INFINITY;
-      float mx = x[0];
+        for (int rt = 0; rt < 2; ++rt)
+          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], sc[tt][rt], 0, 0, 0);
 #pragma unroll
-      for (int k = 1; k < 8; ++k) mx = __builtin_fmaxf(mx, x[k]);
-      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
-      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = __builtin_fmaxf(m_run[rt], mx);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - mref);
-      grew |= mn > m_run[rt];
-      m_run[rt] = mn;
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
+    }
+  };
+
+  // Online softmax of one chunk's scores into the P^T operands. This lane
+  // holds tokens 4 lq + i and 16 + 4 lq + i of its row; k slot j of P^T is
+  // token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4.
+  auto softmax = [&](f32x4 (&sc)[2][2], int c0, h8 (&ph)[2], h8 (&pl)[2]) {
+    float lmax[2];
+    if (c0 + kMqChunk > lim_min) {  // wave-uniform: the chunk crosses a row's limit
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int lim = (jb.t1 < limit[rt] ? jb.t1 : limit[rt]) - c0;  // visible tokens of the chunk
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tt * 16 + 4 * lq + i >= lim) sc[tt][rt][i] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      lmax[rt] = sc[0][rt][0];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lmax[rt] = __builtin_fmaxf(lmax[rt], sc[tt][rt][i]);
+    }
+    const bool over = lmax[0] > m_run[0] + kMqSlack || lmax[1] > m_run[1] + kMqSlack;
+    if (__builtin_amdgcn_ballot_w64(over)) {
+      // Raise the reference of the rows some lane found above it; the row
+      // max is exchanged over the row's four lanes, so the decision and the
+      // new reference are the same in all of them.
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        float mx = lmax[rt];
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+        const bool raise = mx > m_run[rt] + kMqSlack;
+        const float alpha = raise ? __builtin_amdgcn_exp2f(m_run[rt] - mx) : 1.f;
+        m_run[rt] = raise ? mx : m_run[rt];
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
       float p[8], ps = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        p[k] = __builtin_amdgcn_exp2f(x[k] - mref);
-        ps += p[k];
-      }
-      l_run[rt] = l_run[rt] * alpha[rt] + ps;
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[tt * 4 + i] = __builtin_amdgcn_exp2f(sc[tt][rt][i] - mref);
+          ps += p[tt * 4 + i];
+        }
+      l_run[rt] += ps;
       split_hl(p, ph[rt], pl[rt]);
     }
-    if (__builtin_amdgcn_ballot_w64(grew)) {  // some row's max grew: rescale (the row is lr)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        o[dt][0] *= alpha[0];
-        o[dt][1] *= alpha[1];
-      }
-    }
+  };
+
+  // O^T += V^T P^T over the V rows of LDS stage st.
+  auto pv = [&](int st, const h8 (&ph)[2], const h8 (&pl)[2]) {
+    const char *vs_base = sm[st][1];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       // V^T operand: d = 16 dt + lr, tokens 4 lq + j (j < 4) and 16 + 4 lq + j - 4.
@@ -1202,10 +1302,11 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
       const u32x2 a1 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (16 + 4 * lq + (lr >> 2)) * ROWB + col));
       const h8 a = __builtin_bit_cast(h8, u32x4{a0.x, a0.y, a1.x, a1.y});
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < 2; ++rt)
         o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph[rt], o[dt][rt], 0, 0, 0);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
         o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl[rt], o[dt][rt], 0, 0, 0);
-      }
     }
   };
 
@@ -1219,7 +1320,13 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   for (int c = 0; c < nch; ++c) {
     const bool more = c + 1 < nch;
     if (more) load_chunk(jb.t0 + (c + 1) * kMqChunk, kr, vr);
-    if (active) compute(c & 1, jb.t0 + c * kMqChunk);
+    if (active) {
+      f32x4 sc[2][2];
+      score(c & 1, sc);
+      h8 ph[2], pl[2];
+      softmax(sc, jb.t0 + c * kMqChunk, ph, pl);
+      pv(c & 1, ph, pl);
+    }
     if (more) store_chunk((c + 1) & 1, kr, vr);
     __syncthreads();
   }
@@ -1320,8 +1427,10 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
   return hipErrorInvalidValue;
 }
 
+int mq_rows(int) { return 32 * kMqWaves; }
+
 bool mq_supported(int elem, int head_dim, int group) {
-  return elem == 2 && (head_dim == 64 || head_dim == 128) && group >= 1 && group <= kMqRows;
+  return elem == 2 && (head_dim == 64 || head_dim == 128) && group >= 1 && group <= mq_rows(head_dim);
 }
 
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s) {
@@ -1332,11 +1441,11 @@ hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s
   const auto *v = static_cast<const _Float16 *>(a.v_layer);
   const float qscale = a.scale * kLog2e;
   if (a.head_dim == 128)
-    mq_attn_kernel<128><<<grid, 256, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
+    mq_attn_kernel<128><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
                                              a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
                                              g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
   else if (a.head_dim == 64)
-    mq_attn_kernel<64><<<grid, 256, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
+    mq_attn_kernel<64><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
                                             a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
                                             g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
   else
