@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "paged decode attn µs/step + KV append GB/s (% of HBM roofline), 1 GPU"
 PEAK_HBM_GBPS = 8000.0
+PEAK_F16_MFMA_TFLOPS = 2500.0  # dense
 BLOCK = 16
 
 
@@ -46,7 +47,7 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed"],
+                            "mixed", "prefill"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -349,6 +350,57 @@ def bench_tinyllama(args):
           flush=True)
 
 
+def bench_prefill(args):
+    """Chunked-prefill attention at the Qwen2.5-7B layer shape (28 q heads, 4
+    kv heads, head_dim 128, f16): 8 sequences with contexts U[512, 8192]
+    each append a 512-token chunk, and every chunk token attends to its own
+    prefix (causal within the chunk). Planned attention makes each chunk one
+    causal group on the matrix cores; the per-query decode kernel on the same
+    4096 queries is timed beside it. Flops count 4 * q_heads * head_dim per
+    (query token, visible token) pair, QK and PV, once."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_heads, n_kv, hd, n_seq, chunk = 28, 4, 128, 8, 512
+    kvd = n_kv * hd
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(512, 8193, n_seq)
+    n_blocks = int(sum(-(-int(c + chunk) // BLOCK) for c in ctx) * 1.1) + 16
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(n_blocks))
+    _fill_pool_random(kv, kvd, n_blocks, args.seed)
+    kv.append_batch(np.repeat(np.arange(n_seq, dtype=np.uint32), ctx),
+                    np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx]))
+    seqs = np.repeat(np.arange(n_seq, dtype=np.uint32), chunk)
+    pos = np.concatenate([np.arange(int(c), int(c) + chunk, dtype=np.uint64) for c in ctx])
+    sm = torch.from_numpy(kv.append_batch(seqs, pos)).cuda()
+    kn = torch.randn((seqs.size, kvd), device="cuda")
+    kv.write_batch(0, sm, kn, kn)
+    lens = (pos + 1).astype(np.int64)
+    q = torch.randn((seqs.size, n_heads * hd), device="cuda")
+    out = torch.empty_like(q)
+    t0 = time.perf_counter()
+    stats = kv.plan_attention(seqs, lens, n_heads, hd, shared_prefix=True)
+    plan_us = (time.perf_counter() - t0) * 1e6
+    reps = max(args.steps, 10)
+    p_us = _time_op(lambda: kv.planned_attention(0, q, out=out), reps=reps)
+    tables = torch.from_numpy(kv.block_tables(seqs)).cuda()
+    d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
+    d_us = _time_op(lambda: kv.decode_attention(0, q, tables, d_lens, n_heads, hd, out=out), reps=reps)
+    flops = 4.0 * n_heads * hd * float(lens.sum())
+    kv_bytes = int(sum(int(c) + chunk for c in ctx)) * 2 * kvd * 2  # K and V of each context once
+    print(json.dumps({
+        "workload": "prefill qwen2.5-7b f16: 8 chunks x 512 tokens, contexts U[512,8192]",
+        "attention_us": round(p_us, 2), "TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 1),
+        "mfma_frac": round(flops / (p_us * 1e-6) / 1e12 / PEAK_F16_MFMA_TFLOPS, 4),
+        "kv_bytes": kv_bytes, "flops": flops,
+        "plan": {k: stats[k] for k in ("groups", "grouped", "shared_blocks", "prefix_workgroups")},
+        "plan_host_us": round(plan_us, 1),
+        "attention_per_query_us": round(d_us, 2),
+        "per_query_TFLOPs": round(flops / (d_us * 1e-6) / 1e12, 1)}), flush=True)
+
+
 def bench_prefix_cow(args):
     """Prefix sharing at the Llama-3-8B layer shape: 256 sequences hold a
     4088-token prefix (256 blocks, the last holding 8 tokens, refcount 256);
@@ -534,7 +586,7 @@ def main():
     args = _args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                          "(the path shards by sequence across GPUs with no exchange, see DESIGN.md)"}))
+                          "(the path shards by sequence across GPUs with no exchange)"}))
         sys.exit(2)
     import torch
 
@@ -542,7 +594,8 @@ def main():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
     extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
-             "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed}
+             "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
+             "prefill": bench_prefill}
     if args.workload in extra:
         extra[args.workload](args)
         return

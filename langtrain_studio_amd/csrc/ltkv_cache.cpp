@@ -56,9 +56,10 @@ struct Seq {
 };
 
 // Step descriptor of ltkv_plan_attention: host-built tables, uploaded once.
-// Device arrays (int32, each 32-byte aligned inside one buffer): full tables
-// [n][stride], lens [n], suffix tables [n][sstride], suffix lens [n],
-// prefix partials per query [n], members [2 * n_members], jobs [n_jobs].
+// Device arrays (int32, each 32-byte aligned inside one buffer): one table
+// row per group [groups][gstride], the per-query pass's tables [n][sstride]
+// and lengths [n], group partials per query [n], members [2 * n_members],
+// jobs [n_jobs].
 struct AttnPlan {
   bool valid = false;
   uint64_t gen = 0;
@@ -66,7 +67,8 @@ struct AttnPlan {
   int max_pre_parts = 0, n_jobs = 0;
   int suffix_part = 0;  // partition tokens of the per-query pass when grouped
   uint64_t groups = 0, grouped = 0, shared_blocks = 0;
-  size_t off_tables = 0, off_lens = 0, off_stables = 0, off_slens = 0, off_pre = 0,
+  bool groups_only = false;  // every query completed by its group: no per-query pass
+  size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
   std::vector<int32_t> host;  // the arrays above, in device layout
   uint8_t *d = nullptr, *h = nullptr;  // device buffer, pinned staging
@@ -291,11 +293,56 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
 
 // Fewest shared full blocks and members for a prefix group.
 constexpr size_t kMinSharedBlocks = 2;
-// Tokens per shared-prefix partition are at least this (a multiple of the
-// kernel's 32-token staging step).
+// Tokens per group partition are at least this (a multiple of the kernel's
+// 32-token staging step).
 constexpr size_t kMinPrefixPart = 256;
 
 size_t align8(size_t x) { return (x + 7) / 8 * 8; }
+
+// Orders group jobs by work-group id. Work-group b runs on XCD b % 8 (each
+// XCD has its own L2): the jobs of one K/V range (adjacent in `jobs`, same
+// token range and kv head, different member tiles) go to one XCD, ranges are
+// spread over the XCDs longest first onto the least loaded one, and each
+// XCD runs its longest jobs first. Empty jobs pad the XCD queues.
+std::vector<ltkv::MqJob> place_jobs(const std::vector<ltkv::MqJob> &jobs) {
+  constexpr int kXcds = 8;
+  struct Range {
+    size_t first, count;
+    uint64_t work;
+  };
+  std::vector<Range> ranges;
+  for (size_t i = 0; i < jobs.size(); ++i) {
+    const ltkv::MqJob &j = jobs[i];
+    const uint64_t w = (uint64_t)(j.t1 - j.t0);
+    if (!ranges.empty()) {
+      const ltkv::MqJob &f = jobs[ranges.back().first];
+      if (f.table == j.table && f.t0 == j.t0 && f.kvh == j.kvh) {
+        ranges.back().count++;
+        ranges.back().work += w;
+        continue;
+      }
+    }
+    ranges.push_back({i, 1, w});
+  }
+  std::stable_sort(ranges.begin(), ranges.end(), [](const Range &a, const Range &b) { return a.work > b.work; });
+  std::vector<std::vector<ltkv::MqJob>> queue(kXcds);
+  std::vector<uint64_t> load(kXcds, 0);
+  for (const Range &r : ranges) {
+    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    for (size_t k = 0; k < r.count; ++k) queue[x].push_back(jobs[r.first + k]);
+    load[x] += r.work;
+  }
+  size_t depth = 0;
+  for (auto &q : queue) {
+    std::stable_sort(q.begin(), q.end(),
+                     [](const ltkv::MqJob &a, const ltkv::MqJob &b) { return a.t1 - a.t0 > b.t1 - b.t0; });
+    depth = std::max(depth, q.size());
+  }
+  std::vector<ltkv::MqJob> out(depth * kXcds);  // zero-initialised: empty jobs
+  for (int x = 0; x < kXcds; ++x)
+    for (size_t k = 0; k < queue[x].size(); ++k) out[k * kXcds + x] = queue[x][k];
+  return out;
+}
 
 // Builds the plan's host arrays: tables, prefix groups, suffix tables, jobs.
 int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *lens, size_t n_heads,
@@ -313,21 +360,55 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     stride = std::max<size_t>(stride, (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK);
   }
 
-  // Prefix groups: queries bucketed by their first block; in a bucket, the
-  // member set and shared length (common leading full blocks) that save the
-  // most block reads, (members - 1) * blocks.
+  // Groups whose rows attend to a common token range [0, tokens) of one
+  // block table together, each row up to its own limit:
+  //  * causal groups: several queries of one sequence (the tokens of a
+  //    prefill chunk); the range is the longest query's context and each
+  //    query is masked at its own length (model.rs:435-475 over all tokens);
+  //  * prefix groups: the rest, bucketed by first block; in a bucket, the
+  //    member set and shared length (common leading full blocks) that save
+  //    the most block reads, (members - 1) * blocks; each member reads the
+  //    rest of its context in the per-query pass.
   struct Group {
     std::vector<int32_t> members;
-    size_t blocks;
+    size_t tokens;
+    int32_t table_query;  // a member whose table covers the range
   };
   std::vector<Group> groups;
-  std::vector<size_t> pre_blocks(n, 0);
+  std::vector<size_t> pre_tokens(n, 0);  // context of query i covered by its group
   const size_t n_kv_heads = c->kv_dim / head_dim;
   if ((flags & LTKV_PLAN_SHARED_PREFIX) && ltkv::mq_supported((int)c->elem, (int)head_dim, (int)group)) {
+    std::vector<char> taken(n, 0);
+    {
+      std::unordered_map<uint32_t, size_t> seq_of;
+      std::vector<std::vector<int32_t>> by_seq;
+      for (size_t i = 0; i < n; ++i) {
+        if (lens[i] == 0) continue;
+        auto ins = seq_of.emplace(seqs[i], by_seq.size());
+        if (ins.second) by_seq.emplace_back();
+        by_seq[ins.first->second].push_back((int32_t)i);
+      }
+      for (auto &b : by_seq) {
+        if (b.size() < 2) continue;
+        Group gr;
+        gr.table_query = b[0];
+        for (int32_t m : b)
+          if (lens[m] > lens[gr.table_query]) gr.table_query = m;
+        gr.tokens = lens[gr.table_query];
+        if (gr.tokens < kMinSharedBlocks * LTKV_BLOCK) continue;
+        std::stable_sort(b.begin(), b.end(), [&](int32_t x, int32_t y) { return lens[x] < lens[y]; });
+        gr.members = b;
+        for (int32_t m : b) {
+          taken[m] = 1;
+          pre_tokens[m] = lens[m];
+        }
+        groups.push_back(std::move(gr));
+      }
+    }
     std::unordered_map<int32_t, size_t> bucket_of;
     std::vector<std::vector<int32_t>> buckets;
     for (size_t i = 0; i < n; ++i) {
-      if (lens[i] / LTKV_BLOCK < kMinSharedBlocks) continue;
+      if (taken[i] || lens[i] / LTKV_BLOCK < kMinSharedBlocks) continue;
       auto ins = bucket_of.emplace(sq[i]->blocks[0], buckets.size());
       if (ins.second) buckets.emplace_back();
       buckets[ins.first->second].push_back((int32_t)i);
@@ -357,17 +438,21 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
       }
       if (best_count < 2) continue;
       Group gr;
-      gr.blocks = lcp[best_count - 1].first;
+      gr.tokens = lcp[best_count - 1].first * LTKV_BLOCK;
       for (size_t k = 0; k < best_count; ++k) gr.members.push_back(lcp[k].second);
       std::sort(gr.members.begin(), gr.members.end());
-      for (int32_t m : gr.members) pre_blocks[m] = gr.blocks;
+      gr.table_query = gr.members[0];
+      for (int32_t m : gr.members) pre_tokens[m] = gr.tokens;
       groups.push_back(std::move(gr));
     }
   }
 
-  // Shared-prefix jobs: member tiles of mq_rows query rows; each group's
-  // prefix is split into partitions so the launch has about two waves per
-  // SIMD.
+  // Group jobs: member tiles of mq_rows query rows; each group's range is
+  // split into partitions so the launch has about two waves per SIMD. A job
+  // is skipped when every row of its tile ends before its partition starts;
+  // a member has partials for the partitions that start below its limit.
+  // With one partition, a tile whose members read nothing else writes their
+  // outputs itself (pre_parts -1: no per-query pass, no merge).
   const size_t per_job = (size_t)ltkv::mq_rows((int)head_dim) / group;  // members per work-group
   size_t units = 0;
   for (const auto &gr : groups) units += (gr.members.size() + per_job - 1) / per_job * n_kv_heads;
@@ -378,49 +463,79 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   std::vector<int32_t> pre_parts(n, 0);
   int max_pre_parts = 0;
   uint64_t shared_blocks = 0, grouped = 0;
-  for (const auto &gr : groups) {
-    const size_t tokens = gr.blocks * LTKV_BLOCK;
+  size_t gstride = 1;
+  for (const auto &gr : groups) gstride = std::max<size_t>(gstride, (gr.tokens + LTKV_BLOCK - 1) / LTKV_BLOCK);
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const Group &gr = groups[gi];
+    const size_t tokens = gr.tokens;
     const size_t max_split = std::max<size_t>(1, tokens / kMinPrefixPart);
     const size_t split = std::min(max_split, std::max<size_t>(1, (target + units - 1) / units));
     const size_t pt = ((tokens + split - 1) / split + 31) / 32 * 32;
     const size_t parts = (tokens + pt - 1) / pt;
     const size_t m0 = members.size() / 2;
     for (int32_t m : gr.members) {
+      const size_t limit = std::min<size_t>(lens[m], tokens);
       members.push_back(m);
-      members.push_back((int32_t)tokens);
-      pre_parts[m] = (int32_t)parts;
+      members.push_back((int32_t)limit);
+      pre_parts[m] = (int32_t)((limit + pt - 1) / pt);
     }
     const size_t tiles = (gr.members.size() + per_job - 1) / per_job;
+    std::vector<char> direct(tiles, 0);
+    if (parts == 1) {
+      for (size_t t = 0; t < tiles; ++t) {
+        const size_t first = t * per_job, count = std::min(per_job, gr.members.size() - first);
+        bool alone = true;
+        for (size_t k = first; k < first + count; ++k)
+          alone = alone && pre_tokens[gr.members[k]] >= lens[gr.members[k]];
+        direct[t] = alone;
+        if (alone)
+          for (size_t k = first; k < first + count; ++k) pre_parts[gr.members[k]] = -1;
+      }
+    }
     for (size_t p = 0; p < parts; ++p)
       for (size_t h = 0; h < n_kv_heads; ++h)
         for (size_t t = 0; t < tiles; ++t) {
+          const size_t first = t * per_job, count = std::min(per_job, gr.members.size() - first);
+          size_t top = 0;  // highest limit in the tile
+          for (size_t k = first; k < first + count; ++k)
+            top = std::max<size_t>(top, members[2 * (m0 + k) + 1]);
+          if (top <= p * pt) continue;
           ltkv::MqJob j{};
-          j.table = (int32_t)((size_t)gr.members[0] * stride);
+          j.table = (int32_t)(gi * gstride);
           j.t0 = (int32_t)(p * pt);
-          j.t1 = (int32_t)std::min(tokens, (p + 1) * pt);
-          j.member0 = (int32_t)(m0 + t * per_job);
-          j.n_members = (int32_t)std::min(per_job, gr.members.size() - t * per_job);
+          j.t1 = (int32_t)std::min(std::min(tokens, (p + 1) * pt), top);
+          j.member0 = (int32_t)(m0 + first);
+          j.n_members = (int32_t)count;
           j.part = (int32_t)p;
           j.kvh = (int32_t)h;
+          j.direct = direct[t];
           jobs.push_back(j);
         }
     max_pre_parts = std::max(max_pre_parts, (int)parts);
-    shared_blocks += gr.blocks;
+    shared_blocks += (tokens + LTKV_BLOCK - 1) / LTKV_BLOCK;
     grouped += gr.members.size();
   }
+  jobs = place_jobs(jobs);
 
   size_t sstride = 1;
   uint64_t suffix_tokens = 0;
+  // The per-query pass reads positions [pre_tokens, len): whole blocks after a
+  // prefix group's range, nothing after a causal group's.
+  std::vector<size_t> pre_blocks(n, 0);
   for (size_t i = 0; i < n; ++i) {
-    sstride = std::max<size_t>(sstride, (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK - pre_blocks[i]);
-    suffix_tokens += lens[i] - pre_blocks[i] * LTKV_BLOCK;
+    const size_t nb = (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK;
+    pre_blocks[i] = pre_tokens[i] >= lens[i] ? nb : pre_tokens[i] / LTKV_BLOCK;
+    sstride = std::max<size_t>(sstride, nb - pre_blocks[i]);
+    suffix_tokens += lens[i] - pre_tokens[i];
   }
   // With groups the per-query pass covers the (usually short) remainders:
   // single-wave work-groups, about eight per CU, whatever the batch.
   const uint64_t per_wg = suffix_tokens * n_kv_heads / (8 * (uint64_t)c->device_count_cu) + 1;
   P.suffix_part = (int)std::min<uint64_t>(1024, std::max<uint64_t>(64, (per_wg + 63) / 64 * 64));
-  if ((uint64_t)n * std::max(stride, sstride) > (uint64_t)INT32_MAX / 2)
+  if ((uint64_t)n * sstride + (uint64_t)groups.size() * gstride > (uint64_t)INT32_MAX / 2)
     return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
+  bool groups_only = !groups.empty() && suffix_tokens == 0;
+  for (size_t i = 0; i < n && groups_only; ++i) groups_only = pre_parts[i] < 0;
 
   P.n = n;
   P.n_heads = n_heads;
@@ -432,9 +547,9 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.groups = groups.size();
   P.grouped = grouped;
   P.shared_blocks = shared_blocks;
+  P.groups_only = groups_only;
   P.off_tables = 0;
-  P.off_lens = align8(P.off_tables + n * stride);
-  P.off_stables = align8(P.off_lens + n);
+  P.off_stables = align8(P.off_tables + groups.size() * gstride);
   P.off_slens = align8(P.off_stables + n * sstride);
   P.off_pre = align8(P.off_slens + n);
   P.off_members = align8(P.off_pre + n);
@@ -443,14 +558,17 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.bytes = words * 4;
   P.host.assign(words, 0);
   int32_t *h = P.host.data();
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const std::vector<int32_t> &blocks = sq[groups[gi].table_query]->blocks;
+    const size_t nb = (groups[gi].tokens + LTKV_BLOCK - 1) / LTKV_BLOCK;
+    int32_t *row = h + P.off_tables + gi * gstride;
+    for (size_t k = 0; k < gstride; ++k) row[k] = k < nb ? blocks[k] : -1;
+  }
   for (size_t i = 0; i < n; ++i) {
     const size_t nb = (lens[i] + LTKV_BLOCK - 1) / LTKV_BLOCK;
-    int32_t *row = h + P.off_tables + i * stride;
     int32_t *srow = h + P.off_stables + i * sstride;
-    for (size_t k = 0; k < stride; ++k) row[k] = k < nb ? sq[i]->blocks[k] : -1;
     for (size_t k = 0; k < sstride; ++k) srow[k] = pre_blocks[i] + k < nb ? sq[i]->blocks[pre_blocks[i] + k] : -1;
-    h[P.off_lens + i] = (int32_t)lens[i];
-    h[P.off_slens + i] = (int32_t)(lens[i] - pre_blocks[i] * LTKV_BLOCK);
+    h[P.off_slens + i] = (int32_t)(lens[i] - pre_tokens[i]);
     h[P.off_pre + i] = pre_parts[i];
   }
   std::copy(members.begin(), members.end(), h + P.off_members);
@@ -859,6 +977,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
     m.members = d + P.off_members;
     m.pre_o = (float *)a.pre_o;
     m.pre_ml = (float *)a.pre_ml;
+    m.out = d_out;
     m.n_heads = (int)P.n_heads;
     m.n_kv_heads = a.n_kv_heads;
     m.head_dim = (int)P.head_dim;
@@ -867,6 +986,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
     // The two passes run one after the other: the shared-prefix kernel's
     // footprint (two waves per SIMD) leaves no room to overlap them.
     HIP_TRY(ltkv::launch_mq_attention(g, m, c->stream), "shared-prefix attention launch");
+    if (P.groups_only) return LTKV_OK;  // the groups wrote every output
   }
   HIP_TRY(ltkv::launch_decode_attention(g, a, c->stream), "decode attention launch");
   return LTKV_OK;

@@ -45,9 +45,10 @@ struct AttnArgs {
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int part_tokens, max_parts;  // part_tokens 0: per-query partition_tokens(len)
-  // Shared-prefix partials folded into each query's result (planned
-  // attention), or pre_parts == nullptr: query i has pre_parts[i] partials
-  // at pre_o/pre_ml slot (i * n_heads + head) * max_pre_parts + p.
+  // Group partials folded into each query's result (planned attention), or
+  // pre_parts == nullptr: query i has pre_parts[i] partials at pre_o/pre_ml
+  // slot (i * n_heads + head) * max_pre_parts + p; -1: its group wrote the
+  // output and nothing else reads its context.
   const int32_t *pre_parts;
   const float *pre_o, *pre_ml;
   int max_pre_parts;
@@ -93,7 +94,7 @@ struct MqJob {
   int32_t member0, n_members;  // members[2*member0 ...]: (query, token limit) pairs
   int32_t part;                // partial slot of this token range
   int32_t kvh;
-  int32_t pad;
+  int32_t direct;              // 1: the rows' only contribution; write the output
 };
 int mq_rows(int head_dim);  // query rows per work-group
 
@@ -105,6 +106,7 @@ struct MqArgs {
   int n_jobs;
   const int32_t *members;
   float *pre_o, *pre_ml;  // partial slots, laid out as AttnArgs::pre_o/pre_ml
+  float *out;             // outputs of direct jobs
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int max_pre_parts;

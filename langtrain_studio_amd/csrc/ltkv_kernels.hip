@@ -254,6 +254,9 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > table_stride * 16) len = table_stride * 16;
+  // A query with group partials and nothing else to read (or whose group
+  // wrote its output) has no work here.
+  if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
   const int pt = partition_tokens(len, part_tokens);
   const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;  // uniform over the work-group
@@ -458,9 +461,10 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   if (len > max_len) len = max_len;
   const int pt = partition_tokens(len, part_tokens);
   const int npre = pre_parts ? pre_parts[qi] : 0;
-  // With prefix partials the context kernels wrote partials even for a
-  // single partition; an empty context left an empty one (max -inf, sum 0).
-  const int np = npre > 0 ? (len > 0 ? (int)((len + pt - 1) / pt) : 1) : (int)((len + pt - 1) / pt);
+  if (npre < 0) return;  // its group wrote the output
+  // With group partials the context kernels wrote partials even for a
+  // single partition (none for an empty remainder).
+  const int np = (int)((len + pt - 1) / pt);
   if (np <= 1 && npre == 0) return;  // a single partition wrote its output directly
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
@@ -651,6 +655,9 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > table_stride * 16) len = table_stride * 16;
+  // A query with group partials and nothing else to read (or whose group
+  // wrote its output) has no work here.
+  if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
   const int pt = partition_tokens(len, part_tokens);
   const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;  // uniform over the work-group
@@ -1079,7 +1086,8 @@ __global__ void __launch_bounds__(64 * kMqWaves, 2)  // two waves per SIMD: at m
 mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool,
                const float *__restrict__ q, const int32_t *__restrict__ tables,
                const MqJob *__restrict__ jobs, int n_jobs, const int32_t *__restrict__ members,
-               float *__restrict__ pre_o, float *__restrict__ pre_ml, int n_heads, int group,
+               float *__restrict__ pre_o, float *__restrict__ pre_ml, float *__restrict__ out,
+               int n_heads, int group,
                int64_t n_blocks, int64_t block_stride, int64_t slot_stride, float qscale,
                int max_pre_parts) {
   constexpr int KS = HD / 32;                // k steps of the score product
@@ -1092,13 +1100,11 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   static_assert(64 / VPR <= 16, "a wave's rows of a chunk must lie in one block");
   __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V]
 
-  // Work-group b runs on XCD b % 8. Each XCD takes a contiguous run of the
-  // job list, in which the jobs of one token range (its member tiles) are
-  // adjacent, so their K/V reads are served by that XCD's L2.
-  const int per_xcd = (n_jobs + 7) / 8;
-  const int j = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (j >= n_jobs) return;
-  const MqJob jb = jobs[j];
+  // The job list is ordered by work-group id (XCD placement is the host's);
+  // empty jobs pad it.
+  if ((int)blockIdx.x >= n_jobs) return;
+  const MqJob jb = jobs[blockIdx.x];
+  if (jb.n_members <= 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lq = lane >> 4;
   const int rows = jb.n_members * group;
@@ -1108,7 +1114,7 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   // operand Q^T: 8 consecutive d of k step ks at d = 32 ks + 8 lq.
   h8 qh[2][KS], ql[2][KS];
   int limit[2];
-  int64_t slot[2];
+  int64_t slot[2], qrow[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int r = wave * 32 + rt * 16 + lr;
@@ -1119,11 +1125,13 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
       for (int e = 0; e < 8; ++e) x[ks][e] = 0.f;
     limit[rt] = 0;
     slot[rt] = -1;
+    qrow[rt] = 0;
     if (r < rows) {
       const int m = r / group, hh = r - m * group;
       const int qi = members[2 * (jb.member0 + m)];
       limit[rt] = members[2 * (jb.member0 + m) + 1];
       const int64_t qh_idx = (int64_t)qi * n_heads + (int64_t)jb.kvh * group + hh;
+      qrow[rt] = qh_idx;
       slot[rt] = qh_idx * max_pre_parts + jb.part;
       const float *qp = q + qh_idx * HD + 8 * lq;
 #pragma unroll
@@ -1146,13 +1154,9 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   const int32_t *tab = tables + jb.table;
   const int64_t head_off = (int64_t)jb.kvh * HD;
   // Chunks start on block boundaries (t0 % 32 == 0) and a wave's share of a
-  // chunk lies in one block. The job's block ids (at most 64) sit one per
-  // lane and are read with readlane; K/V rows go through buffer descriptors
-  // whose extent ends at t1, so rows past it load as zeros with no branch.
-  const int jb0 = jb.t0 >> 4;
-  const int jb1 = (jb.t1 + 15) >> 4;  // jb1 - jb0 <= 64
-  int32_t my_blk = jb0 + lane < jb1 ? tab[jb0 + lane] : -1;
-  if (my_blk >= n_blocks) my_blk = -1;
+  // chunk lies in one block, so its table entry is one scalar load. K/V
+  // rows go through buffer descriptors whose extent ends at t1: rows past it
+  // load as zeros with no branch.
   const uint32_t row_bytes = (uint32_t)(slot_stride * 2);
   auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT]) {
 #pragma unroll
@@ -1161,11 +1165,10 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
       const int row = idx / VPR, col = idx - row * VPR;
       const int wrow = __builtin_amdgcn_readfirstlane(row);  // first row of this wave's share
       const int bi = (c0 + wrow) >> 4;
-      const int rel = bi - jb0 < 63 ? bi - jb0 : 63;
-      const int32_t blk = __builtin_amdgcn_readlane(my_blk, rel);
       const int valid = jb.t1 - bi * 16;  // rows of the block inside the range
-      const int extent = blk < 0 || valid <= 0 ? 0
-                         : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * 2;
+      int32_t blk = valid > 0 ? tab[bi] : -1;
+      if (blk >= n_blocks) blk = -1;
+      const int extent = blk < 0 ? 0 : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * 2;
       const int64_t base = (int64_t)(blk < 0 ? 0 : blk) * block_stride + head_off;
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void *)(kpool + base), (short)0, extent, kBufferWord3);
@@ -1337,7 +1340,12 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
     float l = l_run[rt];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    if (slot[rt] >= 0) {
+    if (slot[rt] >= 0 && jb.direct) {  // the row's only contribution: normalised output
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      float *po = out + qrow[rt] * HD + 4 * lq;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(po + dt * 16) = o[dt][rt] * inv;
+    } else if (slot[rt] >= 0) {
       float *po = pre_o + slot[rt] * HD + 4 * lq;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(po + dt * 16) = o[dt][rt];
@@ -1435,18 +1443,18 @@ bool mq_supported(int elem, int head_dim, int group) {
 
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s) {
   if (a.n_jobs <= 0) return hipSuccess;
-  const unsigned grid = (unsigned)(8 * ((a.n_jobs + 7) / 8));
+  const unsigned grid = (unsigned)a.n_jobs;
   const int group = a.n_heads / a.n_kv_heads;
   const auto *k = static_cast<const _Float16 *>(a.k_layer);
   const auto *v = static_cast<const _Float16 *>(a.v_layer);
   const float qscale = a.scale * kLog2e;
   if (a.head_dim == 128)
     mq_attn_kernel<128><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
-                                             a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
+                                             a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks,
                                              g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
   else if (a.head_dim == 64)
     mq_attn_kernel<64><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
-                                            a.pre_o, a.pre_ml, a.n_heads, group, g.n_blocks,
+                                            a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks,
                                             g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
   else
     return hipErrorInvalidValue;

@@ -161,3 +161,62 @@ def test_f32_pools_plan_without_groups(gpu):
     ref = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
                              torch.from_numpy(la).to(gpu), 32, 64).cpu().numpy()
     np.testing.assert_array_equal(out, ref)
+
+
+# ---------------------------------------------------------------------------- chunked prefill
+def _prefill_state(rng, kv_dim, chunks, decode=()):
+    """chunks: (seq, context, chunk_len) -- the sequence holds `context`
+    tokens, then appends a chunk of chunk_len tokens (the step's prefill
+    chunk, model.rs:380-429); decode: (seq, len) sequences appending one token."""
+    need = sum(c + n + 32 for _, c, n in chunks) + sum(n + 32 for _, n in decode) + 64 * BLOCK
+    g, o = _caches(1, kv_dim, need, "f16", rng)
+    both = [("gpu", g), ("oracle", o)]
+    for s, ctx, _ in chunks:
+        if ctx:
+            append_rows(both, [s] * ctx, np.arange(ctx), rng, kv_dim)
+    if decode:
+        fill_sequences(both, dict(decode), rng, kv_dim)
+    seqs, pos = [], []
+    for s, ctx, n in chunks:
+        seqs += [s] * n
+        pos += list(range(ctx, ctx + n))
+    for s, n in decode:
+        seqs.append(s)
+        pos.append(n)
+    append_rows(both, seqs, pos, rng, kv_dim)
+    return g, o, seqs, [p + 1 for p in pos]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,head_dim,ctx,chunk", [
+    (28, 4, 128, 1000, 512),   # Qwen2.5-7B heads, a 512-token chunk after 1000 tokens
+    (32, 8, 128, 0, 300),      # the first chunk of a prompt
+    (32, 8, 128, 2047, 33),
+    (32, 4, 64, 700, 100),
+    (16, 2, 64, 64, 200),
+])
+def test_prefill_chunk_causal(gpu, n_heads, n_kv, head_dim, ctx, chunk):
+    """Every token of a prefill chunk attends to its own prefix (causal
+    within the chunk) through one causal group on the matrix cores."""
+    rng = np.random.default_rng(ctx + chunk + head_dim)
+    g, o, seqs, lens = _prefill_state(rng, n_kv * head_dim, [(0, ctx, chunk)])
+    stats, *_ = _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng)
+    assert stats["groups"] == 1 and stats["grouped"] == chunk
+
+
+def test_mixed_step_prefill_decode_and_forks(gpu):
+    """A continuous-batching step: two prefill chunks, decode queries that
+    share nothing, and decode queries of forked sequences, in one plan."""
+    rng = np.random.default_rng(44)
+    kv_dim = 4 * 128
+    g, o, seqs, lens = _prefill_state(rng, kv_dim, [(0, 600, 128), (1, 0, 64)],
+                                      decode=[(5, 900), (6, 33), (7, 1500)])
+    both = [("gpu", g), ("oracle", o)]
+    append_rows(both, [20] * 400, np.arange(400), rng, kv_dim)
+    for child in (21, 22, 23):
+        g.share(20, child, 400)
+        o.share(20, child, 400)
+        append_rows(both, [child], [400], rng, kv_dim)
+    seqs = seqs + [21, 22, 23]
+    lens = lens + [401, 401, 401]
+    stats, *_ = _run(gpu, g, o, seqs, lens, 28, 128, rng)
+    assert stats["groups"] == 3 and stats["grouped"] == 128 + 64 + 3

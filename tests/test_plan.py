@@ -93,18 +93,36 @@ def test_short_prefixes_are_not_grouped():
     assert st["groups"] == 0
 
 
-def test_same_sequence_twice_and_partial_lengths():
-    """Queries may read a prefix of a sequence (lens below its length) and
-    the same sequence more than once (prefill tokens of one chunk)."""
+def test_queries_of_one_sequence_form_a_causal_group():
+    """Several queries of one sequence (the tokens of a prefill chunk, each
+    reading its own prefix) form one group over the longest one's context,
+    partial last block included; a lone query of a sequence does not."""
     c = _meta()
     _fill(c, 0, 0, 300)
-    seqs = [0, 0, 0]
-    lens = [300, 200, 37]
+    st = c.plan_attention([0, 0, 0], [300, 200, 37], 32, 128)
+    assert st["groups"] == 1 and st["grouped"] == 3 and st["shared_blocks"] == -(-300 // BLOCK)
+    _fill(c, 1, 0, 1000)
+    _fill(c, 1, 1000, 1064)  # a 64-token chunk after a 1000-token context
+    st = c.plan_attention([1] * 64 + [0], list(range(1001, 1065)) + [300], 32, 128)
+    assert st["groups"] == 1 and st["grouped"] == 64 and st["shared_blocks"] == -(-1064 // BLOCK)
+    st = c.plan_attention([1, 0], [1064, 300], 32, 128)
+    assert st["groups"] == 0
+    # too short a range to group; empty reads never join a group
+    st = c.plan_attention([0, 0, 0], [31, 20, 0], 32, 128)
+    assert st["groups"] == 0
+
+
+def test_causal_groups_and_prefix_groups_together():
+    """A prefill chunk of one sequence next to decode queries of forks of
+    another: one causal group and one prefix group."""
+    c = _meta()
+    _fork(c, 0, 500, [1, 2, 3], [2, 2, 2])
+    _fill(c, 9, 0, 700)
+    seqs = [9] * 32 + [1, 2, 3]
+    lens = list(range(669, 701)) + [c.len(1), c.len(2), c.len(3)]
     st = c.plan_attention(seqs, lens, 32, 128)
-    # (2 - 1) * 12 shared blocks beat (3 - 1) * 2
-    assert st["groups"] == 1 and st["grouped"] == 2 and st["shared_blocks"] == 200 // BLOCK
-    st = c.plan_attention(seqs, [300, 300, 300], 32, 128)
-    assert st["groups"] == 1 and st["grouped"] == 3 and st["shared_blocks"] == 300 // BLOCK
+    assert st["groups"] == 2 and st["grouped"] == 35
+    assert st["shared_blocks"] == -(-700 // BLOCK) + 500 // BLOCK
 
 
 def test_f32_pools_and_unsupported_groups_plan_without_prefix_groups():
