@@ -47,7 +47,7 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed", "prefill"],
+                            "mixed", "prefill", "rope-append"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -401,6 +401,42 @@ def bench_prefill(args):
         "per_query_TFLOPs": round(flops / (d_us * 1e-6) / 1e12, 1)}), flush=True)
 
 
+def bench_rope_append(args):
+    """Fused RoPE + append (model.rs:414-429 in one launch) at the Qwen2.5-7B
+    continuous-batching step: 4216 tokens (8 prefill chunks x 512 + 120 decode
+    tokens) at positions U[0, 8704), 28 q heads / 4 kv heads / 128, NeoX pairs;
+    and at the Llama-3-8B shape with 4096 tokens (interleaved pairs). Bytes per
+    token: K and V f32 read + f16 written, Q f32 read and written, slot and
+    position; the cos/sin table reads are not counted (cache-resident)."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    rng = np.random.default_rng(args.seed)
+    rows = []
+    for name, n_heads, n_kv, hd, n, neox, base in (("qwen2.5-7b", 28, 4, 128, 4216, True, 1e6),
+                                                     ("llama3-8b", 32, 8, 128, 4096, False, 5e5)):
+        kvd = n_kv * hd
+        n_blocks = n // BLOCK + 64
+        kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+        kv.init_free_order(rng.permutation(n_blocks))
+        kv.rope_init(base, hd, hd, neox, 8704)
+        sm = torch.from_numpy(kv.append_batch(np.zeros(n, np.uint32), np.arange(n, dtype=np.uint64))).cuda()
+        pos = torch.from_numpy(rng.integers(0, 8704, n).astype(np.int32)).cuda()
+        k = torch.randn((n, kvd), device="cuda")
+        v = torch.randn((n, kvd), device="cuda")
+        q = torch.randn((n, n_heads * hd), device="cuda")
+        fused = _time_op(lambda: kv.write_rope(0, sm, pos, k, v, q=q, n_heads=n_heads), reps=20)
+        plain = _time_op(lambda: kv.write_batch(0, sm, k, v), reps=20)
+        nbytes = n * (kvd * (4 + 2) * 2 + n_heads * hd * 8 + 8)
+        rows.append({"shape": f"{name}: {n} tokens, {n_heads}q/{n_kv}kv x {hd}, {'neox' if neox else 'interleaved'}",
+                     "fused_us": round(fused, 2), "bytes": nbytes,
+                     "GBps": round(nbytes / (fused * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (fused * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                     "append_only_us": round(plain, 2)})
+    print(json.dumps({"workload": "rope-append", "rows": rows}), flush=True)
+
+
 def bench_prefix_cow(args):
     """Prefix sharing at the Llama-3-8B layer shape: 256 sequences hold a
     4088-token prefix (256 blocks, the last holding 8 tokens, refcount 256);
@@ -516,6 +552,8 @@ def bench_mixed(args):
     rng = np.random.default_rng(args.seed)
     n_blocks = int((n_dec + n_pre) * 8192 // BLOCK * 1.1) + (n_dec + n_pre) * (steps // BLOCK + 2)
     kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    if args.partition:
+        kv.set_attention_partition(args.partition)
     kv.init_free_order(rng.permutation(n_blocks))
     _fill_pool_random(kv, kvd, n_blocks, args.seed)
     next_id = [0]
@@ -595,7 +633,7 @@ def main():
         sys.exit(1)
     extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
              "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
-             "prefill": bench_prefill}
+             "prefill": bench_prefill, "rope-append": bench_rope_append}
     if args.workload in extra:
         extra[args.workload](args)
         return

@@ -141,6 +141,23 @@ LTKV_API int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n
 LTKV_API int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
                const float *d_k, const float *d_v, size_t src_stride);
 
+/* RoPE of Model::rope (model.rs:291-308) with the table of model.rs:263-265:
+ * inv_freq[i] = base^(-2i / rope_dim), angle = pos * inv_freq[i], cos/sin by
+ * the host libm (as the reference), pairs (2i, 2i+1) or, with neox, (i, i +
+ * rope_dim/2); dimensions past rope_dim are not rotated. Builds the
+ * [max_positions][rope_dim/2] table in HBM for ltkv_write_rope. */
+LTKV_API int ltkv_rope_init(ltkv_cache *c, float base, size_t rope_dim, size_t head_dim, int neox,
+                   size_t max_positions);
+
+/* model.rs:414-429 in one launch: RoPE on each token's K (then written into
+ * its cell as ltkv_write does) and, when d_q is not null, on its Q rows
+ * ([n][q_stride], n_heads heads) in place; V appended unrotated. Tokens with
+ * a position outside the table are skipped (nothing written). Bit-identical
+ * to the reference's f32 rotation (no fused multiply-add) and f16 rounding. */
+LTKV_API int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+                    const int32_t *d_positions, const float *d_k, const float *d_v, size_t src_stride,
+                    float *d_q, size_t q_stride, size_t n_heads);
+
 /* Kernel 2, block copy: the copy-on-write body of kv.rs:99-110 (all layers,
  * K and V) for n pairs d_pairs[2i] = src block, d_pairs[2i+1] = dst block.
  * ltkv_append and ltkv_append_batch launch it themselves; exposed for bulk

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -117,6 +118,10 @@ struct ltkv_cache {
   uint8_t *ws = nullptr;
   size_t ws_bytes = 0;
   size_t attn_part_tokens = 0;  // 0 = automatic
+
+  // RoPE table (ltkv_rope_init): [max_pos][rope_dim / 2] of (cos, sin).
+  float *rope = nullptr;
+  ltkv::RopeGeom rope_geom{};
 
   // Bumped by every metadata change; a plan records the value it was built at.
   uint64_t gen = 0;
@@ -690,6 +695,7 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->h_pairs) (void)hipHostFree(c->h_pairs);
     if (c->d_pairs) (void)hipFree(c->d_pairs);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->rope) (void)hipFree(c->rope);
     if (c->plan.done) (void)hipEventDestroy(c->plan.done);
     if (c->plan.h) (void)hipHostFree(c->plan.h);
     if (c->plan.d) (void)hipFree(c->plan.d);
@@ -818,6 +824,74 @@ int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapp
   HIP_TRY(ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping, d_k,
                              d_v, (int64_t)n, (int64_t)src_stride, c->stream),
           "write launch");
+  return LTKV_OK;
+}
+
+int ltkv_rope_init(ltkv_cache *c, float base, size_t rope_dim, size_t head_dim, int neox,
+                   size_t max_positions) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (head_dim == 0 || head_dim % 8 != 0 || c->kv_dim % head_dim != 0)
+    return fail(LTKV_ERR_ARG, "head_dim %zu must be a multiple of 8 dividing kv_dim %zu", head_dim, c->kv_dim);
+  if (rope_dim == 0 || rope_dim % 8 != 0 || rope_dim > head_dim)
+    return fail(LTKV_ERR_ARG, "rope_dim %zu must be a multiple of 8 and at most head_dim", rope_dim);
+  if (max_positions == 0 || max_positions > (size_t)INT32_MAX / 2)
+    return fail(LTKV_ERR_ARG, "max_positions out of range");
+  if (!(base > 0.f)) return fail(LTKV_ERR_ARG, "rope base must be positive");
+  // model.rs:263-265 (inv_freq) and 296-297 (angle, sin_cos), with the same
+  // libm the reference calls (powf, sinf, cosf).
+  const size_t half = rope_dim / 2;
+  std::vector<float> inv(half);
+  for (size_t i = 0; i < half; ++i) inv[i] = powf(base, -2.0f * (float)i / (float)rope_dim);
+  std::vector<float> tab(max_positions * half * 2);
+  for (size_t p = 0; p < max_positions; ++p)
+    for (size_t i = 0; i < half; ++i) {
+      const float a = (float)p * inv[i];
+      tab[(p * half + i) * 2] = cosf(a);
+      tab[(p * half + i) * 2 + 1] = sinf(a);
+    }
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (c->rope) {  // enqueued appends may still read the old table
+    HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+    HIP_TRY(hipFree(c->rope), "hipFree(rope table)");
+    c->rope = nullptr;
+  }
+  HIP_TRY(hipMalloc((void **)&c->rope, tab.size() * sizeof(float)), "hipMalloc(rope table)");
+  HIP_TRY(hipMemcpy(c->rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice),
+          "hipMemcpy(rope table)");
+  c->rope_geom.table = c->rope;
+  c->rope_geom.max_pos = (int)max_positions;
+  c->rope_geom.rope_dim = (int)rope_dim;
+  c->rope_geom.head_dim = (int)head_dim;
+  c->rope_geom.neox = neox ? 1 : 0;
+  return LTKV_OK;
+}
+
+int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+                    const int32_t *d_positions, const float *d_k, const float *d_v, size_t src_stride,
+                    float *d_q, size_t q_stride, size_t n_heads) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (!c->rope) return fail(LTKV_ERR_ARG, "no RoPE table (ltkv_rope_init)");
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (n == 0) return LTKV_OK;
+  if (!d_slot_mapping || !d_positions || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (src_stride < c->kv_dim || src_stride % 4 != 0)
+    return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
+  const size_t hd = (size_t)c->rope_geom.head_dim;
+  if (d_q && (n_heads == 0 || q_stride < n_heads * hd || q_stride % 4 != 0))
+    return fail(LTKV_ERR_ARG, "q_stride must be >= n_heads * head_dim and a multiple of 4");
+  if (((uintptr_t)d_k | (uintptr_t)d_v | (uintptr_t)d_q) % 16 != 0)
+    return fail(LTKV_ERR_ARG, "K/V/Q rows must be 16-byte aligned");
+  const uint64_t per = c->kv_dim / 8 * 2 + (d_q ? n_heads * hd / 8 : 0);
+  if ((uint64_t)n * per >= (1ull << 32) - 256) return fail(LTKV_ERR_ARG, "too many rows for one launch");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  HIP_TRY(ltkv::launch_write_rope(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping,
+                                  d_positions, d_k, d_v, d_q, (int64_t)n, (int64_t)src_stride,
+                                  (int64_t)q_stride, (int)n_heads, c->rope_geom, c->stream),
+          "write_rope launch");
   return LTKV_OK;
 }
 

@@ -24,6 +24,19 @@ hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const i
                         const float *k, const float *v, int64_t n, int64_t src_stride,
                         hipStream_t s);
 
+// RoPE geometry: table [max_pos][rope_dim / 2] of (cos, sin) of pos * inv_freq[i].
+struct RopeGeom {
+  const float *table;
+  int max_pos, rope_dim, head_dim, neox;
+};
+
+// Kernel 1 with RoPE: K rotated into the pool, V appended, Q (optional,
+// [n][q_stride] with n_heads heads) rotated in place.
+hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
+                            const int32_t *positions, const float *k, const float *v, float *q,
+                            int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
+                            const RopeGeom &r, hipStream_t s);
+
 hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
                               const int32_t *pairs, int64_t n_pairs, hipStream_t s);
 

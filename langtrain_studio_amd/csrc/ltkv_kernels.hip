@@ -23,6 +23,7 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ----------------------------------------------------------------------------
 // f32 -> f16, IEEE round-to-nearest-even (the conversion of f16::from_f32).
@@ -84,6 +85,127 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
     kd[1] = k1;
     vd[0] = v0;
     vd[1] = v1;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 1 fused with RoPE (model.rs:291-308 then kv.rs:123-131): one launch
+// rotates Q in place and K on its way into the pool, and appends V. A thread
+// owns one unit of a head: 4 rotation pairs (8 elements: (2i, 2i+1) pairs
+// adjacent, or NeoX pairs (i, i + rope_dim/2) as 4 + 4) or 8 unrotated
+// elements past rope_dim. cos/sin come from the host-built table (the same
+// libm the reference calls), and the products are not contracted into FMAs
+// (rustc does not contract), so the results are bit-identical.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void rope_pairs(const float *__restrict__ cs, float (&x0)[4], float (&x1)[4]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float c = cs[2 * p], sn = cs[2 * p + 1];
+    const float a = x0[p], b = x1[p];
+    x0[p] = a * c - b * sn;
+    x1[p] = a * sn + b * c;
+  }
+}
+
+template <int ELEM>
+__global__ void __launch_bounds__(256)
+write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
+                  const int32_t *__restrict__ slots, const int32_t *__restrict__ positions,
+                  const float *__restrict__ k, const float *__restrict__ v, float *__restrict__ q,
+                  int64_t n, int64_t src_stride, int64_t q_stride, int kv_dim, int n_kv_heads,
+                  int n_heads, int64_t n_slots, const float *__restrict__ table, int max_pos,
+                  int rope_dim, int head_dim, int neox) {
+  const int upr = rope_dim >> 3;          // rotary units per head
+  const int uph = head_dim >> 3;          // units per head
+  const int ku = n_kv_heads * uph;        // K units per token
+  const int vu = kv_dim >> 3;             // V units per token
+  const int qu = q ? n_heads * uph : 0;   // Q units per token
+  const int per = ku + vu + qu;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / per;
+  if (row >= n) return;
+  int u = (int)(gid - row * per);
+  const int32_t pos = positions[row];
+  if (pos < 0 || pos >= max_pos) return;
+  const int32_t s = slots[row];
+  const bool cell = s >= 0 && (int64_t)s < n_slots;
+  if (u >= ku && u < ku + vu) {  // V: plain append of 8 elements
+    if (!cell) return;
+    const int col = (u - ku) << 3;
+    const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
+    const f32x4 v0 = vs[0], v1 = vs[1];
+    const int64_t dst = (int64_t)s * kv_dim + col;
+    if constexpr (ELEM == 2) {
+      u32x4 vo;
+      vo.x = pack_f16x2(v0.x, v0.y);
+      vo.y = pack_f16x2(v0.z, v0.w);
+      vo.z = pack_f16x2(v1.x, v1.y);
+      vo.w = pack_f16x2(v1.z, v1.w);
+      *reinterpret_cast<u32x4 *>(vpool + dst * 2) = vo;
+    } else {
+      f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
+      vd[0] = v0;
+      vd[1] = v1;
+    }
+    return;
+  }
+  const bool is_q = u >= ku + vu;
+  if (!is_q && !cell) return;
+  if (is_q) u -= ku + vu;
+  const int h = u / uph, w = u - h * uph;
+  const float *src = is_q ? q + row * q_stride : k + row * src_stride;
+  const int hb = h * head_dim;
+  // Element offsets (within the head) of the unit's two halves of 4.
+  int e0, e1;
+  if (w >= upr) {  // past rope_dim: unrotated
+    e0 = (upr << 3) + ((w - upr) << 3);
+    e1 = e0 + 4;
+  } else if (neox) {
+    e0 = w << 2;
+    e1 = e0 + (rope_dim >> 1);
+  } else {
+    e0 = w << 3;
+    e1 = e0 + 4;
+  }
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(src + hb + e0);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(src + hb + e1);
+  float o[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};  // elements e0..e0+3, e1..e1+3
+  if (w < upr) {
+    const float *cs = table + ((int64_t)pos * (rope_dim >> 1)) * 2;
+    if (neox) {  // pairs (e0 + p, e1 + p), pair index e0 + p
+      float x0[4] = {o[0], o[1], o[2], o[3]}, x1[4] = {o[4], o[5], o[6], o[7]};
+      rope_pairs(cs + 2 * e0, x0, x1);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        o[p] = x0[p];
+        o[4 + p] = x1[p];
+      }
+    } else {  // pairs (e0 + 2p, e0 + 2p + 1), pair index e0 / 2 + p
+      float x0[4] = {o[0], o[2], o[4], o[6]}, x1[4] = {o[1], o[3], o[5], o[7]};
+      rope_pairs(cs + e0, x0, x1);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        o[2 * p] = x0[p];
+        o[2 * p + 1] = x1[p];
+      }
+    }
+  }
+  if (is_q) {
+    float *qd = q + row * q_stride + hb;
+    *reinterpret_cast<f32x4 *>(qd + e0) = f32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<f32x4 *>(qd + e1) = f32x4{o[4], o[5], o[6], o[7]};
+    return;
+  }
+  const int64_t dst = (int64_t)s * kv_dim + hb;
+  if constexpr (ELEM == 2) {
+    uint16_t *kd = reinterpret_cast<uint16_t *>(kpool) + dst;
+    *reinterpret_cast<u32x2 *>(kd + e0) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+    *reinterpret_cast<u32x2 *>(kd + e1) = u32x2{pack_f16x2(o[4], o[5]), pack_f16x2(o[6], o[7])};
+  } else {
+    float *kd = reinterpret_cast<float *>(kpool) + dst;
+    *reinterpret_cast<f32x4 *>(kd + e0) = f32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<f32x4 *>(kd + e1) = f32x4{o[4], o[5], o[6], o[7]};
   }
 }
 
@@ -1058,7 +1180,6 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 // i % 4 of the 8 bytes addressed by lane 4 j + i / 4.
 // ----------------------------------------------------------------------------
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) hf4 lds_hf4;
 typedef __attribute__((address_space(3))) char lds_char;
@@ -1373,6 +1494,28 @@ hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const i
     write_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(
         static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n,
         src_stride, g.kv_dim, g.n_blocks * 16);
+  return hipGetLastError();
+}
+
+hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
+                            const int32_t *positions, const float *k, const float *v, float *q,
+                            int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
+                            const RopeGeom &r, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int uph = r.head_dim >> 3;
+  const int n_kv_heads = g.kv_dim / r.head_dim;
+  const int64_t per = (int64_t)n_kv_heads * uph + (g.kv_dim >> 3) + (q ? (int64_t)n_heads * uph : 0);
+  const int64_t blocks = (n * per + 255) / 256;
+  if (g.elem == 2)
+    write_rope_kernel<2><<<(unsigned)blocks, 256, 0, s>>>(
+        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, positions, k, v, q,
+        n, src_stride, q_stride, g.kv_dim, n_kv_heads, n_heads, g.n_blocks * 16, r.table, r.max_pos,
+        r.rope_dim, r.head_dim, r.neox);
+  else
+    write_rope_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(
+        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, positions, k, v, q,
+        n, src_stride, q_stride, g.kv_dim, n_kv_heads, n_heads, g.n_blocks * 16, r.table, r.max_pos,
+        r.rope_dim, r.head_dim, r.neox);
   return hipGetLastError();
 }
 

@@ -222,6 +222,32 @@ class KvCache:
             _dev_ptr(k, torch.float32, "k", self.device), _dev_ptr(v, torch.float32, "v", self.device),
             k.shape[1]))
 
+    def rope_init(self, base: float, rope_dim: int, head_dim: int, neox: bool, max_positions: int) -> None:
+        """RoPE table of Model::rope (model.rs:263-265, 291-308) for write_rope."""
+        _check(self._lib.ltkv_rope_init(self._h, float(base), rope_dim, head_dim, 1 if neox else 0,
+                                        max_positions))
+
+    def write_rope(self, layer: int, slot_mapping, positions, k, v, q=None, n_heads: int = 0) -> None:
+        """Kernel 1 with RoPE (model.rs:414-429): k rotated into its cell, v appended,
+        q ([n][n_heads*head_dim] f32, optional) rotated in place."""
+        import torch
+
+        n = slot_mapping.numel()
+        if k.dim() != 2 or k.shape != v.shape or k.shape[0] != n or k.shape[1] < self.kv_dim:
+            raise ValueError("k and v must be [n][>=kv_dim] and match slot_mapping")
+        if positions.numel() != n:
+            raise ValueError("positions must match slot_mapping")
+        qp, qs = None, 0
+        if q is not None:
+            if q.dim() != 2 or q.shape[0] != n:
+                raise ValueError("q must be [n][n_heads*head_dim]")
+            qp, qs = _dev_ptr(q, torch.float32, "q", self.device), q.shape[1]
+        _check(self._lib.ltkv_write_rope(
+            self._h, layer, n, _dev_ptr(slot_mapping, torch.int32, "slot_mapping", self.device),
+            _dev_ptr(positions, torch.int32, "positions", self.device),
+            _dev_ptr(k, torch.float32, "k", self.device), _dev_ptr(v, torch.float32, "v", self.device),
+            k.shape[1], qp, qs, n_heads))
+
     def copy_blocks(self, pairs) -> None:
         """Kernel 2: copy block pairs[i,0] -> pairs[i,1] (all layers, K and V)."""
         import torch

@@ -548,6 +548,53 @@ void ora_write_batch(void *h, size_t layer, size_t n, const int32_t *slot_mappin
   }
 }
 
+// Model::rope (model.rs:291-308) with inv_freq of model.rs:263-265: per head,
+// pair i rotates (v[a], v[b]) by pos * inv_freq[i], a/b = (i, i + rope_dim/2)
+// for NeoX models, else (2i, 2i + 1); (sin, cos) = f32::sin_cos, i.e. libm
+// sinf/cosf; no fused multiply-add (built with -ffp-contract=off).
+static void rope(float *x, size_t n_heads, size_t head_dim, size_t rope_dim, bool neox,
+                 const std::vector<float> &inv_freq, size_t pos) {
+  const size_t half = rope_dim / 2;
+  for (size_t h = 0; h < n_heads; ++h) {
+    float *v = x + h * head_dim;
+    for (size_t i = 0; i < inv_freq.size(); ++i) {
+      const float ang = (float)pos * inv_freq[i];
+      const float sn = sinf(ang), cs = cosf(ang);
+      const size_t a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
+      const float x0 = v[a], x1 = v[b];
+      v[a] = x0 * cs - x1 * sn;
+      v[b] = x0 * sn + x1 * cs;
+    }
+  }
+}
+
+static std::vector<float> rope_inv_freq(float base, size_t rope_dim) {
+  std::vector<float> inv(rope_dim / 2);
+  for (size_t i = 0; i < inv.size(); ++i) inv[i] = powf(base, -2.0f * (float)i / (float)rope_dim);
+  return inv;
+}
+
+// The per-token body of model.rs:414-429: RoPE on the token's q (n_heads
+// heads, in place, when q is not null) and k (the cache's kv heads), then
+// write(layer, block, slot, k, v). Rows are kv_dim (k, v) / q_stride (q) apart.
+void ora_write_rope_batch(void *h, size_t layer, size_t n, const int32_t *slot_mapping,
+                          const int32_t *positions, const float *k, const float *v, float *q,
+                          size_t q_stride, size_t n_heads, float base, size_t rope_dim,
+                          size_t head_dim, int neox) {
+  auto *kv = (OracleKv *)h;
+  const std::vector<float> inv = rope_inv_freq(base, rope_dim);
+  std::vector<float> kr(kv->kv_dim);
+  for (size_t i = 0; i < n; ++i) {
+    const size_t pos = (size_t)positions[i];
+    if (q) rope(q + i * q_stride, n_heads, head_dim, rope_dim, neox != 0, inv, pos);
+    if (slot_mapping[i] < 0) continue;
+    std::copy(k + i * kv->kv_dim, k + (i + 1) * kv->kv_dim, kr.begin());
+    rope(kr.data(), kv->kv_dim / head_dim, head_dim, rope_dim, neox != 0, inv, pos);
+    kv->write(layer, (size_t)slot_mapping[i] / kBlock, (size_t)slot_mapping[i] % kBlock, kr.data(),
+              v + i * kv->kv_dim);
+  }
+}
+
 // rows(layer, seq, n) collected into contiguous [n][kv_dim] buffers (kv.rs:133-150).
 int ora_rows(void *h, size_t layer, uint32_t seq, size_t n, void *k_out, void *v_out) {
   auto *kv = (OracleKv *)h;

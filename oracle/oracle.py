@@ -67,6 +67,7 @@ def load():
         "ora_append_batch": (C.c_int, [vp, sz, vp, vp, vp, P(sz)]),
         "ora_write": (None, [vp, sz, sz, sz, vp, vp]),
         "ora_write_batch": (None, [vp, sz, sz, vp, vp, vp]),
+        "ora_write_rope_batch": (None, [vp, sz, sz, vp, vp, vp, vp, vp, sz, sz, C.c_float, sz, sz, C.c_int]),
         "ora_rows": (C.c_int, [vp, sz, u32, sz, vp, vp]),
         "ora_block_table": (C.c_int, [vp, u32, vp, sz, P(sz)]),
         "ora_truncate": (None, [vp, u32, sz]),
@@ -202,6 +203,21 @@ class OracleKv:
         v = np.ascontiguousarray(v, dtype=np.float32)
         assert k.shape == (sm.size, self.kv_dim) and v.shape == k.shape
         self._lib.ora_write_batch(self._h, layer, sm.size, _ptr(sm), _ptr(k), _ptr(v))
+
+    # -- model.rs:291-308 + 414-429: RoPE on q (in place) and k, then write
+    def write_rope_batch(self, layer: int, slot_mapping, positions, k, v, base: float, rope_dim: int,
+                         head_dim: int, neox: bool, q=None, n_heads: int = 0) -> None:
+        sm = np.ascontiguousarray(slot_mapping, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        assert k.shape == (sm.size, self.kv_dim) and v.shape == k.shape and pos.shape == sm.shape
+        qp, qs = None, 0
+        if q is not None:
+            assert q.dtype == np.float32 and q.flags.c_contiguous and q.shape[0] == sm.size
+            qp, qs = _ptr(q), q.shape[1]
+        self._lib.ora_write_rope_batch(self._h, layer, sm.size, _ptr(sm), _ptr(pos), _ptr(k), _ptr(v), qp,
+                                       qs, n_heads, float(base), rope_dim, head_dim, 1 if neox else 0)
 
     # -- kv.rs:133-150 (collected)
     def rows(self, layer: int, seq: int, n: int):

@@ -480,3 +480,72 @@ def test_attention_zero_length_gives_zeros(gpu):
     lens = torch.zeros(2, dtype=torch.int32, device=gpu)
     out = g.decode_attention(0, q, tables, lens, 2, 128)
     assert (out.cpu().numpy() == 0).all()
+
+
+# ---------------------------------------------------------------------------- fused RoPE + append
+@pytest.mark.parametrize("dtype,n_heads,n_kv,head_dim,rope_dim,neox,base", [
+    ("f16", 32, 8, 128, 128, False, 500000.0),   # Llama-3-8B
+    ("f16", 28, 4, 128, 128, True, 1000000.0),   # Qwen2.5-7B (NeoX pairs)
+    ("f16", 8, 2, 128, 64, True, 10000.0),       # partial rotary
+    ("f32", 32, 4, 64, 64, False, 10000.0),      # TinyLlama, f32 cells
+])
+def test_write_rope_bit_exact(gpu, dtype, n_heads, n_kv, head_dim, rope_dim, neox, base):
+    """model.rs:414-429 fused: q rotated in place and k rotated into its cell
+    (then f32->f16 RNE), v appended; pools and q bit-identical to the oracle
+    for positions up to 32767, including skipped slots."""
+    import torch
+
+    rng = np.random.default_rng(head_dim + rope_dim + n_heads)
+    kv_dim = n_kv * head_dim
+    g, o = _caches(1, kv_dim, 600 * BLOCK, dtype, rng.permutation(600))
+    g.rope_init(base, rope_dim, head_dim, neox, 32768)
+    lens = {0: 700, 1: 1200, 2: 33}
+    seqs = np.concatenate([np.full(n, s, dtype=np.uint32) for s, n in lens.items()])
+    pos = np.concatenate([np.arange(n, dtype=np.uint64) for n in lens.values()])
+    sm = g.append_batch(seqs, pos)
+    assert np.array_equal(sm, o.append_batch(seqs, pos))
+    sm[5] = -1  # a skipped row
+    n = sm.size
+    k = rng.standard_normal((n, kv_dim), dtype=np.float32) * 3
+    v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    q = rng.standard_normal((n, n_heads * head_dim), dtype=np.float32)
+    p32 = pos.astype(np.int32) * 23 % 32768  # positions need not follow the cells here
+    dq = torch.from_numpy(q).to(gpu)
+    g.write_rope(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(p32).to(gpu), torch.from_numpy(k).to(gpu),
+                 torch.from_numpy(v).to(gpu), q=dq, n_heads=n_heads)
+    qo = q.copy()
+    o.write_rope_batch(0, sm, p32, k, v, base, rope_dim, head_dim, neox, q=qo, n_heads=n_heads)
+    np.testing.assert_array_equal(_bits(dq.cpu().numpy()), _bits(qo))
+    gk, gv = g.read_pool(0)
+    ok, ov = o.pool(0)
+    np.testing.assert_array_equal(_bits(gk), _bits(ok))
+    np.testing.assert_array_equal(_bits(gv), _bits(ov))
+
+
+def test_write_rope_equals_write_of_rotated_rows(gpu):
+    """Without q, the fused launch writes exactly what ltkv_write writes for
+    rows rotated by the oracle; positions outside the table write nothing."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    kv_dim, hd = 512, 128
+    g, o = _caches(1, kv_dim, 64 * BLOCK, "f16")
+    g.rope_init(10000.0, hd, hd, False, 4096)
+    sm = g.append_batch(np.zeros(40, np.uint32), np.arange(40, dtype=np.uint64))
+    o.append_batch(np.zeros(40, np.uint32), np.arange(40, dtype=np.uint64))
+    k = rng.standard_normal((40, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((40, kv_dim), dtype=np.float32)
+    pos = np.arange(40, dtype=np.int32) * 100
+    pos[3] = 4096  # outside the table: skipped
+    pos[4] = -1
+    g.write_rope(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(pos).to(gpu), torch.from_numpy(k).to(gpu),
+                 torch.from_numpy(v).to(gpu))
+    keep = np.ones(40, bool)
+    keep[[3, 4]] = False
+    sm_o = sm.copy()
+    sm_o[~keep] = -1
+    o.write_rope_batch(0, sm_o, np.where(keep, pos, 0), k, v, 10000.0, hd, hd, False)
+    gk, gv = g.read_pool(0)
+    ok, ov = o.pool(0)
+    np.testing.assert_array_equal(gk, ok)
+    np.testing.assert_array_equal(gv, ov)

@@ -333,3 +333,49 @@ def test_pool_concurrent_callers():
     for t in threads:
         t.join()
     assert not errors
+
+
+# ---------------------------------------------------------------------------- RoPE (model.rs:291-308)
+def _rope64(x, n_heads, head_dim, rope_dim, neox, base, pos):
+    """float64 rotation on the same f32 angles (pos * inv_freq, both f32)."""
+    x = x.astype(np.float64).copy()
+    half = rope_dim // 2
+    inv = np.array([np.float32(base) ** np.float32(-2.0 * i / rope_dim) for i in range(half)], dtype=np.float64)
+    ang = (np.float32(pos) * inv.astype(np.float32)).astype(np.float64)
+    for h in range(n_heads):
+        v = x[h * head_dim:(h + 1) * head_dim]
+        a = np.arange(half) if neox else 2 * np.arange(half)
+        b = a + half if neox else a + 1
+        x0, x1 = v[a].copy(), v[b].copy()
+        v[a] = x0 * np.cos(ang) - x1 * np.sin(ang)
+        v[b] = x0 * np.sin(ang) + x1 * np.cos(ang)
+    return x
+
+
+@pytest.mark.parametrize("neox,rope_dim,head_dim", [(False, 128, 128), (True, 128, 128), (True, 64, 128),
+                                                    (False, 64, 64)])
+def test_oracle_rope_against_float64(neox, rope_dim, head_dim):
+    """The oracle's rotation (applied to q in place) against float64 numpy on
+    the same f32 angles: pairing, signs and frequencies; position 0 is the
+    identity and dimensions past rope_dim are untouched, bit for bit."""
+    rng = np.random.default_rng(rope_dim + head_dim + neox)
+    n_kv, n_heads = 2, 4
+    kv_dim = n_kv * head_dim
+    o = OracleKv(1, kv_dim, 64 * 16, dtype="f32")
+    pos = np.array([0, 1, 7, 100, 4095, 32767], dtype=np.int32)
+    sm = o.append_batch(np.zeros(pos.size, np.uint32), np.arange(pos.size, dtype=np.uint64))
+    k = rng.standard_normal((pos.size, kv_dim), dtype=np.float32)
+    q = rng.standard_normal((pos.size, n_heads * head_dim), dtype=np.float32)
+    q0 = q.copy()
+    o.write_rope_batch(0, sm, pos, k, k, 500000.0, rope_dim, head_dim, neox, q=q, n_heads=n_heads)
+    np.testing.assert_array_equal(q[0], q0[0])
+    for i, p in enumerate(pos):
+        want = _rope64(q0[i], n_heads, head_dim, rope_dim, neox, 500000.0, int(p))
+        np.testing.assert_allclose(q[i], want, rtol=0, atol=2e-6 * (1 + np.abs(want)).max())
+        for h in range(n_heads):
+            tail = slice(h * head_dim + rope_dim, (h + 1) * head_dim)
+            np.testing.assert_array_equal(q[i, tail], q0[i, tail])
+    kr, _ = o.rows(0, 0, pos.size)
+    for i, p in enumerate(pos):  # f32 pools hold the rotated k exactly as the oracle computed it
+        want = _rope64(k[i], n_kv, head_dim, rope_dim, neox, 500000.0, int(p))
+        np.testing.assert_allclose(kr[i], want, rtol=0, atol=2e-6 * (1 + np.abs(want)).max())
