@@ -611,13 +611,45 @@ def bench_mixed(args):
     att_us = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]) * 1e3)
     app_bytes = float(np.mean([(p >= 0).sum() for p in plan_sm])) * (kvd * 12 + 4)
     att_bytes = float(np.mean([l.astype(np.int64).sum() for l in plan_lens])) * 2 * kvd * 2 + 2 * q.numel() * 4
+
+    # One more step at the final state with every token of the batch: the
+    # fused RoPE append of all 4216 tokens, then one planned attention over
+    # all of them (each prefill chunk a causal group on the matrix cores, the
+    # decode tokens per query), timed 4 times back to back after a warm call.
+    seqs, pos = [], []
+    for sid, target in pre:
+        start = kv.len(sid)
+        seqs += [sid] * chunk
+        pos += list(range(start, start + chunk))
+    for sid in dec:
+        seqs.append(sid)
+        pos.append(kv.len(sid))
+    kv.rope_init(1e6, hd, hd, True, 8192 + chunk + steps + 1)
+    sm = torch.from_numpy(kv.append_batch(np.array(seqs, np.uint32), np.array(pos, np.uint64))).cuda()
+    d_pos = torch.from_numpy(np.array(pos, np.int32)).cuda()
+    qa = torch.randn((len(seqs), n_heads * hd), device="cuda")
+    out_all = torch.empty_like(qa)
+    rope_us = _time_op(lambda: kv.write_rope(0, sm, d_pos, kn, kn, q=qa, n_heads=n_heads), reps=10)
+    stats = kv.plan_attention(np.array(seqs, np.uint32), np.array(pos, np.int64) + 1, n_heads, hd)
+    kv.planned_attention(0, qa, out=out_all)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(4):
+        kv.planned_attention(0, qa, out=out_all)
+    e1.record()
+    torch.cuda.synchronize()
+    all_us = e0.elapsed_time(e1) * 1e3 / 4
     print(json.dumps({
         "workload": "mixed qwen2.5-7b f16: 8x512 prefill append + 120 decode, 2% churn, "
                     f"{steps} steps", "append_us": round(app_us, 2),
         "append_GBps": round(app_bytes / (app_us * 1e-6) / 1e9, 1),
         "attention_us": round(att_us, 2), "attention_bytes": round(att_bytes),
         "attention_frac": round(att_bytes / (att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
-        "step_us": round(app_us + att_us, 2)}), flush=True)
+        "step_us": round(app_us + att_us, 2),
+        "full_step": {"rope_append_us": round(rope_us, 2),
+                      "attention_all_tokens_us": round(all_us, 2),
+                      "plan": {k: stats[k] for k in ("groups", "grouped", "prefix_workgroups")}}}),
+        flush=True)
 
 
 def main():

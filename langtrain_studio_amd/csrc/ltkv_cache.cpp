@@ -69,7 +69,8 @@ struct AttnPlan {
   int suffix_part = 0;  // partition tokens of the per-query pass when grouped
   uint64_t groups = 0, grouped = 0, shared_blocks = 0;
   bool groups_only = false;  // every query completed by its group: no per-query pass
-  size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0,
+  size_t n_pass = 0;         // queries of the per-query pass (the rest are completed by groups)
+  size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0, off_qmap = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
   std::vector<int32_t> host;  // the arrays above, in device layout
   uint8_t *d = nullptr, *h = nullptr;  // device buffer, pinned staging
@@ -301,6 +302,8 @@ constexpr size_t kMinSharedBlocks = 2;
 // Tokens per group partition are at least this (a multiple of the kernel's
 // 32-token staging step).
 constexpr size_t kMinPrefixPart = 256;
+// Longest per-query remainder for which grouped plans use single-wave work-groups.
+constexpr size_t kShortRemainder = 512;
 
 size_t align8(size_t x) { return (x + 7) / 8 * 8; }
 
@@ -539,8 +542,10 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.suffix_part = (int)std::min<uint64_t>(1024, std::max<uint64_t>(64, (per_wg + 63) / 64 * 64));
   if ((uint64_t)n * sstride + (uint64_t)groups.size() * gstride > (uint64_t)INT32_MAX / 2)
     return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
-  bool groups_only = !groups.empty() && suffix_tokens == 0;
-  for (size_t i = 0; i < n && groups_only; ++i) groups_only = pre_parts[i] < 0;
+  std::vector<int32_t> qmap;  // queries left for the per-query pass
+  for (size_t i = 0; i < n; ++i)
+    if (pre_parts[i] >= 0) qmap.push_back((int32_t)i);
+  const bool groups_only = qmap.empty();
 
   P.n = n;
   P.n_heads = n_heads;
@@ -553,11 +558,13 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.grouped = grouped;
   P.shared_blocks = shared_blocks;
   P.groups_only = groups_only;
+  P.n_pass = qmap.size();
   P.off_tables = 0;
   P.off_stables = align8(P.off_tables + groups.size() * gstride);
   P.off_slens = align8(P.off_stables + n * sstride);
   P.off_pre = align8(P.off_slens + n);
-  P.off_members = align8(P.off_pre + n);
+  P.off_qmap = align8(P.off_pre + n);
+  P.off_members = align8(P.off_qmap + qmap.size());
   P.off_jobs = align8(P.off_members + members.size());
   const size_t words = P.off_jobs + jobs.size() * (sizeof(ltkv::MqJob) / 4);
   P.bytes = words * 4;
@@ -576,6 +583,7 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     h[P.off_slens + i] = (int32_t)(lens[i] - pre_tokens[i]);
     h[P.off_pre + i] = pre_parts[i];
   }
+  std::copy(qmap.begin(), qmap.end(), h + P.off_qmap);
   std::copy(members.begin(), members.end(), h + P.off_members);
   if (!jobs.empty()) std::memcpy(h + P.off_jobs, jobs.data(), jobs.size() * sizeof(ltkv::MqJob));
   return LTKV_OK;
@@ -1008,11 +1016,13 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
   const size_t group = P.n_heads / (c->kv_dim / P.head_dim);
   const bool grouped = P.groups > 0;
-  // Grouped plans are batch-dependent anyway: their per-query pass takes the
-  // plan's partition and single-wave work-groups unless a partition is fixed.
+  // Grouped plans are batch-dependent anyway: when every query's remainder is
+  // short (forks reading a few private blocks), their per-query pass takes
+  // the plan's partition and single-wave work-groups unless a partition is
+  // fixed; long remainders keep the four-wave per-query policy.
   int part = (int)c->attn_part_tokens;
   int waves = 4;
-  if (grouped && part == 0) {
+  if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) {
     part = P.suffix_part;
     waves = 1;
   }
@@ -1036,6 +1046,10 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   a.table_stride = (int64_t)P.sstride;
   a.lens = d + P.off_slens;
   a.waves = waves;
+  if (P.n_pass < P.n) {  // only the queries that groups did not complete
+    a.n = (int64_t)P.n_pass;
+    a.qmap = d + P.off_qmap;
+  }
   if (grouped) {
     a.pre_parts = d + P.off_pre;
     a.pre_o = (float *)(c->ws + pre_o_off);

@@ -356,7 +356,8 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
             float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
-            int max_parts, const int32_t *__restrict__ pre_parts) {
+            int max_parts, const int32_t *__restrict__ pre_parts,
+            const int32_t *__restrict__ qmap) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
   constexpr int RPL = 64 / L;      // rows per wave load
@@ -367,7 +368,8 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   // query (one per kv head) are dispatched together.
   const int kvh = (int)(blockIdx.x % n_kv_heads);
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
-  const int64_t qi = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int64_t qx = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int64_t qi = qmap ? qmap[qx] : qx;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane % L, rg = lane / L;
@@ -574,9 +576,11 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
                   const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
                   int part_tokens, int max_parts, int64_t max_len,
                   const int32_t *__restrict__ pre_parts, const float *__restrict__ pre_o,
-                  const float *__restrict__ pre_ml, int max_pre_parts) {
+                  const float *__restrict__ pre_ml, int max_pre_parts,
+                  const int32_t *__restrict__ qmap) {
   const int h = (int)(blockIdx.x % n_heads);
-  const int64_t qi = blockIdx.x / n_heads;
+  const int64_t qx = blockIdx.x / n_heads;
+  const int64_t qi = qmap ? qmap[qx] : qx;
   const int d = threadIdx.x;
   int64_t len = lens[qi];
   if (len < 0) len = 0;
@@ -618,7 +622,8 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   const unsigned mgrid = (unsigned)(a.n * a.n_heads);
   attn_merge_kernel<HD><<<mgrid, HD, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
                                              a.part_tokens, a.max_parts, a.table_stride * 16,
-                                             a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts);
+                                             a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
+                                             a.qmap);
   return hipGetLastError();
 }
 
@@ -750,7 +755,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
               float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
-              int max_parts, const int32_t *__restrict__ pre_parts) {
+              int max_parts, const int32_t *__restrict__ pre_parts,
+              const int32_t *__restrict__ qmap) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
@@ -768,7 +774,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   const int kvh = (int)(blockIdx.x % n_kv_heads);
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
-  const int64_t qi = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int64_t qx = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int64_t qi = qmap ? qmap[qx] : qx;
   const int lane = threadIdx.x & 63;
   const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, rg = lane >> 4;
@@ -1103,7 +1110,7 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
           static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
           a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
           g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens,
-          a.max_parts, a.pre_parts);
+          a.max_parts, a.pre_parts, a.qmap);
       return launch_merge<HD>(a, s);
     }
   }
@@ -1111,7 +1118,7 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts);
+      a.pre_parts, a.qmap);
   return launch_merge<HD>(a, s);
 }
 
@@ -1122,7 +1129,7 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts);
+      a.pre_parts, a.qmap);
   return launch_merge<HD>(a, s);
 }
 

@@ -220,3 +220,22 @@ def test_mixed_step_prefill_decode_and_forks(gpu):
     lens = lens + [401, 401, 401]
     stats, *_ = _run(gpu, g, o, seqs, lens, 28, 128, rng)
     assert stats["groups"] == 3 and stats["grouped"] == 128 + 64 + 3
+
+
+def test_decode_queries_in_a_mixed_plan_match_the_decode_kernel(gpu):
+    """Prefill chunks (completed by their causal groups) next to decode
+    queries with long contexts: the per-query pass covers only the decode
+    queries, with the per-query partition policy, so their outputs equal the
+    decode kernel's bit for bit; the chunk tokens match the oracle."""
+    import torch
+
+    rng = np.random.default_rng(45)
+    kv_dim, n_heads, hd = 4 * 128, 28, 128
+    g, o, seqs, lens = _prefill_state(rng, kv_dim, [(0, 900, 96), (1, 40, 64)],
+                                      decode=[(5, 1300), (6, 2100), (7, 700)])
+    stats, q, out, tables, la = _run(gpu, g, o, seqs, lens, n_heads, hd, rng)
+    assert stats["groups"] == 2 and stats["grouped"] == 160
+    dec = slice(160, 163)
+    ref = g.decode_attention(0, torch.from_numpy(q[dec].copy()).to(gpu), torch.from_numpy(tables[dec].copy()).to(gpu),
+                             torch.from_numpy(la[dec].copy()).to(gpu), n_heads, hd).cpu().numpy()
+    np.testing.assert_array_equal(out[dec], ref)
