@@ -68,6 +68,29 @@ def _profiled_traffic():
     return int(m.group(1)) if m else None
 
 
+def _host_cpus() -> str:
+    """Logical CPUs this process may use and the host's CPU model and sockets."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    model, sockets, logical = "unknown", set(), 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "model name":
+                    model = val.strip()
+                elif key == "physical id":
+                    sockets.add(val.strip())
+                elif key == "processor":
+                    logical += 1
+    except OSError:
+        pass
+    return f"{usable} of {logical or '?'} logical CPUs usable, {len(sockets) or '?'} socket(s), {model}"
+
+
 def _cpu_threads(req: int) -> int:
     if req > 0:
         return req
@@ -700,13 +723,17 @@ def main():
     app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9
     roofline_us = att_bytes / (PEAK_HBM_GBPS * 1e9) * 1e6
 
-    cpu = None
+    cpu = cpu1 = None
     if not args.no_cpu:
         threads = _cpu_threads(args.cpu_threads)
+        host = _host_cpus()
         cpu_us, n = cpu_baseline(w, threads, args.cpu_seconds)
         cpu = {"value": round(cpu_us, 1), "unit": "µs/step", "cores": threads, "kind": "port",
                "sample": f"{n} decode steps of the same workload (64 seqs, append+write+attention, "
-                         f"same cache state), oracle C++ restatement, {threads} threads"}
+                         f"same cache state), oracle C++ restatement, {threads} threads; host: {host}"}
+        cpu1_us, n1 = cpu_baseline(w, 1, min(args.cpu_seconds, 5.0))
+        cpu1 = {"value": round(cpu1_us, 1), "unit": "µs/step", "cores": 1, "kind": "port",
+                "sample": f"{n1} decode steps, same work, one thread"}
 
     out = {
         "metric": METRIC,
@@ -736,6 +763,7 @@ def main():
                      "bytes_per_launch": round(att_bytes)},
         "wall_s": round(wall, 3),
         "cpu_baseline": cpu,
+        "cpu_baseline_1thread": cpu1,
     }
     print(json.dumps(out), flush=True)
 

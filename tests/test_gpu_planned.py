@@ -239,3 +239,61 @@ def test_decode_queries_in_a_mixed_plan_match_the_decode_kernel(gpu):
     ref = g.decode_attention(0, torch.from_numpy(q[dec].copy()).to(gpu), torch.from_numpy(tables[dec].copy()).to(gpu),
                              torch.from_numpy(la[dec].copy()).to(gpu), n_heads, hd).cpu().numpy()
     np.testing.assert_array_equal(out[dec], ref)
+
+
+def test_continuous_batching_churn_matches_oracle(gpu):
+    """Config-4 semantics at small scale, 6 steps: each step appends a prefill
+    chunk of one stream and a token per decode sequence (fused RoPE append),
+    decode sequences finish (blocks freed LIFO, kv.rs:76-81) and arrivals
+    reuse them; tables and pools stay bit-identical to the oracle and every
+    step's attention (per-query and planned) is within tolerance."""
+    import torch
+
+    rng = np.random.default_rng(46)
+    n_heads, n_kv, hd = 28, 4, 128
+    kv_dim = n_kv * hd
+    g, o = _caches(1, kv_dim, 300 * BLOCK, "f16", rng)
+    both = [("gpu", g), ("oracle", o)]
+    g.rope_init(1e6, hd, hd, True, 4096)
+    dec = list(range(6))
+    fill_sequences(both, {s: int(rng.integers(20, 200)) for s in dec}, rng, kv_dim)
+    stream, next_id = 100, 200
+    for step in range(6):
+        seqs = [stream] * 48 + dec
+        pos = list(range(g.len(stream), g.len(stream) + 48)) + [g.len(s) for s in dec]
+        sm = g.append_batch(seqs, pos)
+        np.testing.assert_array_equal(sm, o.append_batch(seqs, pos))
+        k = rng.standard_normal((len(seqs), kv_dim), dtype=np.float32)
+        v = rng.standard_normal((len(seqs), kv_dim), dtype=np.float32)
+        q = rng.standard_normal((len(seqs), n_heads * hd), dtype=np.float32)
+        dq = torch.from_numpy(q.copy()).to(gpu)
+        g.write_rope(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(np.array(pos, np.int32)).to(gpu),
+                     torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), q=dq, n_heads=n_heads)
+        o.write_rope_batch(0, sm, np.array(pos, np.int32), k, v, 1e6, hd, hd, True, q=q, n_heads=n_heads)
+        np.testing.assert_array_equal(dq.cpu().numpy().view(np.uint32), q.view(np.uint32))
+        lens = [p + 1 for p in pos]
+        tables, la = tables_and_lens(g, seqs, lens)
+        want = o.attention_tables(0, tables, la, q, n_heads, hd, threads=8)
+        flat = g.decode_attention(0, dq, torch.from_numpy(tables).to(gpu), torch.from_numpy(la).to(gpu),
+                                  n_heads, hd).cpu().numpy()
+        attention_close(flat, want, "f16")
+        g.plan_attention(seqs, lens, n_heads, hd)
+        attention_close(g.planned_attention(0, dq).cpu().numpy(), want, "f16")
+        for i, s in enumerate(dec):  # a third finish; arrivals take their place
+            if rng.random() < 0.34:
+                g.truncate(s, 0)
+                o.truncate(s, 0)
+                dec[i] = next_id
+                fill_sequences(both, {next_id: int(rng.integers(1, 120))}, rng, kv_dim)
+                next_id += 1
+        if g.len(stream) > 200:  # the prompt is done: a new stream starts
+            g.truncate(stream, 0)
+            o.truncate(stream, 0)
+            stream += 1
+        assert g.free_blocks() == o.free_blocks()
+        for s in dec + [stream]:
+            np.testing.assert_array_equal(g.block_table(s), o.block_table(s))
+        gk, gv = g.read_pool(0)
+        ok, ov = o.pool(0)
+        np.testing.assert_array_equal(gk, ok)
+        np.testing.assert_array_equal(gv, ov)
