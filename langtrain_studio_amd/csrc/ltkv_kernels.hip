@@ -569,19 +569,26 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
 }
 
 // Merge of the context partitions of one (query, head): O = sum_p o_p 2^(m_p-M),
-// L = sum_p l_p 2^(m_p-M), out = O / L. One thread per output element.
+// L = sum_p l_p 2^(m_p-M), out = O / L. A (query, head) pair takes HD/4
+// threads with 4 output elements each (16-byte loads and stores), a
+// work-group 256 / (HD/4) pairs; the partition loop is unrolled so several
+// partials are in flight per thread.
 template <int HD>
-__global__ void __launch_bounds__(HD)
+__global__ void __launch_bounds__(256)
 attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                   const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
                   int part_tokens, int max_parts, int64_t max_len,
                   const int32_t *__restrict__ pre_parts, const float *__restrict__ pre_o,
                   const float *__restrict__ pre_ml, int max_pre_parts,
-                  const int32_t *__restrict__ qmap) {
-  const int h = (int)(blockIdx.x % n_heads);
-  const int64_t qx = blockIdx.x / n_heads;
+                  const int32_t *__restrict__ qmap, int64_t n_pairs) {
+  constexpr int TPP = HD / 4;     // threads per (query, head)
+  constexpr int PPW = 256 / TPP;  // pairs per work-group
+  const int64_t pair = (int64_t)blockIdx.x * PPW + threadIdx.x / TPP;
+  if (pair >= n_pairs) return;
+  const int d = (threadIdx.x % TPP) * 4;
+  const int h = (int)(pair % n_heads);
+  const int64_t qx = pair / n_heads;
   const int64_t qi = qmap ? qmap[qx] : qx;
-  const int d = threadIdx.x;
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
@@ -599,18 +606,23 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   for (int p = 0; p < np; ++p) mx = __builtin_fmaxf(mx, ml[2 * p]);
   for (int p = 0; p < npre; ++p) mx = __builtin_fmaxf(mx, pml[2 * p]);
   const float mref = mx == -INFINITY ? 0.f : mx;
-  float lsum = 0.f, o = 0.f;
+  float lsum = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int p = 0; p < npre; ++p) {
     const float a = __builtin_amdgcn_exp2f(pml[2 * p] - mref);
     lsum += pml[2 * p + 1] * a;
-    o += pre_o[(qh * max_pre_parts + p) * HD + d] * a;
+    o += *reinterpret_cast<const f32x4 *>(pre_o + (qh * max_pre_parts + p) * HD + d) * a;
   }
+#pragma unroll 4
   for (int p = 0; p < np; ++p) {
     const float a = __builtin_amdgcn_exp2f(ml[2 * p] - mref);
     lsum += ml[2 * p + 1] * a;
-    o += part_o[(qh * max_parts + p) * HD + d] * a;
+    o += *reinterpret_cast<const f32x4 *>(part_o + (qh * max_parts + p) * HD + d) * a;
   }
-  out[qh * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+  f32x4 r = {0.f, 0.f, 0.f, 0.f};
+  if (lsum > 0.f) r = f32x4{o.x / lsum, o.y / lsum, o.z / lsum, o.w / lsum};
+  *reinterpret_cast<f32x4 *>(out + qh * HD + d) = r;
 }
 
 // Launch check of the attention kernel, then the partition merge when some
@@ -619,11 +631,13 @@ template <int HD>
 hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || (a.max_parts == 1 && !a.pre_parts)) return e;
-  const unsigned mgrid = (unsigned)(a.n * a.n_heads);
-  attn_merge_kernel<HD><<<mgrid, HD, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
-                                             a.part_tokens, a.max_parts, a.table_stride * 16,
-                                             a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
-                                             a.qmap);
+  const int64_t pairs = a.n * a.n_heads;
+  constexpr int ppw = 256 / (HD / 4);
+  const unsigned mgrid = (unsigned)((pairs + ppw - 1) / ppw);
+  attn_merge_kernel<HD><<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
+                                              a.part_tokens, a.max_parts, a.table_stride * 16,
+                                              a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
+                                              a.qmap, pairs);
   return hipGetLastError();
 }
 
