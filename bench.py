@@ -47,7 +47,7 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed", "prefill", "rope-append"],
+                            "mixed", "prefill", "rope-append", "decode-q8"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -106,12 +106,13 @@ class Llama3Decode:
 
     n_heads, n_kv, head_dim, batch = 32, 8, 128, 64
 
-    def __init__(self, steps: int, seed: int, partition: int):
+    def __init__(self, steps: int, seed: int, partition: int, dtype: str = "f16"):
         import torch
 
         from langtrain_studio_amd import KvCache
 
         self.torch = torch
+        self.dtype = dtype
         dev = torch.device("cuda", 0)
         self.dev = dev
         rng = np.random.default_rng(seed)
@@ -122,7 +123,7 @@ class Llama3Decode:
         need = sum(math.ceil((int(c) + steps) / BLOCK) for c in self.ctx)
         self.n_blocks = int(math.ceil(need * 1.1))
         stream = torch.cuda.current_stream(dev)
-        self.kv = KvCache(1, kvd, self.n_blocks * BLOCK, dtype="f16", device=0, stream=stream)
+        self.kv = KvCache(1, kvd, self.n_blocks * BLOCK, dtype=dtype, device=0, stream=stream)
         if partition:
             self.kv.set_attention_partition(partition)
         self.order = rng.permutation(self.n_blocks)
@@ -170,16 +171,21 @@ class Llama3Decode:
         self.kv.decode_attention(0, self.d_q[s], self.d_tables, self.d_lens[s], self.n_heads, self.head_dim,
                                  out=self.d_out)
 
+    # Bytes one cached token row (K or V) occupies: f16 elements, or q8_0
+    # quants plus one f16 scale per 32 elements.
+    def row_bytes(self) -> int:
+        return self.kvd * 2 if self.dtype == "f16" else self.kvd + self.kvd // 32 * 2
+
     # Algorithmic bytes of one launch at step s.
     def attention_bytes(self, s: int) -> float:
         lens = self.lens[s].astype(np.int64)
-        kv = lens.sum() * 2 * self.kvd * 2
+        kv = lens.sum() * 2 * self.row_bytes()
         qo = 2 * self.batch * self.n_heads * self.head_dim * 4
         tables = (-(-lens // BLOCK)).sum() * 4 + self.batch * 4
         return float(kv + qo + tables)
 
     def append_bytes(self) -> float:
-        return float(self.batch * self.kvd * (4 + 4 + 2 + 2) + self.batch * 4)
+        return float(self.batch * (self.kvd * (4 + 4) + 2 * self.row_bytes()) + self.batch * 4)
 
 
 def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
@@ -187,11 +193,13 @@ def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
     running the same decode steps on the same cache state."""
     from oracle import OracleKv
 
-    o = OracleKv(1, w.kvd, w.n_blocks * BLOCK, dtype="f16")
+    o = OracleKv(1, w.kvd, w.n_blocks * BLOCK, dtype=w.dtype)
     o.init_free_order(w.order)
     o.append_batch(w.pre_seqs, w.pre_pos)
     k, v = w.kv.read_pool(0)  # device state after the GPU run (same cells; the
     o.load_pool(0, k, v)      # timed steps rewrite the decode cells identically)
+    if w.dtype == "q8_0":
+        o.load_scales(0, *w.kv.read_scales(0))
     seqs = np.arange(w.batch, dtype=np.uint32)
 
     def step(s):
@@ -675,25 +683,10 @@ def bench_mixed(args):
         flush=True)
 
 
-def main():
-    args = _args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                          "(the path shards by sequence across GPUs with no exchange)"}))
-        sys.exit(2)
+def _time_decode(w: Llama3Decode, steps: int, warmup: int):
+    """Times `steps` decode steps (append then attention) with HIP events on
+    the stream both run on: (µs per step, attention µs, append µs, wall s)."""
     import torch
-
-    if not torch.cuda.is_available():
-        print(json.dumps({"error": "no HIP device visible"}))
-        sys.exit(1)
-    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
-             "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
-             "prefill": bench_prefill, "rope-append": bench_rope_append}
-    if args.workload in extra:
-        extra[args.workload](args)
-        return
-    steps, warmup = args.steps, args.warmup
-    w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition)
 
     for s in range(warmup):  # rewrites the same cells with the same data: state unchanged
         w.append(s)
@@ -714,10 +707,55 @@ def main():
     total_ms = ev[0][0].elapsed_time(ev[-1][2])
     app_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
     att_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    return total_ms * 1e3 / steps, float(att_ms.mean() * 1e3), float(app_ms.mean() * 1e3), wall
 
-    us_step = total_ms * 1e3 / steps
-    att_us = float(att_ms.mean() * 1e3)
-    app_us = float(app_ms.mean() * 1e3)
+
+def bench_decode_q8(args):
+    """The Llama-3-8B decode step on a q8_0 KV cache (int8 quants plus one f16
+    scale per 32 elements: 1.06 bytes per element instead of 2)."""
+    steps, warmup = args.steps, args.warmup
+    w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition, dtype="q8_0")
+    us_step, att_us, app_us, wall = _time_decode(w, steps, warmup)
+    att_bytes = float(np.mean([w.attention_bytes(s) for s in range(steps)]))
+    att_gbps = att_bytes / (att_us * 1e-6) / 1e9
+    app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9
+    line = {
+        "workload": "decode-q8 llama3-8b-layer: 32q/8kv heads, head_dim 128, q8_0 KV, 64 seqs ctx "
+                    "U[2048,4096], 1 append + 1 decode attention per step",
+        "steps": steps, "step_us": round(us_step, 2),
+        "attention_us": round(att_us, 2), "attention_bytes": round(att_bytes),
+        "attention_GBps": round(att_gbps, 1), "attention_frac": round(att_gbps / PEAK_HBM_GBPS, 4),
+        "append_us": round(app_us, 2), "append_GBps": round(app_gbps, 1),
+        "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4), "wall_s": round(wall, 3),
+    }
+    if not args.no_cpu:
+        threads = _cpu_threads(args.cpu_threads)
+        cpu_us, n = cpu_baseline(w, threads, min(args.cpu_seconds, 10.0))
+        line["cpu_baseline"] = {"value": round(cpu_us, 1), "unit": "µs/step", "cores": threads, "kind": "port",
+                                "sample": f"{n} decode steps of the same workload on the oracle's q8_0 mode"}
+    print(json.dumps(line), flush=True)
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                          "(the path shards by sequence across GPUs with no exchange)"}))
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
+             "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
+             "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8}
+    if args.workload in extra:
+        extra[args.workload](args)
+        return
+    steps, warmup = args.steps, args.warmup
+    w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition)
+    us_step, att_us, app_us, wall = _time_decode(w, steps, warmup)
     att_bytes = float(np.mean([w.attention_bytes(s) for s in range(steps)]))
     att_gbps = att_bytes / (att_us * 1e-6) / 1e9
     app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9

@@ -63,8 +63,14 @@ enum {
 #define LTKV_NO_DEVICE (-1)
 
 /* Storage element type. F16 is the reference's (kv.rs:5-6); F32 stores the
- * f32 input unrounded (same algorithm without the rounding step). */
-enum { LTKV_F16 = 0, LTKV_F32 = 1 };
+ * f32 input unrounded (same algorithm without the rounding step). Q8_0
+ * stores each 32-element run of a row as 32 int8 quants plus an f16 scale d
+ * (the Q8_0 block of quant.rs:188-193, quantised as quant.rs:785-791 and
+ * read back as d * q): quants in the K/V pools ([n_blocks][16][kv_dim]
+ * bytes), scales in K/V scale pools ([n_blocks][16][kv_dim/32] f16).
+ * kv_dim must be a multiple of 32. Gather, rows and the RoPE append have no
+ * Q8_0 form (LTKV_ERR_ARG). */
+enum { LTKV_F16 = 0, LTKV_F32 = 1, LTKV_Q8_0 = 2 };
 
 /* Thread-local message of the last failing call on this thread. */
 LTKV_API const char *ltkv_last_error(void);
@@ -85,7 +91,7 @@ LTKV_API int ltkv_set_stream(ltkv_cache *c, void *hip_stream);
 /* ---- queries (kv.rs:50-60,185-187) ------------------------------------- */
 
 LTKV_API size_t ltkv_capacity(const ltkv_cache *c);    /* KvCache::capacity: n_blocks*16 */
-LTKV_API size_t ltkv_bytes(const ltkv_cache *c);       /* KvCache::bytes: K+V pool bytes */
+LTKV_API size_t ltkv_bytes(const ltkv_cache *c);       /* KvCache::bytes: K+V pool (and scale pool) bytes */
 LTKV_API size_t ltkv_len(const ltkv_cache *c, uint32_t seq); /* KvCache::len (0 if unknown) */
 LTKV_API size_t ltkv_free_blocks(const ltkv_cache *c); /* KvCache::free_blocks */
 LTKV_API size_t ltkv_n_blocks(const ltkv_cache *c);
@@ -136,8 +142,10 @@ LTKV_API int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n
 /* Kernel 1, slot-mapped append: KvCache::write (kv.rs:123-131) for n rows,
  * as the per-token loop of model.rs:414-429. Row i of d_k/d_v (f32, row
  * stride src_stride >= kv_dim elements) goes to cell d_slot_mapping[i] =
- * block*16+slot of `layer`, rounded f32->f16 RNE (F16) or stored as is
- * (F32). Negative or out-of-range slots are skipped. */
+ * block*16+slot of `layer`, rounded f32->f16 RNE (F16), stored as is
+ * (F32) or quantised per 32 elements (Q8_0: amax = max |x| ignoring NaN,
+ * d = amax / 127, q = round-half-away(x / d) saturated to int8, NaN -> 0,
+ * d stored as f16 RNE). Negative or out-of-range slots are skipped. */
 LTKV_API int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
                const float *d_k, const float *d_v, size_t src_stride);
 
@@ -229,6 +237,10 @@ LTKV_API int ltkv_plan_stats(const ltkv_cache *c, uint64_t out[6]);
 
 /* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */
 LTKV_API int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v);
+
+/* Copy one layer's K and V scale pools ([n_blocks][16][kv_dim/32] f16 bits)
+ * of a Q8_0 cache to host. */
+LTKV_API int ltkv_read_scales(ltkv_cache *c, size_t layer, uint16_t *h_k, uint16_t *h_v);
 
 /* KvCache::rows(layer, seq, n) collected to host [n][kv_dim] buffers. */
 LTKV_API int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v);

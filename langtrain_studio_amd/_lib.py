@@ -12,7 +12,7 @@ import os
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libltkv.so")
 
 OK, ERR_FULL, ERR_NONCONTIG, ERR_RANGE, ERR_HIP, ERR_ARG = 0, 1, 2, 3, 4, 5
-F16, F32 = 0, 1
+F16, F32, Q8_0 = 0, 1, 2
 NO_DEVICE = -1
 BLOCK = 16
 
@@ -52,6 +52,7 @@ SIGNATURES = {
     "ltkv_planned_attention": (_int, [_vp, _sz, _f32, _vp, _vp]),
     "ltkv_plan_stats": (_int, [_vp, _vp]),
     "ltkv_read_pool": (_int, [_vp, _sz, _vp, _vp]),
+    "ltkv_read_scales": (_int, [_vp, _sz, _vp, _vp]),
     "ltkv_rows": (_int, [_vp, _sz, _u32, _sz, _vp, _vp]),
     "ltkv_write_row": (_int, [_vp, _sz, _u32, _u32, _vp, _vp]),
     "ltkv_synchronize": (_int, [_vp]),

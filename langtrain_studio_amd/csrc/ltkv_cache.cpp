@@ -101,6 +101,9 @@ struct ltkv_cache {
   size_t n_layers = 0, kv_dim = 0, n_blocks = 0, elem = 2;
   ltkv::PoolGeom geom{};
   void *k = nullptr, *v = nullptr;  // [layer][block][slot][kv_dim]
+  // Q8_0: per-32-element f16 scales, [layer][block][slot][kv_dim / 32].
+  void *ks = nullptr, *vs = nullptr;
+  ltkv::PoolGeom sgeom{};  // the scale pools as a pool of 2-byte elements
   hipStream_t stream = nullptr;
 
   std::vector<uint32_t> refs;   // kv.rs:23
@@ -133,6 +136,10 @@ struct ltkv_cache {
   size_t layer_elems() const { return n_blocks * LTKV_BLOCK * kv_dim; }
   uint8_t *k_layer(size_t l) const { return (uint8_t *)k + l * layer_elems() * elem; }
   uint8_t *v_layer(size_t l) const { return (uint8_t *)v + l * layer_elems() * elem; }
+  bool q8() const { return dtype == LTKV_Q8_0; }
+  size_t layer_scales() const { return n_blocks * LTKV_BLOCK * (kv_dim / 32); }
+  uint16_t *k_scales(size_t l) const { return ks ? (uint16_t *)ks + l * layer_scales() : nullptr; }
+  uint16_t *v_scales(size_t l) const { return vs ? (uint16_t *)vs + l * layer_scales() : nullptr; }
 
   bool alloc(int32_t *b) {  // kv.rs:67-74
     if (free.empty()) return false;
@@ -212,6 +219,9 @@ struct ltkv_cache {
     pairs_in_flight = true;
     HIP_TRY(ltkv::launch_copy_blocks(geom, (int)n_layers, k, v, d_pairs, (int64_t)n, stream),
             "copy_blocks launch");
+    if (q8())
+      HIP_TRY(ltkv::launch_copy_blocks(sgeom, (int)n_layers, ks, vs, d_pairs, (int64_t)n, stream),
+              "copy_blocks launch (scales)");
     return LTKV_OK;
   }
 
@@ -283,6 +293,8 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   ltkv::AttnArgs a{};
   a.k_layer = c->k_layer(layer);
   a.v_layer = c->v_layer(layer);
+  a.k_scale = c->k_scales(layer);
+  a.v_scale = c->v_scales(layer);
   a.q = d_q;
   a.out = d_out;
   a.part_o = ws.bytes ? (float *)(c->ws + ws.part_o_off) : nullptr;
@@ -632,7 +644,10 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
   *out = nullptr;
   if (n_layers == 0 || kv_dim == 0 || kv_dim % 8 != 0)
     return fail(LTKV_ERR_ARG, "n_layers must be > 0 and kv_dim a positive multiple of 8");
-  if (dtype != LTKV_F16 && dtype != LTKV_F32) return fail(LTKV_ERR_ARG, "dtype must be F16 or F32");
+  if (dtype != LTKV_F16 && dtype != LTKV_F32 && dtype != LTKV_Q8_0)
+    return fail(LTKV_ERR_ARG, "dtype must be F16, F32 or Q8_0");
+  if (dtype == LTKV_Q8_0 && kv_dim % 32 != 0)
+    return fail(LTKV_ERR_ARG, "Q8_0 needs kv_dim a multiple of 32 (one scale per 32 elements)");
   const size_t n_blocks = (n_tokens + LTKV_BLOCK - 1) / LTKV_BLOCK;  // kv.rs:36
   if (n_blocks > (size_t)INT32_MAX / LTKV_BLOCK)
     return fail(LTKV_ERR_ARG, "n_tokens too large for 32-bit cell indices");
@@ -650,13 +665,18 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
   c->n_layers = n_layers;
   c->kv_dim = kv_dim;
   c->n_blocks = n_blocks;
-  c->elem = dtype == LTKV_F16 ? 2 : 4;
+  c->elem = dtype == LTKV_F16 ? 2 : dtype == LTKV_F32 ? 4 : 1;
   c->geom.n_blocks = (int64_t)n_blocks;
   c->geom.block_stride = (int64_t)(LTKV_BLOCK * kv_dim);
   c->geom.slot_stride = (int64_t)kv_dim;
   c->geom.head_stride = 0;  // token-major: set per call from head_dim
   c->geom.kv_dim = (int)kv_dim;
   c->geom.elem = (int)c->elem;
+  c->sgeom = c->geom;
+  c->sgeom.block_stride = (int64_t)(LTKV_BLOCK * (kv_dim / 32));
+  c->sgeom.slot_stride = (int64_t)(kv_dim / 32);
+  c->sgeom.kv_dim = (int)(kv_dim / 32);
+  c->sgeom.elem = 2;
   c->refs.assign(n_blocks, 0);
   c->free.reserve(n_blocks);
   for (size_t b = n_blocks; b-- > 0;) c->free.push_back((int32_t)b);  // (0..n).rev()
@@ -682,6 +702,13 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
     else if ((e = hipMalloc(&c->v, bytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(V pool)");
     else if ((e = hipMemset(c->k, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K pool)");
     else if ((e = hipMemset(c->v, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
+  }
+  const size_t sbytes = c->q8() ? n_layers * c->layer_scales() * 2 : 0;
+  if (rc == LTKV_OK && sbytes > 0) {
+    if ((e = hipMalloc(&c->ks, sbytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(K scales)");
+    else if ((e = hipMalloc(&c->vs, sbytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(V scales)");
+    else if ((e = hipMemset(c->ks, 0, sbytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K scales)");
+    else if ((e = hipMemset(c->vs, 0, sbytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V scales)");
   }
   if (rc == LTKV_OK && (e = hipEventCreateWithFlags(&c->pairs_done, hipEventDisableTiming)) != hipSuccess)
     rc = hip_fail(e, "hipEventCreate");
@@ -709,6 +736,8 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->plan.d) (void)hipFree(c->plan.d);
     if (c->k) (void)hipFree(c->k);
     if (c->v) (void)hipFree(c->v);
+    if (c->ks) (void)hipFree(c->ks);
+    if (c->vs) (void)hipFree(c->vs);
   }
   delete c;
 }
@@ -721,7 +750,8 @@ int ltkv_set_stream(ltkv_cache *c, void *hip_stream) {
 
 size_t ltkv_capacity(const ltkv_cache *c) { return c ? c->n_blocks * LTKV_BLOCK : 0; }
 size_t ltkv_bytes(const ltkv_cache *c) {
-  return c ? 2 * c->n_layers * c->layer_elems() * c->elem : 0;
+  if (!c) return 0;
+  return 2 * c->n_layers * (c->layer_elems() * c->elem + (c->q8() ? c->layer_scales() * 2 : 0));
 }
 size_t ltkv_len(const ltkv_cache *c, uint32_t seq) {
   if (!c) return 0;
@@ -829,9 +859,15 @@ int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapp
     return fail(LTKV_ERR_ARG, "too many rows for one launch");
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  HIP_TRY(ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping, d_k,
-                             d_v, (int64_t)n, (int64_t)src_stride, c->stream),
-          "write launch");
+  if (c->q8())
+    HIP_TRY(ltkv::launch_write_q8(c->geom, c->k_layer(layer), c->v_layer(layer), c->k_scales(layer),
+                                  c->v_scales(layer), d_slot_mapping, d_k, d_v, (int64_t)n,
+                                  (int64_t)src_stride, c->stream),
+            "write launch");
+  else
+    HIP_TRY(ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping, d_k,
+                               d_v, (int64_t)n, (int64_t)src_stride, c->stream),
+            "write launch");
   return LTKV_OK;
 }
 
@@ -882,6 +918,7 @@ int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
   if (!c->rope) return fail(LTKV_ERR_ARG, "no RoPE table (ltkv_rope_init)");
+  if (c->q8()) return fail(LTKV_ERR_ARG, "the RoPE append has no Q8_0 form");
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
   if (n == 0) return LTKV_OK;
   if (!d_slot_mapping || !d_positions || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
@@ -912,6 +949,10 @@ int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   HIP_TRY(ltkv::launch_copy_blocks(c->geom, (int)c->n_layers, c->k, c->v, d_pairs, (int64_t)n, c->stream),
           "copy_blocks launch");
+  if (c->q8())
+    HIP_TRY(ltkv::launch_copy_blocks(c->sgeom, (int)c->n_layers, c->ks, c->vs, d_pairs, (int64_t)n,
+                                     c->stream),
+            "copy_blocks launch (scales)");
   return LTKV_OK;
 }
 
@@ -921,6 +962,7 @@ int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (c->q8()) return fail(LTKV_ERR_ARG, "gather has no Q8_0 form");
   if (n == 0 || table_stride == 0) return LTKV_OK;
   if (!d_tables || !d_lens || !d_out_offsets || !d_k_out || !d_v_out)
     return fail(LTKV_ERR_ARG, "null device pointer");
@@ -1116,9 +1158,25 @@ int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v) {
   return LTKV_OK;
 }
 
+int ltkv_read_scales(ltkv_cache *c, size_t layer, uint16_t *h_k, uint16_t *h_v) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (!c->q8()) return fail(LTKV_ERR_ARG, "only Q8_0 caches have scale pools");
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  if (!h_k || !h_v) return fail(LTKV_ERR_ARG, "null host pointer");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  const size_t bytes = c->layer_scales() * 2;
+  HIP_TRY(hipMemcpyAsync(h_k, c->k_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read K scales");
+  HIP_TRY(hipMemcpyAsync(h_v, c->v_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read V scales");
+  HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  return LTKV_OK;
+}
+
 int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v) {
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (c->q8()) return fail(LTKV_ERR_ARG, "rows has no Q8_0 form (ltkv_read_pool, ltkv_read_scales)");
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
   if (n == 0) return LTKV_OK;
   if (!h_k || !h_v) return fail(LTKV_ERR_ARG, "null host pointer");
@@ -1176,7 +1234,11 @@ int ltkv_write_row(ltkv_cache *c, size_t layer, uint32_t block, uint32_t slot, c
   uint8_t *d = nullptr;
   HIP_TRY(hipMalloc((void **)&d, total), "hipMalloc(row staging)");
   hipError_t e = hipMemcpyAsync(d, h.data(), total, hipMemcpyHostToDevice, c->stream);
-  if (e == hipSuccess)
+  if (e == hipSuccess && c->q8())
+    e = ltkv::launch_write_q8(c->geom, c->k_layer(layer), c->v_layer(layer), c->k_scales(layer),
+                              c->v_scales(layer), (const int32_t *)d, (const float *)(d + 16),
+                              (const float *)(d + 16 + row), 1, (int64_t)c->kv_dim, c->stream);
+  else if (e == hipSuccess)
     e = ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), (const int32_t *)d,
                            (const float *)(d + 16), (const float *)(d + 16 + row), 1,
                            (int64_t)c->kv_dim, c->stream);

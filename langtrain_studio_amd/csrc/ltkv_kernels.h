@@ -17,8 +17,14 @@ struct PoolGeom {
   int64_t slot_stride;   // elements between consecutive slots of a block
   int64_t head_stride;   // elements between consecutive kv heads of a block
   int kv_dim;
-  int elem;              // bytes per element: 2 (f16) or 4 (f32)
+  int elem;              // bytes per element: 1 (q8_0 quants), 2 (f16) or 4 (f32)
 };
+
+// Kernel 1 for q8_0 cells (elem 1): quants into k/v_layer, per-32 f16 scales
+// into k/v_scale ([cell][kv_dim / 32]).
+hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale,
+                           void *v_scale, const int32_t *slots, const float *k, const float *v,
+                           int64_t n, int64_t src_stride, hipStream_t s);
 
 hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
                         const float *k, const float *v, int64_t n, int64_t src_stride,
@@ -47,6 +53,7 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
 
 struct AttnArgs {
   const void *k_layer, *v_layer;
+  const void *k_scale, *v_scale;  // q8_0 pools: per-32 f16 scales of the layer, else null
   const float *q;
   const int32_t *tables;
   int64_t table_stride;

@@ -89,6 +89,62 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
 }
 
 // ----------------------------------------------------------------------------
+// Kernel 1 for q8_0 cells: one thread quantises one 32-element block of a K
+// or V row as quantize_block (quant.rs:785-791): d = max|x| / 127 (NaN
+// ignored, as f32::max), q = round-half-away(x / d) saturated to int8 (NaN
+// -> 0, as `as i8`); the 32 quants go to the cell and d, rounded to f16, to
+// the scale pool (the Q8_0 block of quant.rs:188-193: f16 d + 32 int8).
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
+                uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
+                const float *__restrict__ k, const float *__restrict__ v, int64_t n, int64_t src_stride,
+                int kv_dim, int64_t n_slots) {
+  const int per = kv_dim >> 4;  // 32-element blocks of K and of V per row
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / per;
+  if (row >= n) return;
+  const int u = (int)(gid - row * per);
+  const int32_t s = slots[row];
+  if (s < 0 || (int64_t)s >= n_slots) return;
+  const bool is_v = u >= (per >> 1);
+  const int blk = is_v ? u - (per >> 1) : u;
+  const float *src = (is_v ? v : k) + row * src_stride + blk * 32;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; i += 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4 *>(src + i);
+    x[i] = t.x;
+    x[i + 1] = t.y;
+    x[i + 2] = t.z;
+    x[i + 3] = t.w;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
+  const float d = amax / 127.f;
+  const float id = d > 0.f ? 1.f / d : 0.f;
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float r = __builtin_roundf(x[4 * i + j] * id);  // half away from zero
+      int qv = 0;
+      if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
+      word |= (uint32_t)(qv & 0xff) << (8 * j);
+    }
+    w[i] = word;
+  }
+  const int64_t cell = (int64_t)s * kv_dim + blk * 32;
+  int8_t *dq = (is_v ? vpool : kpool) + cell;
+  *reinterpret_cast<u32x4 *>(dq) = u32x4{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<u32x4 *>(dq + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  (is_v ? vscale : kscale)[(int64_t)s * (kv_dim >> 5) + blk] = (uint16_t)f16_bits(d);
+}
+
+// ----------------------------------------------------------------------------
 // Kernel 1 fused with RoPE (model.rs:291-308 then kv.rs:123-131): one launch
 // rotates Q in place and K on its way into the pool, and appends V. A thread
 // owns one unit of a head: 4 rotation pairs (8 elements: (2i, 2i+1) pairs
@@ -344,6 +400,28 @@ struct Tile<float> {
   }
 };
 
+typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
+
+template <>
+struct Tile<int8_t> {  // q8_0 quants, 8 per 8-byte load: the block scale is applied by the caller
+  static constexpr int E = 8;
+  __device__ static __forceinline__ void unpack(const u32x2 &u, float (&f)[8]) {
+    const i8x8 b = __builtin_bit_cast(i8x8, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)b[i];
+  }
+};
+
+// Register vector of one lane's load of a tile row: 16 bytes, 8 for q8_0.
+template <typename T>
+struct TileVec {
+  using type = u32x4;
+};
+template <>
+struct TileVec<int8_t> {
+  using type = u32x2;
+};
+
 constexpr int kAttnWaves = 4;
 constexpr int kBufferWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9-family raw buffers
 constexpr int kNt = 2;                    // buffer load cache policy: non-temporal
@@ -357,9 +435,11 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
             int max_parts, const int32_t *__restrict__ pre_parts,
-            const int32_t *__restrict__ qmap) {
+            const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
+            const uint16_t *__restrict__ vscale) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
+  constexpr bool Q8 = std::is_same_v<T, int8_t>;  // q8_0: per-32 f16 scales in kscale/vscale
   constexpr int RPL = 64 / L;      // rows per wave load
   constexpr int LOADS = 16 / RPL;  // wave loads per 16-row tile
   static_assert(L >= 4 && L <= 32 && LOADS >= 1, "unsupported head_dim / dtype");
@@ -416,19 +496,30 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
   const int64_t head_off = (int64_t)kvh * head_stride;
 
-  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
+  // q8_0: a lane's E = 16 elements lie in one 32-element block; its scale
+  // sits at cell * (kv_dim / 32) + (head_off + c * E) / 32 of the scale pool.
+  const int64_t sl_stride = slot_stride >> 5;
+  const int64_t sl_lane = (head_off + c * E) >> 5;
+  float ksc[2][LOADS], vsc[2][LOADS];  // scales of the two tiles in flight (q8_0 only)
+  using TV = typename TileVec<T>::type;
+  auto load_tile = [&](int b, TV (&kr)[LOADS], TV (&vr)[LOADS], int st) {
     int32_t blk = tab[b];
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
     const int64_t base = (int64_t)blk * block_stride + head_off + lane_off;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int64_t o = base + (int64_t)j * RPL * slot_stride;
-      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kpool + o));
-      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vpool + o));
+      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(kpool + o));
+      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(vpool + o));
+      if constexpr (Q8) {
+        const int64_t so = ((int64_t)blk * 16 + rg + j * RPL) * sl_stride + sl_lane;
+        ksc[st][j] = (float)__builtin_bit_cast(_Float16, kscale[so]);
+        vsc[st][j] = (float)__builtin_bit_cast(_Float16, vscale[so]);
+      }
     }
   };
 
-  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
+  auto compute_tile = [&](int b, const TV (&kr)[LOADS], const TV (&vr)[LOADS], int st) {
     const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     float s[LOADS][G];
 #pragma unroll
@@ -440,6 +531,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
         float a = 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) a = __builtin_fmaf(qv[h][e], kf[e], a);
+        if constexpr (Q8) a *= ksc[st][j];  // dot(q, d * k) = d * dot(q, k) within the block
         s[j][h] = group_sum<L>(a);
       }
     }
@@ -474,14 +566,18 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
     for (int j = 0; j < LOADS; ++j) {
       float vf[E];
       Tile<T>::unpack(vr[j], vf);
-      if (valid < 16 && rg + j * RPL >= valid) {
+      const bool stale = valid < 16 && rg + j * RPL >= valid;
+      if (stale) {
 #pragma unroll
         for (int e = 0; e < E; ++e) vf[e] = 0.f;  // stale slots may hold non-finite bits
       }
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+      for (int h = 0; h < G; ++h) {
+        float w = p[j][h];
+        if constexpr (Q8) w = stale ? 0.f : w * vsc[st][j];  // weight times the V block scale
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(p[j][h], vf[e], acc[h][e]);
+        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
+      }
     }
   };
 
@@ -489,18 +585,18 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   // one is computed. Past the end the prefetch re-reads the current tile
   // (cache hit) so the wait counts stay static.
   {
-    u32x4 ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
+    TV ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
     int b = b0 + wave;
-    if (b < b1) load_tile(b, ka, va);
+    if (b < b1) load_tile(b, ka, va, 0);
     while (b < b1) {
       const int bn = b + kAttnWaves < b1 ? b + kAttnWaves : b;
-      load_tile(bn, kb, vb);
-      compute_tile(b, ka, va);
+      load_tile(bn, kb, vb, 1);
+      compute_tile(b, ka, va, 0);
       b += kAttnWaves;
       if (b >= b1) break;
       const int bn2 = b + kAttnWaves < b1 ? b + kAttnWaves : b;
-      load_tile(bn2, ka, va);
-      compute_tile(b, kb, vb);
+      load_tile(bn2, ka, va, 0);
+      compute_tile(b, kb, vb, 1);
       b += kAttnWaves;
     }
   }
@@ -770,9 +866,12 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
               int max_parts, const int32_t *__restrict__ pre_parts,
-              const int32_t *__restrict__ qmap) {
+              const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
+              const uint16_t *__restrict__ vscale) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
+  using TV = typename TileVec<T>::type;
+  constexpr bool Q8 = std::is_same_v<T, int8_t>;  // q8_0: per-32 f16 scales in kscale/vscale
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
   constexpr int GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;  // group padded to a power of two
   // Groups of 8 heads scatter the tile in two passes of two row slots, which
@@ -855,10 +954,16 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   // Per-lane byte offsets inside a head tile, fixed for the whole loop.
   const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
-  const uint32_t col_off = (uint32_t)(c * 16);
+  const uint32_t col_off = (uint32_t)(c * (int)sizeof(TV));
   uint32_t roff[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) roff[j] = (uint32_t)(rg + RPL * j) * row_bytes + col_off;
+  // q8_0: a lane's 8 elements lie in one 32-element block; its f16 scale sits
+  // at cell * (kv_dim / 32) + (head offset + 8 c) / 32 of the scale pool.
+  const uint32_t srow_bytes = (uint32_t)(slot_stride >> 5) * 2;
+  const uint32_t scol = (uint32_t)(c * E >> 5) * 2;  // inside the head's scales
+  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 2;
+  float ksc[3][LOADS], vsc[3][LOADS];  // scales of the tiles in flight (q8_0 only)
   int my_row[NPL];  // tile rows of this lane's scores after the scatter
   {
     int jj = 0;
@@ -885,7 +990,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   // row inside the context: rows past it (and every row of a prefetch past
   // the wave's last tile, extent 0) read as zeros without touching memory,
   // so every load is unconditional and the wait counts stay static.
-  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
+  auto load_tile = [&](int b, TV (&kr)[LOADS], TV (&vr)[LOADS], int st) {
     const int bb = b < b1 ? b : b1 - 1;
     int32_t blk = tab[bb];
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
@@ -898,12 +1003,31 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
         (void *)(vbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      kr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, roff[j], 0, kNt));
-      vr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, roff[j], 0, kNt));
+      if constexpr (sizeof(TV) == 16) {
+        kr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b128(rk, roff[j], 0, kNt));
+        vr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b128(rv, roff[j], 0, kNt));
+      } else {
+        kr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b64(rk, roff[j], 0, kNt));
+        vr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b64(rv, roff[j], 0, kNt));
+      }
+    }
+    if constexpr (Q8) {  // the rows' block scales, zero past the context (extent)
+      const int sext = rows > 0 ? (rows - 1) * (int)srow_bytes + HD / 32 * 2 : 0;
+      const int64_t sblk = (int64_t)blk * 16 * (int64_t)srow_bytes + shead;
+      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
+      const __amdgpu_buffer_rsrc_t sv = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t so = (uint32_t)(rg + RPL * j) * srow_bytes + scol;
+        ksc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sk, so, 0, 0));
+        vsc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sv, so, 0, 0));
+      }
     }
   };
 
-  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
+  auto compute_tile = [&](int b, const TV (&kr)[LOADS], const TV (&vr)[LOADS], int st) {
     const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     float sc[NPL];  // this lane's scores: one per pass
 #pragma unroll
@@ -933,6 +1057,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
           float a = 0.f;
 #pragma unroll
           for (int e = 0; e < E; ++e) a = __builtin_fmaf(qu[e], kf[jj][e], a);
+          if constexpr (Q8) a *= ksc[st][pass * RPP + jj];  // the lane's block scale
           v[u * RPP + jj] = a;
         }
       }
@@ -978,7 +1103,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
       static_for<0, G>([&](auto hc) {
         constexpr int h = decltype(hc)::value;
         // (head h, row slot j): pass j / RPP, index h * RPP + j % RPP of it
-        const float w = bcast16<S::src(h * RPP + j % RPP)>(p[j / RPP]);
+        float w = bcast16<S::src(h * RPP + j % RPP)>(p[j / RPP]);
+        if constexpr (Q8) w *= vsc[st][j];  // the V row's block scale for this lane
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
       });
@@ -993,29 +1119,29 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     int b = b0 + wave;
     if (b < b1) {
       if constexpr (STAGES == 3) {
-        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS], k2[LOADS], v2[LOADS];
-        load_tile(b, k0, v0);
-        load_tile(b + W, k1, v1);
+        TV k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS], k2[LOADS], v2[LOADS];
+        load_tile(b, k0, v0, 0);
+        load_tile(b + W, k1, v1, 1);
         for (;;) {
-          load_tile(b + 2 * W, k2, v2);
-          compute_tile(b, k0, v0);
+          load_tile(b + 2 * W, k2, v2, 2);
+          compute_tile(b, k0, v0, 0);
           if ((b += W) >= b1) break;
-          load_tile(b + 2 * W, k0, v0);
-          compute_tile(b, k1, v1);
+          load_tile(b + 2 * W, k0, v0, 0);
+          compute_tile(b, k1, v1, 1);
           if ((b += W) >= b1) break;
-          load_tile(b + 2 * W, k1, v1);
-          compute_tile(b, k2, v2);
+          load_tile(b + 2 * W, k1, v1, 1);
+          compute_tile(b, k2, v2, 2);
           if ((b += W) >= b1) break;
         }
       } else {
-        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
-        load_tile(b, k0, v0);
+        TV k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
+        load_tile(b, k0, v0, 0);
         for (;;) {
-          load_tile(b + W, k1, v1);
-          compute_tile(b, k0, v0);
+          load_tile(b + W, k1, v1, 1);
+          compute_tile(b, k0, v0, 0);
           if ((b += W) >= b1) break;
-          load_tile(b + W, k0, v0);
-          compute_tile(b, k1, v1);
+          load_tile(b + W, k0, v0, 0);
+          compute_tile(b, k1, v1, 1);
           if ((b += W) >= b1) break;
         }
       }
@@ -1124,7 +1250,8 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
           static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
           a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
           g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens,
-          a.max_parts, a.pre_parts, a.qmap);
+          a.max_parts, a.pre_parts, a.qmap,
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
       return launch_merge<HD>(a, s);
     }
   }
@@ -1132,7 +1259,8 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap);
+      a.pre_parts, a.qmap,
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
   return launch_merge<HD>(a, s);
 }
 
@@ -1143,7 +1271,8 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap);
+      a.pre_parts, a.qmap,
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
   return launch_merge<HD>(a, s);
 }
 
@@ -1501,6 +1630,18 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
 
 }  // namespace
 
+hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale,
+                           void *v_scale, const int32_t *slots, const float *k, const float *v,
+                           int64_t n, int64_t src_stride, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t threads = n * (g.kv_dim >> 4);
+  const int64_t blocks = (threads + 255) / 256;
+  write_q8_kernel<<<(unsigned)blocks, 256, 0, s>>>(
+      static_cast<int8_t *>(k_layer), static_cast<int8_t *>(v_layer), static_cast<uint16_t *>(k_scale),
+      static_cast<uint16_t *>(v_scale), slots, k, v, n, src_stride, g.kv_dim, g.n_blocks * 16);
+  return hipGetLastError();
+}
+
 hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
                         const float *k, const float *v, int64_t n, int64_t src_stride,
                         hipStream_t s) {
@@ -1583,13 +1724,16 @@ AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_
 }
 
 bool attention_supported(int elem, int head_dim, int group) {
-  return (elem == 2 || elem == 4) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
+  return (elem == 1 || elem == 2 || elem == 4) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
          group <= 8;
 }
 
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  if (g.elem == 2) {
+  if (g.elem == 1) {
+    if (a.head_dim == 64) return launch_attn_hd<int8_t, 64>(g, a, s);
+    if (a.head_dim == 128) return launch_attn_hd<int8_t, 128>(g, a, s);
+  } else if (g.elem == 2) {
     if (a.head_dim == 64) return launch_attn_hd<_Float16, 64>(g, a, s);
     if (a.head_dim == 128) return launch_attn_hd<_Float16, 128>(g, a, s);
   } else {

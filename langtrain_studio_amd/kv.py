@@ -69,24 +69,25 @@ class KvCache:
     """kv.rs KvCache with its pools in HBM.
 
     ``KvCache(n_layers, kv_dim, n_tokens)`` is ``KvCache::new`` (kv.rs:35-48);
-    ``dtype`` selects the storage ("f16" as the reference, or "f32") and
-    ``device`` the HIP device (``None`` = a metadata-only cache with no
+    ``dtype`` selects the storage ("f16" as the reference, "f32", or
+    "q8_0": int8 quants with one f16 scale per 32 elements, quant.rs:785-791)
+    and ``device`` the HIP device (``None`` = a metadata-only cache with no
     pools, whose device ops raise).
     """
 
     def __init__(self, n_layers: int, kv_dim: int, n_tokens: int, dtype: str = "f16",
                  device: Optional[int] = 0, stream=None):
-        if dtype not in ("f16", "f32"):
-            raise ValueError("dtype must be 'f16' or 'f32'")
+        codes = {"f16": _lib.F16, "f32": _lib.F32, "q8_0": _lib.Q8_0}
+        if dtype not in codes:
+            raise ValueError("dtype must be 'f16', 'f32' or 'q8_0'")
         self._lib = _lib.load()
         h = C.c_void_p()
         dev = _lib.NO_DEVICE if device is None else int(device)
-        _check(self._lib.ltkv_create(n_layers, kv_dim, n_tokens, _lib.F16 if dtype == "f16" else _lib.F32,
-                                     dev, C.byref(h)))
+        _check(self._lib.ltkv_create(n_layers, kv_dim, n_tokens, codes[dtype], dev, C.byref(h)))
         self._h = h
         self.n_layers = n_layers
         self.dtype = dtype
-        self.elem = 2 if dtype == "f16" else 4
+        self.elem = {"f16": 2, "f32": 4, "q8_0": 1}[dtype]
         self.device = device
         self.n_blocks = self._lib.ltkv_n_blocks(h)
         self._plan_shape = None
@@ -261,7 +262,7 @@ class KvCache:
         """Kernel 3: rows 0..lens[i] of each table to k_out/v_out rows out_offsets[i]..."""
         import torch
 
-        dt = torch.float16 if self.elem == 2 else torch.float32
+        dt = {1: torch.int8, 2: torch.float16, 4: torch.float32}[self.elem]
         n = lens.numel()
         if tables.dim() != 2 or tables.shape[0] != n or out_offsets.numel() != n:
             raise ValueError("tables must be [n][stride]; lens and out_offsets [n]")
@@ -342,12 +343,22 @@ class KvCache:
         _check(self._lib.ltkv_set_attention_partition(self._h, tokens))
 
     def read_pool(self, layer: int = 0) -> tuple[np.ndarray, np.ndarray]:
-        """Raw K and V pools of one layer, [n_blocks][16][kv_dim] on the host."""
-        dt = np.uint16 if self.elem == 2 else np.float32
+        """Raw K and V pools of one layer, [n_blocks][16][kv_dim] on the host
+        (f16 bits as uint16, float32, or q8_0 quants as int8)."""
+        dt = {1: np.int8, 2: np.uint16, 4: np.float32}[self.elem]
         shape = (self.n_blocks, BLOCK, self.kv_dim)
         k = np.empty(shape, dtype=dt)
         v = np.empty(shape, dtype=dt)
         _check(self._lib.ltkv_read_pool(self._h, layer, _np_ptr(k), _np_ptr(v)))
+        return k, v
+
+    def read_scales(self, layer: int = 0) -> tuple[np.ndarray, np.ndarray]:
+        """K and V scale pools of one layer of a q8_0 cache,
+        [n_blocks][16][kv_dim/32] f16 bits (uint16) on the host."""
+        shape = (self.n_blocks, BLOCK, self.kv_dim // 32)
+        k = np.empty(shape, dtype=np.uint16)
+        v = np.empty(shape, dtype=np.uint16)
+        _check(self._lib.ltkv_read_scales(self._h, layer, _np_ptr(k), _np_ptr(v)))
         return k, v
 
     def synchronize(self) -> None:

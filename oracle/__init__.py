@@ -6,4 +6,4 @@ ltkv_oracle.cpp for the reference file:line each function restates.
 """
 
 from .oracle import (OracleError, OracleKv, f16_to_f32, f32_to_f16, has_f16c, load,  # noqa: F401
-                     pool_selftest)
+                     pool_selftest, quantize_block)

@@ -17,9 +17,16 @@
 //   * engine/crates/native/src/pool.rs:14,77-167,188-199  spin-then-park pool
 //     that runs the attention tasks.
 //
+//   * engine/crates/native/src/quant.rs:785-791  quantize_block (int8 per 32
+//     elements, scale amax / 127) and quant.rs:188-193 (Q8_0 block: f16 d
+//     then 32 int8, read back as d * q) for the Q8_0 storage mode.
+//
 // Storage dtype: the reference stores f16 only (kv.rs:5-6,21-22). Mode F32
 // is the same algorithm with the rounding step removed (no reference
-// counterpart; used by the TinyLlama-shaped f32 workload).
+// counterpart; used by the TinyLlama-shaped f32 workload). Mode Q8_0 stores
+// each row as Q8_0 blocks (the KV cache type of the engine's llama.cpp
+// backend, hardware.rs:173 / llama.rs:113-118); attention reads the
+// dequantised rows d * q and is otherwise the same closure.
 //
 // Build: oracle/Makefile (g++ -O3 -ffp-contract=off; no FMA contraction,
 // matching rustc's default).
@@ -238,6 +245,25 @@ class Pool {
 
 // ---------------------------------------------------------------------------
 // KvCache restatement (kv.rs:15-187).
+// quant.rs:785-791: amax folded with f32::max (a NaN element is ignored),
+// d = amax / 127, id = 1 / d (0 when d is 0), q = (v * id).round() as i8:
+// round half away from zero, then Rust's saturating float -> int cast
+// (NaN -> 0, beyond the range -> -128 / 127).
+inline int8_t sat_i8(float r) {
+  if (std::isnan(r)) return 0;
+  if (r >= 127.0f) return 127;
+  if (r <= -128.0f) return -128;
+  return (int8_t)(int)r;
+}
+float quantize_block(const float *x, int8_t *q) {
+  float amax = 0.0f;
+  for (int i = 0; i < 32; ++i) amax = std::fmax(amax, std::fabs(x[i]));
+  const float d = amax / 127.0f;
+  const float id = d > 0.0f ? 1.0f / d : 0.0f;
+  for (int i = 0; i < 32; ++i) q[i] = sat_i8(std::round(x[i] * id));
+  return d;
+}
+
 // ---------------------------------------------------------------------------
 struct Seq {
   std::vector<size_t> blocks;
@@ -245,8 +271,9 @@ struct Seq {
 };
 
 struct OracleKv {
-  size_t n_layers, kv_dim, n_blocks, elem;  // elem: 2 (f16) or 4 (f32)
+  size_t n_layers, kv_dim, n_blocks, elem;  // elem: 2 (f16), 4 (f32) or 1 (Q8_0 quants)
   std::vector<uint8_t> k, v;                 // [layer][block][slot][kv_dim]
+  std::vector<uint16_t> ks, vs;              // Q8_0: f16 d per 32, [layer][block][slot][kv_dim/32]
   std::vector<uint32_t> refs;
   std::vector<size_t> free;  // stack; back() is popped first
   std::unordered_map<uint32_t, Seq> seqs;
@@ -258,6 +285,10 @@ struct OracleKv {
     const size_t size = n_layers * n_blocks * kBlock * kv_dim * elem;
     k.assign(size, 0);
     v.assign(size, 0);
+    if (elem == 1) {
+      ks.assign(size / 32, 0);
+      vs.assign(size / 32, 0);
+    }
     refs.assign(n_blocks, 0);
     free.reserve(n_blocks);
     for (size_t b = n_blocks; b-- > 0;) free.push_back(b);  // (0..n).rev(): pop gives 0,1,2..
@@ -306,6 +337,11 @@ struct OracleKv {
           const size_t src = offset(l, last, 0) * elem, dst = offset(l, nb, 0) * elem;
           std::memmove(&k[dst], &k[src], n);
           std::memmove(&v[dst], &v[src], n);
+          if (elem == 1) {  // the block's scales travel with its quants
+            const size_t ns = kBlock * kv_dim / 32, s0 = offset(l, last, 0) / 32, d0 = offset(l, nb, 0) / 32;
+            std::memmove(&ks[d0], &ks[s0], ns * 2);
+            std::memmove(&vs[d0], &vs[s0], ns * 2);
+          }
         }
         release(last);
         s.blocks.back() = nb;
@@ -323,10 +359,22 @@ struct OracleKv {
     if (elem == 2) {
       narrow_row(kr, (uint16_t *)&k[o], kv_dim);
       narrow_row(vr, (uint16_t *)&v[o], kv_dim);
+    } else if (elem == 1) {
+      for (size_t b = 0; b < kv_dim / 32; ++b) {
+        ks[o / 32 + b] = f32_to_f16(quantize_block(kr + 32 * b, (int8_t *)&k[o + 32 * b]));
+        vs[o / 32 + b] = f32_to_f16(quantize_block(vr + 32 * b, (int8_t *)&v[o + 32 * b]));
+      }
     } else {
       std::memcpy(&k[o], kr, kv_dim * 4);
       std::memcpy(&v[o], vr, kv_dim * 4);
     }
+  }
+
+  // Q8_0 row read back as d * q (quant.rs:188-193); o = the row's byte offset.
+  void dequant(const std::vector<uint8_t> &pool, const std::vector<uint16_t> &sc, size_t o, size_t col,
+               size_t n, float *dst) const {
+    for (size_t i = 0; i < n; ++i)
+      dst[i] = f16_to_f32(sc[(o + col + i) / 32]) * (float)(int8_t)pool[o + col + i];
   }
 
   // Byte offset of position p of a sequence's table (kv.rs:146-148).
@@ -398,6 +446,8 @@ void attention_task(const OracleKv &kv, size_t layer, const std::vector<size_t> 
     const uint8_t *kr = kv.k.data() + kv.row_offset(layer, blocks, p) + col;
     if (kv.elem == 2)
       widen_row((const uint16_t *)kr, row.data(), hd);
+    else if (kv.elem == 1)
+      kv.dequant(kv.k, kv.ks, kv.row_offset(layer, blocks, p), col, hd, row.data());
     else
       std::memcpy(row.data(), kr, hd * 4);
     for (size_t g = 0; g < group; ++g) scores[g * len + p] = dot8(qs + g * hd, row.data(), hd) * scale;
@@ -419,6 +469,8 @@ void attention_task(const OracleKv &kv, size_t layer, const std::vector<size_t> 
     const uint8_t *vr = kv.v.data() + kv.row_offset(layer, blocks, p) + col;
     if (kv.elem == 2)
       widen_row((const uint16_t *)vr, row.data(), hd);
+    else if (kv.elem == 1)
+      kv.dequant(kv.v, kv.vs, kv.row_offset(layer, blocks, p), col, hd, row.data());
     else
       std::memcpy(row.data(), vr, hd * 4);
     for (size_t g = 0; g < group; ++g) {
@@ -469,16 +521,21 @@ int ora_has_f16c(void) {
 #endif
 }
 
+// dtype 0 = f16, 1 = f32, 2 = Q8_0 (kv_dim a multiple of 32).
 void *ora_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype) {
-  if (kv_dim == 0 || n_layers == 0 || (dtype != 0 && dtype != 1)) return nullptr;
-  return new OracleKv(n_layers, kv_dim, n_tokens, dtype == 0 ? 2 : 4);
+  if (kv_dim == 0 || n_layers == 0 || dtype < 0 || dtype > 2) return nullptr;
+  if (dtype == 2 && kv_dim % 32 != 0) return nullptr;
+  return new OracleKv(n_layers, kv_dim, n_tokens, dtype == 0 ? 2 : dtype == 1 ? 4 : 1);
 }
+
+// quant.rs:785-791 on one 32-element block: quants to q, returns d (f32).
+float ora_quantize_block(const float *x, int8_t *q) { return quantize_block(x, q); }
 void ora_destroy(void *h) { delete (OracleKv *)h; }
 
 size_t ora_capacity(void *h) { return ((OracleKv *)h)->n_blocks * kBlock; }
 size_t ora_bytes(void *h) {
   auto *kv = (OracleKv *)h;
-  return kv->k.size() + kv->v.size();
+  return kv->k.size() + kv->v.size() + 2 * (kv->ks.size() + kv->vs.size());
 }
 size_t ora_n_blocks(void *h) { return ((OracleKv *)h)->n_blocks; }
 size_t ora_len(void *h, uint32_t seq) { return ((OracleKv *)h)->len(seq); }
@@ -644,6 +701,25 @@ void ora_load_pool(void *h, size_t layer, const void *k_in, const void *v_in) {
   const size_t n = kv->n_blocks * kBlock * kv->kv_dim * kv->elem;
   std::memcpy(&kv->k[layer * n], k_in, n);
   std::memcpy(&kv->v[layer * n], v_in, n);
+}
+
+// Q8_0 scale pools of one layer ([block][slot][kv_dim/32] f16 bits), read or
+// replaced like ora_pool / ora_load_pool.
+int ora_scales(void *h, size_t layer, uint16_t *k_out, uint16_t *v_out) {
+  auto *kv = (OracleKv *)h;
+  if (kv->elem != 1) return 5;
+  const size_t n = kv->n_blocks * kBlock * kv->kv_dim / 32;
+  std::memcpy(k_out, &kv->ks[layer * n], n * 2);
+  std::memcpy(v_out, &kv->vs[layer * n], n * 2);
+  return 0;
+}
+int ora_load_scales(void *h, size_t layer, const uint16_t *k_in, const uint16_t *v_in) {
+  auto *kv = (OracleKv *)h;
+  if (kv->elem != 1) return 5;
+  const size_t n = kv->n_blocks * kBlock * kv->kv_dim / 32;
+  std::memcpy(&kv->ks[layer * n], k_in, n * 2);
+  std::memcpy(&kv->vs[layer * n], v_in, n * 2);
+  return 0;
 }
 
 // Attention over the cache (model.rs:431-475) for n tokens of a batch:

@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libltkv_oracle.so")
 _lib = None
 
-F16, F32 = 0, 1
+F16, F32, Q8_0 = 0, 1, 2
 BLOCK = 16
 
 _ERRORS = {1: "full", 2: "noncontig", 3: "range", 5: "arg"}
@@ -77,6 +77,9 @@ def load():
         "ora_attention": (C.c_int, [vp, sz, sz, vp, vp, sz, sz, C.c_float, vp, vp, sz]),
         "ora_attention_tables": (C.c_int, [vp, sz, sz, vp, sz, vp, sz, sz, C.c_float, vp, vp, sz]),
         "ora_pool_selftest": (u64, [sz, sz, vp]),
+        "ora_quantize_block": (C.c_float, [vp, vp]),
+        "ora_scales": (C.c_int, [vp, sz, vp, vp]),
+        "ora_load_scales": (C.c_int, [vp, sz, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -111,6 +114,15 @@ def has_f16c() -> bool:
     return bool(load().ora_has_f16c())
 
 
+def quantize_block(x) -> tuple[float, np.ndarray]:
+    """quant.rs:785-791 on one 32-element block: (d as f32, int8 quants)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size == 32
+    q = np.empty(32, dtype=np.int8)
+    d = load().ora_quantize_block(_ptr(x), _ptr(q))
+    return float(d), q
+
+
 def pool_selftest(threads: int, n: int) -> np.ndarray:
     hits = np.zeros(max(n, 1), dtype=np.uint32)
     load().ora_pool_selftest(threads, n, _ptr(hits))
@@ -122,11 +134,12 @@ class OracleKv:
 
     def __init__(self, n_layers: int, kv_dim: int, n_tokens: int, dtype: str = "f16"):
         self._lib = load()
+        codes = {"f16": F16, "f32": F32, "q8_0": Q8_0}
         self.dtype = dtype
-        self.elem = 2 if dtype == "f16" else 4
+        self.elem = {"f16": 2, "f32": 4, "q8_0": 1}[dtype]
         self.kv_dim = kv_dim
         self.n_layers = n_layers
-        h = self._lib.ora_create(n_layers, kv_dim, n_tokens, F16 if dtype == "f16" else F32)
+        h = self._lib.ora_create(n_layers, kv_dim, n_tokens, codes[dtype])
         if not h:
             raise OracleError(5, "bad arguments")
         self._h = h
@@ -221,7 +234,7 @@ class OracleKv:
 
     # -- kv.rs:133-150 (collected)
     def rows(self, layer: int, seq: int, n: int):
-        dt = np.uint16 if self.elem == 2 else np.float32
+        dt = {1: np.int8, 2: np.uint16, 4: np.float32}[self.elem]
         k = np.empty((n, self.kv_dim), dtype=dt)
         v = np.empty((n, self.kv_dim), dtype=dt)
         rc = self._lib.ora_rows(self._h, layer, seq, n, _ptr(k), _ptr(v))
@@ -246,7 +259,7 @@ class OracleKv:
         self._lib.ora_share(self._h, src, dst, length)
 
     def pool(self, layer: int = 0):
-        dt = np.uint16 if self.elem == 2 else np.float32
+        dt = {1: np.int8, 2: np.uint16, 4: np.float32}[self.elem]
         shape = (self.n_blocks, BLOCK, self.kv_dim)
         k = np.empty(shape, dtype=dt)
         v = np.empty(shape, dtype=dt)
@@ -254,11 +267,29 @@ class OracleKv:
         return k, v
 
     def load_pool(self, layer, k, v) -> None:
-        dt = np.uint16 if self.elem == 2 else np.float32
+        dt = {1: np.int8, 2: np.uint16, 4: np.float32}[self.elem]
         shape = (self.n_blocks, BLOCK, self.kv_dim)
         k = np.ascontiguousarray(k, dtype=dt).reshape(shape)
         v = np.ascontiguousarray(v, dtype=dt).reshape(shape)
         self._lib.ora_load_pool(self._h, layer, _ptr(k), _ptr(v))
+
+    def scales(self, layer: int = 0):
+        """Q8_0 scale pools of one layer, [n_blocks][16][kv_dim/32] f16 bits."""
+        shape = (self.n_blocks, BLOCK, self.kv_dim // 32)
+        k = np.empty(shape, dtype=np.uint16)
+        v = np.empty(shape, dtype=np.uint16)
+        rc = self._lib.ora_scales(self._h, layer, _ptr(k), _ptr(v))
+        if rc:
+            self._raise(rc)
+        return k, v
+
+    def load_scales(self, layer, k, v) -> None:
+        shape = (self.n_blocks, BLOCK, self.kv_dim // 32)
+        k = np.ascontiguousarray(k, dtype=np.uint16).reshape(shape)
+        v = np.ascontiguousarray(v, dtype=np.uint16).reshape(shape)
+        rc = self._lib.ora_load_scales(self._h, layer, _ptr(k), _ptr(v))
+        if rc:
+            self._raise(rc)
 
     # -- model.rs:431-475
     def attention(self, layer, seqs, positions, q, n_heads, head_dim, scale=None, threads=1):

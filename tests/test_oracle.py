@@ -379,3 +379,114 @@ def test_oracle_rope_against_float64(neox, rope_dim, head_dim):
     for i, p in enumerate(pos):  # f32 pools hold the rotated k exactly as the oracle computed it
         want = _rope64(k[i], n_kv, head_dim, rope_dim, neox, 500000.0, int(p))
         np.testing.assert_allclose(kr[i], want, rtol=0, atol=2e-6 * (1 + np.abs(want)).max())
+
+
+# ---------------------------------------------------------------------------- Q8_0 (quant.rs:785-791)
+def test_quantize_block_known_answers():
+    """Hand-derived blocks: amax 127 gives d = 1 exactly, so q = round(x)
+    with ties away from zero (RNE would give 2 for 2.5 and 0 for 0.5)."""
+    x = np.zeros(32, np.float32)
+    x[:10] = [127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 63.5, -126.5, 1.4999999]
+    d, q = oracle.quantize_block(x)
+    assert d == 1.0
+    assert q[:10].tolist() == [127, 3, -3, 1, -1, 2, -2, 64, -127, 1]
+    assert (q[10:] == 0).all()
+    # amax 254: d = 2, id = 0.5; 5 -> 2.5 -> 3, -7 -> -3.5 -> -4, 1 -> 0.5 -> 1
+    x = np.zeros(32, np.float32)
+    x[:4] = [-254, 5, -7, 1]
+    d, q = oracle.quantize_block(x)
+    assert d == 2.0 and q[:4].tolist() == [-127, 3, -4, 1]
+
+
+def test_quantize_block_special_values():
+    # all zeros: d = 0, id = 0
+    d, q = oracle.quantize_block(np.zeros(32, np.float32))
+    assert d == 0.0 and (q == 0).all()
+    # NaN is skipped by f32::max and quantises to 0 (NaN as i8 == 0)
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2] = np.nan, 127.0, -3.0
+    d, q = oracle.quantize_block(x)
+    assert d == 1.0 and q[0] == 0 and q[1] == 127 and q[2] == -3
+    x[:] = np.nan
+    d, q = oracle.quantize_block(x)
+    assert d == 0.0 and (q == 0).all()
+    # inf: d = inf, id = 1 / inf = 0; inf * 0 = NaN -> 0, finite * 0 = 0
+    x = np.ones(32, np.float32)
+    x[3] = -np.inf
+    d, q = oracle.quantize_block(x)
+    assert d == np.inf and (q == 0).all()
+    # subnormal amax: 1 / d overflows to inf, so quants saturate (as i8 of +-inf)
+    x = np.zeros(32, np.float32)
+    x[:3] = [1e-40, -1e-40, 0.0]
+    d, q = oracle.quantize_block(x)
+    assert d == np.float32(np.float32(1e-40) / np.float32(127))
+    with np.errstate(over="ignore"):
+        assert np.isinf(np.float32(1.0) / np.float32(d))
+    assert q[:3].tolist() == [127, -128, 0]
+
+
+def test_quantize_block_round_trip_bound():
+    """Random blocks over many magnitudes: q = round(x / d) within
+    [-127, 127], the element of largest magnitude maps to +-127, and
+    |x - d q| <= d / 2 (up to the rounding of x * id)."""
+    rng = np.random.default_rng(7)
+    for i in range(2000):
+        x = (rng.standard_normal(32) * 10.0 ** rng.integers(-30, 30)).astype(np.float32)
+        d, q = oracle.quantize_block(x)
+        assert d == np.float32(np.abs(x).max()) / np.float32(127)
+        assert np.abs(q.astype(int)).max() == 127
+        j = np.argmax(np.abs(x))
+        assert q[j] == np.sign(x[j]) * 127
+        err = np.abs(x.astype(np.float64) - np.float64(d) * q)
+        assert (err <= 0.5 * d * (1 + 1e-5)).all(), i
+
+
+def test_q8_pool_layout_and_attention():
+    """Q8_0 storage: row quants and per-32 f16 scales equal quantize_block of
+    each 32-element run; attention equals the float64 brute force over the
+    dequantised rows d * q, which stay within d / 2 (+ the f16 rounding of d)
+    of the rows written; copy-on-write copies scales with quants."""
+    rng = np.random.default_rng(11)
+    n_heads, n_kv, hd = 8, 2, 64
+    kvd = n_kv * hd
+    kv = OracleKv(1, kvd, 40 * BLOCK, dtype="q8_0")
+    lens = [1, 17, 120]
+    written = {}
+    for s, n in enumerate(lens):
+        k = rng.standard_normal((n, kvd), dtype=np.float32)
+        v = rng.standard_normal((n, kvd), dtype=np.float32)
+        for p in range(n):
+            b, sl = kv.append(s, p)
+            kv.write(0, b, sl, k[p], v[p])
+        written[s] = (k, v)
+    kv.share(2, 5, 100)
+    b, sl = kv.append(5, 100)  # copy-on-write of block 6 of seq 2
+    kv.write(0, b, sl, *[rng.standard_normal(kvd, dtype=np.float32)] * 2)
+    written[5] = tuple(np.concatenate([w[:100], np.zeros((1, kvd), np.float32)]) for w in written[2])
+    qk, qv = kv.pool(0)
+    sk, sv = kv.scales(0)
+
+    def deq(quants, scales, seq, n):
+        t = kv.block_table(seq)
+        cells = [(t[p // BLOCK], p % BLOCK) for p in range(n)]
+        qs = np.stack([quants[b, s] for b, s in cells]).astype(np.float64)
+        ds = np.stack([oracle.f16_to_f32(scales[b, s]) for b, s in cells]).astype(np.float64)
+        return qs * np.repeat(ds, 32, axis=1)
+
+    for s, n in enumerate(lens):
+        t = kv.block_table(s)
+        for p in range(n):
+            for blk in range(kvd // 32):
+                d, q = oracle.quantize_block(written[s][0][p, blk * 32:(blk + 1) * 32])
+                assert sk[t[p // BLOCK], p % BLOCK, blk] == oracle.f32_to_f16(np.float32(d))
+                np.testing.assert_array_equal(qk[t[p // BLOCK], p % BLOCK, blk * 32:(blk + 1) * 32], q)
+    q = rng.standard_normal((4, n_heads * hd), dtype=np.float32)
+    seqs, n_ctx = [0, 1, 2, 5], lens + [100]
+    got = kv.attention(0, np.array(seqs), np.array(n_ctx[:3] + [100]) - 1, q, n_heads, hd, threads=2)
+    for i, (s, n) in enumerate(zip(seqs, n_ctx)):
+        k = deq(qk, sk, s, n)
+        v = deq(qv, sv, s, n)
+        bound = np.repeat(np.abs(written[s][0][:n]).reshape(n, -1, 32).max(axis=2) / 127, 32, axis=1)
+        assert (np.abs(k - written[s][0][:n]) <= bound * (0.5 + 2 ** -10 * 128)).all()
+        want = _brute_force(k, v, q[i], n_heads, hd, float(np.float32(1.0 / np.sqrt(hd))))
+        np.testing.assert_allclose(got[i], want, atol=2e-6, rtol=1e-5)
