@@ -198,8 +198,8 @@ def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
     o.append_batch(w.pre_seqs, w.pre_pos)
     k, v = w.kv.read_pool(0)  # device state after the GPU run (same cells; the
     o.load_pool(0, k, v)      # timed steps rewrite the decode cells identically)
-    if w.dtype == "q8_0":
-        o.load_scales(0, *w.kv.read_scales(0))
+    if w.dtype == "q8_0":  # device layout [block][group][slot] -> the oracle's [block][slot][group]
+        o.load_scales(0, *(x.transpose(0, 2, 1) for x in w.kv.read_scales(0)))
     seqs = np.arange(w.batch, dtype=np.uint32)
 
     def step(s):

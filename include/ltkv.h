@@ -67,7 +67,9 @@ enum {
  * stores each 32-element run of a row as 32 int8 quants plus an f16 scale d
  * (the Q8_0 block of quant.rs:188-193, quantised as quant.rs:785-791 and
  * read back as d * q): quants in the K/V pools ([n_blocks][16][kv_dim]
- * bytes), scales in K/V scale pools ([n_blocks][16][kv_dim/32] f16).
+ * bytes), scales in K/V scale pools ([n_blocks][kv_dim/32][16] f16: per
+ * block, the 16 slots of each 32-element group are adjacent, so one kv
+ * head's scales of a block are one contiguous run).
  * kv_dim must be a multiple of 32. Gather, rows and the RoPE append have no
  * Q8_0 form (LTKV_ERR_ARG). */
 enum { LTKV_F16 = 0, LTKV_F32 = 1, LTKV_Q8_0 = 2 };
@@ -238,7 +240,7 @@ LTKV_API int ltkv_plan_stats(const ltkv_cache *c, uint64_t out[6]);
 /* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */
 LTKV_API int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v);
 
-/* Copy one layer's K and V scale pools ([n_blocks][16][kv_dim/32] f16 bits)
+/* Copy one layer's K and V scale pools ([n_blocks][kv_dim/32][16] f16 bits)
  * of a Q8_0 cache to host. */
 LTKV_API int ltkv_read_scales(ltkv_cache *c, size_t layer, uint16_t *h_k, uint16_t *h_v);
 

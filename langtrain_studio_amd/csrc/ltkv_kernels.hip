@@ -24,6 +24,8 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // ----------------------------------------------------------------------------
 // f32 -> f16, IEEE round-to-nearest-even (the conversion of f16::from_f32).
@@ -141,7 +143,9 @@ write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t
   int8_t *dq = (is_v ? vpool : kpool) + cell;
   *reinterpret_cast<u32x4 *>(dq) = u32x4{w[0], w[1], w[2], w[3]};
   *reinterpret_cast<u32x4 *>(dq + 16) = u32x4{w[4], w[5], w[6], w[7]};
-  (is_v ? vscale : kscale)[(int64_t)s * (kv_dim >> 5) + blk] = (uint16_t)f16_bits(d);
+  // Scale pool layout [block][kv_dim / 32][16 slots]: the scales of one kv
+  // head of a block are one contiguous run (HD / 32 x 16 x 2 bytes).
+  (is_v ? vscale : kscale)[(((int64_t)(s >> 4) * (kv_dim >> 5) + blk) << 4) + (s & 15)] = (uint16_t)f16_bits(d);
 }
 
 // ----------------------------------------------------------------------------
@@ -496,9 +500,9 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
   const int64_t head_off = (int64_t)kvh * head_stride;
 
-  // q8_0: a lane's E = 16 elements lie in one 32-element block; its scale
-  // sits at cell * (kv_dim / 32) + (head_off + c * E) / 32 of the scale pool.
-  const int64_t sl_stride = slot_stride >> 5;
+  // q8_0: a lane's E elements lie in one 32-element group; its scale sits at
+  // (block * (kv_dim / 32) + group) * 16 + slot of the scale pool.
+  const int64_t sl_groups = slot_stride >> 5;
   const int64_t sl_lane = (head_off + c * E) >> 5;
   float ksc[2][LOADS], vsc[2][LOADS];  // scales of the two tiles in flight (q8_0 only)
   using TV = typename TileVec<T>::type;
@@ -512,7 +516,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
       kr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(kpool + o));
       vr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(vpool + o));
       if constexpr (Q8) {
-        const int64_t so = ((int64_t)blk * 16 + rg + j * RPL) * sl_stride + sl_lane;
+        const int64_t so = (((int64_t)blk * sl_groups + sl_lane) << 4) + rg + j * RPL;
         ksc[st][j] = (float)__builtin_bit_cast(_Float16, kscale[so]);
         vsc[st][j] = (float)__builtin_bit_cast(_Float16, vscale[so]);
       }
@@ -958,11 +962,11 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   uint32_t roff[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) roff[j] = (uint32_t)(rg + RPL * j) * row_bytes + col_off;
-  // q8_0: a lane's 8 elements lie in one 32-element block; its f16 scale sits
-  // at cell * (kv_dim / 32) + (head offset + 8 c) / 32 of the scale pool.
-  const uint32_t srow_bytes = (uint32_t)(slot_stride >> 5) * 2;
-  const uint32_t scol = (uint32_t)(c * E >> 5) * 2;  // inside the head's scales
-  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 2;
+  // q8_0: a lane's 8 elements lie in one 32-element group; the head's scales
+  // of a block are the run [block][head groups][16 slots] of the scale pool.
+  const int64_t sgroups = slot_stride >> 5;                     // groups per row
+  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 32;  // bytes to the head's groups
+  const uint32_t sgrp = (uint32_t)(c * E >> 5) * 32;             // bytes to this lane's group
   float ksc[3][LOADS], vsc[3][LOADS];  // scales of the tiles in flight (q8_0 only)
   int my_row[NPL];  // tile rows of this lane's scores after the scatter
   {
@@ -1011,18 +1015,23 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
         vr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b64(rv, roff[j], 0, kNt));
       }
     }
-    if constexpr (Q8) {  // the rows' block scales, zero past the context (extent)
-      const int sext = rows > 0 ? (rows - 1) * (int)srow_bytes + HD / 32 * 2 : 0;
-      const int64_t sblk = (int64_t)blk * 16 * (int64_t)srow_bytes + shead;
+    if constexpr (Q8) {  // the rows' group scales; zero past the context
+      const int sext = rows > 0 ? HD / 32 * 32 : 0;
+      const int64_t sblk = (int64_t)blk * sgroups * 32 + shead;
       const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
       const __amdgpu_buffer_rsrc_t sv = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) {
-        const uint32_t so = (uint32_t)(rg + RPL * j) * srow_bytes + scol;
+        const uint32_t so = sgrp + (uint32_t)(rg + RPL * j) * 2;
         ksc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sk, so, 0, 0));
         vsc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sv, so, 0, 0));
+      }
+      if (rows < 16) {  // slots past the context may hold any scale (inf: d * 0 = NaN)
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j)
+          if (rg + RPL * j >= rows) ksc[st][j] = vsc[st][j] = 0.f;
       }
     }
   };
@@ -1240,6 +1249,440 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   }
 }
 
+// ----------------------------------------------------------------------------
+// Kernel 4 with the scores on MFMA (f16 and q8_0 tiles). The per-element work
+// of the VALU kernels above, a G-way dot product per K element and a G-way
+// FMA per V element, keeps the VALU busy for most of the time the tile's
+// bytes take to arrive (and longer for 1-byte q8_0 elements). Here the score
+// product of a 16-token tile runs as HD/32 v_mfma_f32_16x16x32_f16:
+//   S^T[token][col] = K Q'^T   A = the K tile straight from the loads
+//                              (lane l: token l % 16, d = 32 ks + 8 (l / 16)),
+//                              B = Q' in registers, D lane l: tokens
+//                              4 (l / 16) + i of column l % 16.
+// Q is f32, split into f16 hi + lo parts held in two columns of Q' (head h
+// in column h, its lo part in column 15 - h), so one MFMA covers both and a
+// row_mirror DPP add sums them: scores keep f32 accuracy over the exact f16
+// (or int8) K elements. q8_0 tiles convert exactly to f16 and each k step
+// (one 32-element scale block) accumulates separately, scaled by its block
+// scale afterwards. The V side stays on the VALU in the D layout: lane
+// (l % 16, l / 16) holds HD/16 elements of tokens 4 (l / 16) + i, and takes
+// the weight of head h from lane h of its row (row_newbcast). Softmax state
+// is per lane row group, merged at the end as in attn16_kernel.
+// ----------------------------------------------------------------------------
+template <int B>
+struct BufVec;
+template <>
+struct BufVec<16> {
+  using type = u32x4;
+  template <int AUX>
+  __device__ static __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+  }
+};
+template <>
+struct BufVec<8> {
+  using type = u32x2;
+  template <int AUX>
+  __device__ static __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX));
+  }
+};
+template <>
+struct BufVec<4> {
+  using type = uint32_t;
+  template <int AUX>
+  __device__ static __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
+  }
+};
+
+// int8 x 8 -> f16 x 8, exact: each byte, biased to u = x + 128 in [0, 255],
+// becomes the mantissa of an f16 in [1024, 2048) (bits 0x6400 | u, value
+// 1024 + u), and 1152 is subtracted: two v_perm_b32 and two packed f16
+// subtractions per four elements.
+__device__ __forceinline__ h8 i8x8_to_h8(const u32x2 &w) {
+  constexpr uint32_t kHi = 0x64646464u;
+  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
+  const h2 bias = {(_Float16)1152.f, (_Float16)1152.f};
+  const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04010400u)) - bias;
+  const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04030402u)) - bias;
+  const h2 p2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, b, 0x04010400u)) - bias;
+  const h2 p3 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, b, 0x04030402u)) - bias;
+  return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <typename T, int E, typename V>
+__device__ __forceinline__ void unpack_row(const V &v, float (&f)[E]) {
+  if constexpr (std::is_same_v<T, _Float16>) {
+    typedef _Float16 hv __attribute__((ext_vector_type(E)));
+    const hv x = __builtin_bit_cast(hv, v);
+#pragma unroll
+    for (int i = 0; i < E; ++i) f[i] = (float)x[i];
+  } else {
+    typedef int8_t bv __attribute__((ext_vector_type(E)));
+    const bv x = __builtin_bit_cast(bv, v);
+#pragma unroll
+    for (int i = 0; i < E; ++i) f[i] = (float)x[i];
+  }
+}
+
+template <typename T, int HD, int G, int NW>
+__global__ void __launch_bounds__(64 * NW)
+attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
+                 const int32_t *__restrict__ tables, int64_t table_stride,
+                 const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
+                 float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
+                 int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
+                 int max_parts, const int32_t *__restrict__ pre_parts,
+                 const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
+                 const uint16_t *__restrict__ vscale) {
+  constexpr bool Q8 = std::is_same_v<T, int8_t>;
+  constexpr int KS = HD / 32;                  // MFMA k steps: one q8_0 scale group each
+  constexpr int E = HD / 16;                   // V elements per lane per token
+  constexpr int RB = HD * (int)sizeof(T);      // bytes of a head row
+  constexpr int CB = RB / 16;                  // bytes of a lane's slice of a row (16 lanes a row)
+  constexpr int KB = 8 * (int)sizeof(T);       // bytes of an MFMA A slice (8 elements)
+  constexpr int PITCH = RB + 16;               // LDS bytes per staged K row
+  using CV = typename BufVec<CB>::type;
+  static_assert(G >= 1 && G <= 8, "hi and lo columns of the group must fit 16");
+  static_assert(HD % 32 == 0 && (E == 4 || E == 8), "head_dim 64 or 128");
+  __shared__ __attribute__((aligned(16))) char sk_lds[NW][16 * PITCH];  // wave-private K tile
+
+  const int kvh = (int)(blockIdx.x % n_kv_heads);
+  const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
+  const int64_t qx = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  const int64_t qi = qmap ? qmap[qx] : qx;
+  const int lane = threadIdx.x & 63;
+  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15, lq = lane >> 4;
+  const int n_heads = n_kv_heads * G;
+
+  int64_t len = lens[qi];
+  if (len < 0) len = 0;
+  if (len > table_stride * 16) len = table_stride * 16;
+  // A query with group partials and nothing else to read (or whose group
+  // wrote its output) has no work here.
+  if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
+  const int pt = partition_tokens(len, part_tokens);
+  const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+  if (part >= np) return;  // uniform over the work-group
+  const int64_t tok0 = (int64_t)part * pt;
+  const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
+  const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
+
+  // B operand Q'^T: column lr < G holds the hi part of head lr, column
+  // 15 - h the lo part of head h; the other columns are zero.
+  h8 qb[KS];
+  {
+    const bool hi = lr < G, lo = lr >= 16 - G;
+    const int h = hi ? lr : 15 - lr;
+    const float *qp = q + qi * (int64_t)n_heads * HD + ((int64_t)kvh * G + ((hi || lo) ? h : 0)) * HD + 8 * lq;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float x[8];
+      const f32x4 a = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
+      const f32x4 b = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = a[e] * qscale;
+        x[4 + e] = b[e] * qscale;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 xh = (_Float16)x[e];
+        qb[ks][e] = hi ? xh : lo ? (_Float16)(x[e] - (float)xh) : (_Float16)0.f;
+      }
+    }
+  }
+
+  // Per-lane byte offsets. K and V are both loaded in row order, 16 lanes a
+  // row (lane (lr, lq) takes rows 4 lq + i, bytes [CB lr, CB lr + CB)): K is
+  // then staged through LDS into the MFMA A layout, V is used in place.
+  const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
+  uint32_t roff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) roff[i] = (uint32_t)(4 * lq + i) * row_bytes + (uint32_t)(lr * CB);
+  // q8_0 scales: the head's groups of a block are the run [HD / 32 groups][16
+  // slots]; a lane reads the four slots 4 lq .. 4 lq + 3 of a group at once.
+  const int64_t sgroups = slot_stride >> 5;
+  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 32;
+  const uint32_t vsoff = (uint32_t)((lr * E) >> 5) * 32 + (uint32_t)(8 * lq);
+  const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh * head_stride);
+  const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh * head_stride);
+  const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
+  char *sk = sk_lds[wave];
+
+  float m_own = -INFINITY, l_own = 0.f;  // softmax state of head lr (or 15 - lr), row group lq
+  float acc[G][E];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+
+  const int32_t *tab = tables + qi * table_stride;
+
+  struct Stage {
+    CV k[4], v[4];
+    u32x2 ks[Q8 ? KS : 1];  // q8_0: K scales of slots 4 lq .. 4 lq + 3, per group
+    u32x2 vs;               // q8_0: V scales of the lane's group, slots 4 lq .. 4 lq + 3
+  };
+
+  // Loads go through buffer descriptors whose extent ends at the last row
+  // inside the context: rows past it (and every row of a prefetch past the
+  // wave's last tile, extent 0) read as zeros without touching memory.
+  auto load_tile = [&](int b, Stage &st) {
+    const int bb = b < b1 ? b : b1 - 1;
+    int32_t blk = tab[bb];
+    if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
+    const int valid = b < b1 ? (int)(tok1 - (int64_t)b * 16) : 0;
+    const int rows = valid < 16 ? valid : 16;
+    const int extent = rows > 0 ? (rows - 1) * (int)row_bytes + RB : 0;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(kbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(vbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st.k[i] = BufVec<CB>::template load<kNt>(rk, roff[i]);
+      st.v[i] = BufVec<CB>::template load<kNt>(rv, roff[i]);
+    }
+    if constexpr (Q8) {
+      const int sext = rows > 0 ? KS * 32 : 0;
+      const int64_t sblk = (int64_t)blk * sgroups * 32 + shead;
+      const __amdgpu_buffer_rsrc_t skr = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
+      const __amdgpu_buffer_rsrc_t svr = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) st.ks[ks] = BufVec<8>::template load<0>(skr, (uint32_t)(ks * 32 + 8 * lq));
+      st.vs = BufVec<8>::template load<0>(svr, vsoff);
+      if (rows < 16) {  // slots past the context may hold any scale (inf: d * 0 = NaN)
+        typedef uint16_t s4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s4 x = __builtin_bit_cast(s4, st.ks[ks]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * lq + i >= rows) x[i] = 0;
+          st.ks[ks] = __builtin_bit_cast(u32x2, x);
+        }
+        s4 y = __builtin_bit_cast(s4, st.vs);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * lq + i >= rows) y[i] = 0;
+        st.vs = __builtin_bit_cast(u32x2, y);
+      }
+    }
+  };
+
+  auto compute_tile = [&](int b, const Stage &st) {
+    // K tile into the A layout: row lr, elements 32 ks + 8 lq .. + 8.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<CV *>(sk + (4 * lq + i) * PITCH + lr * CB) = st.k[i];
+    typename BufVec<KB>::type ka[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      ka[ks] = *reinterpret_cast<const typename BufVec<KB>::type *>(sk + lr * PITCH + (32 * ks + 8 * lq) * (int)sizeof(T));
+    f32x4 s;
+    if constexpr (Q8) {
+      f32x4 c[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        c[ks] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(ka[ks]), qb[ks], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                       0, 0, 0);
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const h4 d = __builtin_bit_cast(h4, st.ks[ks]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = ks == 0 ? (float)d[i] * c[0][i] : __builtin_fmaf((float)d[i], c[ks][i], s[i]);
+      }
+    } else {
+      s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, ka[ks]), qb[ks], s, 0, 0, 0);
+    }
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = s[i] + dpp<0x140>(s[i]);  // hi + lo (row_mirror: lane ^ 15)
+    const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
+    if (valid < 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * lq + i >= valid) sc[i] = -INFINITY;
+    }
+    // Online softmax of this lane's head over its row group's tokens.
+    const float bm = __builtin_fmaxf(__builtin_fmaxf(sc[0], sc[1]), __builtin_fmaxf(sc[2], sc[3]));
+    const float mn = __builtin_fmaxf(m_own, bm);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m_own - mref);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
+    l_own = l_own * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    const bool grew = mn > m_own;
+    m_own = mn;
+    if (__builtin_amdgcn_ballot_w64(grew)) {  // wave-uniform: some head's max grew
+      static_for<0, G>([&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        const float a = bcast16<h>(alpha);
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] *= a;
+      });
+    }
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 vsd = __builtin_bit_cast(h4, st.vs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float vf[E];
+      unpack_row<T, E>(st.v[i], vf);
+      float vsc = 1.f;
+      if constexpr (Q8) vsc = (float)vsd[i];
+      static_for<0, G>([&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        float w = bcast16<h>(p[i]);
+        if constexpr (Q8) w *= vsc;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
+      });
+    }
+  };
+
+  // Software pipeline: two tiles in flight while one is computed. Loads
+  // past the wave's last tile read nothing (extent 0).
+  {
+    constexpr int W = NW;
+    int b = b0 + wave;
+    if (b < b1) {
+      Stage s0, s1, s2;
+      load_tile(b, s0);
+      load_tile(b + W, s1);
+      for (;;) {
+        load_tile(b + 2 * W, s2);
+        compute_tile(b, s0);
+        if ((b += W) >= b1) break;
+        load_tile(b + 2 * W, s0);
+        compute_tile(b, s1);
+        if ((b += W) >= b1) break;
+        load_tile(b + 2 * W, s1);
+        compute_tile(b, s2);
+        if ((b += W) >= b1) break;
+      }
+    }
+  }
+
+  // Every lane takes the (max, sum) of all heads of its row group, then the
+  // four row groups of the wave are merged (lanes 16 and 32 apart).
+  float m[G], l[G];
+  static_for<0, G>([&](auto hc) {
+    constexpr int h = decltype(hc)::value;
+    m[h] = bcast16<h>(m_own);
+    l[h] = bcast16<h>(l_own);
+  });
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mo = __shfl_xor(m[h], off);
+      const float lo = __shfl_xor(l[h], off);
+      const float mn = __builtin_fmaxf(m[h], mo);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float as = __builtin_amdgcn_exp2f(m[h] - mref);
+      const float ao = __builtin_amdgcn_exp2f(mo - mref);
+      l[h] = l[h] * as + lo * ao;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[h][e] = acc[h][e] * as + __shfl_xor(acc[h][e], off) * ao;
+      m[h] = mn;
+    }
+  }
+
+  const int64_t qh0 = qi * n_heads + (int64_t)kvh * G;
+  const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
+  if constexpr (NW == 1) {
+    // One wave: the lanes of row group 0 hold the merged numerators.
+    if (lq == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        if (direct) {
+          const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
+          float *o = out + (qh0 + h) * HD + lr * E;
+#pragma unroll
+          for (int e = 0; e < E; ++e) o[e] = l[h] > 0.f ? acc[h][e] * inv : 0.f;
+        } else {
+          const int64_t pi = (qh0 + h) * max_parts + part;
+#pragma unroll
+          for (int e = 0; e < E; ++e) part_o[pi * HD + lr * E + e] = acc[h][e];
+          if (lr == 0) {
+            part_ml[2 * pi] = m[h];
+            part_ml[2 * pi + 1] = l[h];
+          }
+        }
+      }
+    }
+    return;
+  }
+
+  // Merge the waves through LDS.
+  __shared__ float sm_acc[NW][G][HD];
+  __shared__ float sm_m[NW][G], sm_l[NW][G];
+  if (lq == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) sm_acc[wave][h][lr * E + e] = acc[h][e];
+      if (lr == 0) {
+        sm_m[wave][h] = m[h];
+        sm_l[wave][h] = l[h];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW) {
+    const int h = idx / HD, d = idx - h * HD;
+    float mx = sm_m[0][h];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float a = __builtin_amdgcn_exp2f(sm_m[w][h] - mref);
+      lsum += sm_l[w][h] * a;
+      o += sm_acc[w][h][d] * a;
+    }
+    if (direct) {
+      out[(qh0 + h) * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+    } else {
+      const int64_t pi = (qh0 + h) * max_parts + part;
+      part_o[pi * HD + d] = o;
+      if (d == 0) {
+        part_ml[2 * pi] = mx;
+        part_ml[2 * pi + 1] = lsum;
+      }
+    }
+  }
+}
+
+// Which pools take the MFMA-score kernel: q8_0, whose 1-byte elements make
+// the VALU kernels VALU-bound (measured: 141 us for the Llama-3-8B batch of
+// 64 x 2-4k contexts against 113 us here). For f16 the VALU kernel already
+// streams at the rate of its access pattern and stays.
+constexpr bool kMfmaDecodeQ8 = true, kMfmaDecodeF16 = false;
+
+// One wave per work-group: each wave streams a whole partition, which for
+// the q8_0 pools measured 10% faster than four waves sharing it.
+template <typename T, int HD, int G>
+hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
+  attn_mfma_kernel<T, HD, G, 1><<<grid, 64, 0, s>>>(
+      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
+      a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
+      g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts, a.pre_parts, a.qmap,
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
+  return launch_merge<HD>(a, s);
+}
+
 template <typename T, int HD, int G>
 hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
@@ -1283,7 +1726,9 @@ constexpr bool kRow16 = HD / Tile<T>::E == 16;
 
 template <typename T, int HD, int G>
 hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  if constexpr (kRow16<T, HD>)
+  if constexpr ((kMfmaDecodeQ8 && std::is_same_v<T, int8_t>) || (kMfmaDecodeF16 && std::is_same_v<T, _Float16>))
+    return launch_attn_mfma_t<T, HD, G>(g, a, s);
+  else if constexpr (kRow16<T, HD>)
     return launch_attn16_t<T, HD, G>(g, a, s);
   else
     return launch_attn_t<T, HD, G>(g, a, s);
@@ -1329,7 +1774,6 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 // ds_read_b64_tr_b16 within each 16-lane group: lane i, element j is element
 // i % 4 of the 8 bytes addressed by lane 4 j + i / 4.
 // ----------------------------------------------------------------------------
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) hf4 lds_hf4;
 typedef __attribute__((address_space(3))) char lds_char;

@@ -354,8 +354,9 @@ class KvCache:
 
     def read_scales(self, layer: int = 0) -> tuple[np.ndarray, np.ndarray]:
         """K and V scale pools of one layer of a q8_0 cache,
-        [n_blocks][16][kv_dim/32] f16 bits (uint16) on the host."""
-        shape = (self.n_blocks, BLOCK, self.kv_dim // 32)
+        [n_blocks][kv_dim/32][16] f16 bits (uint16) on the host: the scale of
+        slot s, 32-element group g of block b is [b][g][s]."""
+        shape = (self.n_blocks, self.kv_dim // 32, BLOCK)
         k = np.empty(shape, dtype=np.uint16)
         v = np.empty(shape, dtype=np.uint16)
         _check(self._lib.ltkv_read_scales(self._h, layer, _np_ptr(k), _np_ptr(v)))

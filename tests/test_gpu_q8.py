@@ -32,10 +32,10 @@ def _assert_q8_equal(g, o, layers):
         ok, ov = o.pool(layer)
         np.testing.assert_array_equal(gk, ok, err_msg=f"K quants, layer {layer}")
         np.testing.assert_array_equal(gv, ov, err_msg=f"V quants, layer {layer}")
-        gks, gvs = g.read_scales(layer)
-        oks, ovs = o.scales(layer)
-        np.testing.assert_array_equal(gks, oks, err_msg=f"K scales, layer {layer}")
-        np.testing.assert_array_equal(gvs, ovs, err_msg=f"V scales, layer {layer}")
+        gks, gvs = g.read_scales(layer)  # [block][group][slot]
+        oks, ovs = o.scales(layer)       # [block][slot][group]
+        np.testing.assert_array_equal(gks, oks.transpose(0, 2, 1), err_msg=f"K scales, layer {layer}")
+        np.testing.assert_array_equal(gvs, ovs.transpose(0, 2, 1), err_msg=f"V scales, layer {layer}")
 
 
 def q8_rows(rng, n, kv_dim):
