@@ -52,7 +52,7 @@ def _args():
     return p.parse_args()
 
 
-TRAFFIC_PROFILE = "profiles/attn16_llama3_decode.md"
+TRAFFIC_PROFILE = "profiles/attn_mfma_llama3_decode.md"
 
 
 def _profiled_traffic():
@@ -797,7 +797,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(att_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": _profiled_traffic(),
                      "traffic_source": TRAFFIC_PROFILE,
-                     "kernel": "attn16_kernel + attn_merge_kernel (one decode-attention launch)",
+                     "kernel": "attn_mfma_kernel + attn_merge_kernel (one decode-attention launch)",
                      "bytes_per_launch": round(att_bytes)},
         "wall_s": round(wall, 3),
         "cpu_baseline": cpu,

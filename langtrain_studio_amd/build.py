@@ -18,8 +18,10 @@ HEADERS = [os.path.join(CSRC, "ltkv_kernels.h"), os.path.join(os.path.dirname(PK
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-# Packed FP32 (v_pk_*_f32) is disabled for all device code.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Packed FP32 (v_pk_*_f32) is disabled for all device code. MFMA operands and
+# results live in VGPRs: with AGPR accumulators the decode attention kernel
+# copied its 32 accumulators between AGPRs and VGPRs on every tile.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wno-unused-command-line-argument"]
 
 

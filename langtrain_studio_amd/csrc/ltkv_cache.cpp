@@ -1060,14 +1060,10 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   const bool grouped = P.groups > 0;
   // Grouped plans are batch-dependent anyway: when every query's remainder is
   // short (forks reading a few private blocks), their per-query pass takes
-  // the plan's partition and single-wave work-groups unless a partition is
-  // fixed; long remainders keep the four-wave per-query policy.
+  // the plan's partition unless one is fixed; long remainders keep the
+  // per-query policy.
   int part = (int)c->attn_part_tokens;
-  int waves = 4;
-  if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) {
-    part = P.suffix_part;
-    waves = 1;
-  }
+  if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) part = P.suffix_part;
   const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
   if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
@@ -1087,7 +1083,6 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
   a.lens = d + P.off_slens;
-  a.waves = waves;
   if (P.n_pass < P.n) {  // only the queries that groups did not complete
     a.n = (int64_t)P.n_pass;
     a.qmap = d + P.off_qmap;

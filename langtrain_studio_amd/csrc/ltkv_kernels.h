@@ -72,7 +72,6 @@ struct AttnArgs {
   const int32_t *pre_parts;
   const float *pre_o, *pre_ml;
   int max_pre_parts;
-  int waves;  // 1: single-wave work-groups (f16 x 128 only), else four
   // Queries the launch covers: qmap[0..n) (query indices), or all n when null.
   const int32_t *qmap;
 };

@@ -26,6 +26,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) hf4 lds_hf4;
+typedef __attribute__((address_space(3))) char lds_char;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8 bytes addressed by lane 4 j + i / 4 as its element j.
+__device__ __forceinline__ hf4 lds_read_tr(const char *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4 *)(lds_char *)p);
+}
 
 // ----------------------------------------------------------------------------
 // f32 -> f16, IEEE round-to-nearest-even (the conversion of f16::from_f32).
@@ -347,7 +357,8 @@ gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpo
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 4: GQA paged decode attention.
+// Kernel 4: GQA paged decode attention, VALU form (f32 pools; f16 and q8_0
+// pools take attn_mfma_kernel below).
 //
 // Work-group = 4 waves on (query, kv head, context partition). The waves take
 // the partition's blocks round-robin. For one block a wave reads the head's
@@ -377,22 +388,10 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Element tile of the VALU decode kernels (f32 pools): 4 elements per
+// 16-byte load.
 template <typename T>
 struct Tile;
-
-// The whole 16-byte vector is bit-cast at once: this clang drops a
-// __builtin_bit_cast whose operand is a single ext-vector element (u.y).
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-template <>
-struct Tile<_Float16> {
-  static constexpr int E = 8;  // elements per 16-byte load
-  __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[8]) {
-    const f16x8 h = __builtin_bit_cast(f16x8, u);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
-  }
-};
 
 template <>
 struct Tile<float> {
@@ -402,28 +401,6 @@ struct Tile<float> {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = v[i];
   }
-};
-
-typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
-
-template <>
-struct Tile<int8_t> {  // q8_0 quants, 8 per 8-byte load: the block scale is applied by the caller
-  static constexpr int E = 8;
-  __device__ static __forceinline__ void unpack(const u32x2 &u, float (&f)[8]) {
-    const i8x8 b = __builtin_bit_cast(i8x8, u);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = (float)b[i];
-  }
-};
-
-// Register vector of one lane's load of a tile row: 16 bytes, 8 for q8_0.
-template <typename T>
-struct TileVec {
-  using type = u32x4;
-};
-template <>
-struct TileVec<int8_t> {
-  using type = u32x2;
 };
 
 constexpr int kAttnWaves = 4;
@@ -439,11 +416,9 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
             int max_parts, const int32_t *__restrict__ pre_parts,
-            const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
-            const uint16_t *__restrict__ vscale) {
+            const int32_t *__restrict__ qmap) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
-  constexpr bool Q8 = std::is_same_v<T, int8_t>;  // q8_0: per-32 f16 scales in kscale/vscale
   constexpr int RPL = 64 / L;      // rows per wave load
   constexpr int LOADS = 16 / RPL;  // wave loads per 16-row tile
   static_assert(L >= 4 && L <= 32 && LOADS >= 1, "unsupported head_dim / dtype");
@@ -500,30 +475,19 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
   const int64_t head_off = (int64_t)kvh * head_stride;
 
-  // q8_0: a lane's E elements lie in one 32-element group; its scale sits at
-  // (block * (kv_dim / 32) + group) * 16 + slot of the scale pool.
-  const int64_t sl_groups = slot_stride >> 5;
-  const int64_t sl_lane = (head_off + c * E) >> 5;
-  float ksc[2][LOADS], vsc[2][LOADS];  // scales of the two tiles in flight (q8_0 only)
-  using TV = typename TileVec<T>::type;
-  auto load_tile = [&](int b, TV (&kr)[LOADS], TV (&vr)[LOADS], int st) {
+  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
     int32_t blk = tab[b];
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
     const int64_t base = (int64_t)blk * block_stride + head_off + lane_off;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int64_t o = base + (int64_t)j * RPL * slot_stride;
-      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(kpool + o));
-      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const TV *>(vpool + o));
-      if constexpr (Q8) {
-        const int64_t so = (((int64_t)blk * sl_groups + sl_lane) << 4) + rg + j * RPL;
-        ksc[st][j] = (float)__builtin_bit_cast(_Float16, kscale[so]);
-        vsc[st][j] = (float)__builtin_bit_cast(_Float16, vscale[so]);
-      }
+      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kpool + o));
+      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vpool + o));
     }
   };
 
-  auto compute_tile = [&](int b, const TV (&kr)[LOADS], const TV (&vr)[LOADS], int st) {
+  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
     const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     float s[LOADS][G];
 #pragma unroll
@@ -535,7 +499,6 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
         float a = 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) a = __builtin_fmaf(qv[h][e], kf[e], a);
-        if constexpr (Q8) a *= ksc[st][j];  // dot(q, d * k) = d * dot(q, k) within the block
         s[j][h] = group_sum<L>(a);
       }
     }
@@ -570,18 +533,14 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
     for (int j = 0; j < LOADS; ++j) {
       float vf[E];
       Tile<T>::unpack(vr[j], vf);
-      const bool stale = valid < 16 && rg + j * RPL >= valid;
-      if (stale) {
+      if (valid < 16 && rg + j * RPL >= valid) {
 #pragma unroll
         for (int e = 0; e < E; ++e) vf[e] = 0.f;  // stale slots may hold non-finite bits
       }
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float w = p[j][h];
-        if constexpr (Q8) w = stale ? 0.f : w * vsc[st][j];  // weight times the V block scale
+      for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
-      }
+        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(p[j][h], vf[e], acc[h][e]);
     }
   };
 
@@ -589,18 +548,18 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   // one is computed. Past the end the prefetch re-reads the current tile
   // (cache hit) so the wait counts stay static.
   {
-    TV ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
+    u32x4 ka[LOADS], va[LOADS], kb[LOADS], vb[LOADS];
     int b = b0 + wave;
-    if (b < b1) load_tile(b, ka, va, 0);
+    if (b < b1) load_tile(b, ka, va);
     while (b < b1) {
       const int bn = b + kAttnWaves < b1 ? b + kAttnWaves : b;
-      load_tile(bn, kb, vb, 1);
-      compute_tile(b, ka, va, 0);
+      load_tile(bn, kb, vb);
+      compute_tile(b, ka, va);
       b += kAttnWaves;
       if (b >= b1) break;
       const int bn2 = b + kAttnWaves < b1 ? b + kAttnWaves : b;
-      load_tile(bn2, ka, va, 0);
-      compute_tile(b, kb, vb, 1);
+      load_tile(bn2, ka, va);
+      compute_tile(b, kb, vb);
       b += kAttnWaves;
     }
   }
@@ -742,8 +701,8 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 4, 16-lane form (f16 head_dim 128 and f32 head_dim 64: one 16-byte
-// load per lane covers a row across 16 lanes, a DPP row).
+// Kernel 4, 16-lane VALU form (f32 head_dim 64: one 16-byte load per lane
+// covers a row across 16 lanes, a DPP row).
 //
 // Differences from attn_kernel, all aimed at VALU count per KV byte:
 //  * the rows x heads partial dots of a tile are reduce-scattered over the 16
@@ -870,12 +829,9 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
               int max_parts, const int32_t *__restrict__ pre_parts,
-              const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
-              const uint16_t *__restrict__ vscale) {
+              const int32_t *__restrict__ qmap) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
-  using TV = typename TileVec<T>::type;
-  constexpr bool Q8 = std::is_same_v<T, int8_t>;  // q8_0: per-32 f16 scales in kscale/vscale
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
   constexpr int GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;  // group padded to a power of two
   // Groups of 8 heads scatter the tile in two passes of two row slots, which
@@ -958,16 +914,10 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   // Per-lane byte offsets inside a head tile, fixed for the whole loop.
   const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
-  const uint32_t col_off = (uint32_t)(c * (int)sizeof(TV));
+  const uint32_t col_off = (uint32_t)(c * 16);
   uint32_t roff[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) roff[j] = (uint32_t)(rg + RPL * j) * row_bytes + col_off;
-  // q8_0: a lane's 8 elements lie in one 32-element group; the head's scales
-  // of a block are the run [block][head groups][16 slots] of the scale pool.
-  const int64_t sgroups = slot_stride >> 5;                     // groups per row
-  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 32;  // bytes to the head's groups
-  const uint32_t sgrp = (uint32_t)(c * E >> 5) * 32;             // bytes to this lane's group
-  float ksc[3][LOADS], vsc[3][LOADS];  // scales of the tiles in flight (q8_0 only)
   int my_row[NPL];  // tile rows of this lane's scores after the scatter
   {
     int jj = 0;
@@ -994,7 +944,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
   // row inside the context: rows past it (and every row of a prefetch past
   // the wave's last tile, extent 0) read as zeros without touching memory,
   // so every load is unconditional and the wait counts stay static.
-  auto load_tile = [&](int b, TV (&kr)[LOADS], TV (&vr)[LOADS], int st) {
+  auto load_tile = [&](int b, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
     const int bb = b < b1 ? b : b1 - 1;
     int32_t blk = tab[bb];
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
@@ -1007,36 +957,12 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
         (void *)(vbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      if constexpr (sizeof(TV) == 16) {
-        kr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b128(rk, roff[j], 0, kNt));
-        vr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b128(rv, roff[j], 0, kNt));
-      } else {
-        kr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b64(rk, roff[j], 0, kNt));
-        vr[j] = __builtin_bit_cast(TV, __builtin_amdgcn_raw_buffer_load_b64(rv, roff[j], 0, kNt));
-      }
-    }
-    if constexpr (Q8) {  // the rows' group scales; zero past the context
-      const int sext = rows > 0 ? HD / 32 * 32 : 0;
-      const int64_t sblk = (int64_t)blk * sgroups * 32 + shead;
-      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
-      const __amdgpu_buffer_rsrc_t sv = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
-#pragma unroll
-      for (int j = 0; j < LOADS; ++j) {
-        const uint32_t so = sgrp + (uint32_t)(rg + RPL * j) * 2;
-        ksc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sk, so, 0, 0));
-        vsc[st][j] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(sv, so, 0, 0));
-      }
-      if (rows < 16) {  // slots past the context may hold any scale (inf: d * 0 = NaN)
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j)
-          if (rg + RPL * j >= rows) ksc[st][j] = vsc[st][j] = 0.f;
-      }
+      kr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, roff[j], 0, kNt));
+      vr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, roff[j], 0, kNt));
     }
   };
 
-  auto compute_tile = [&](int b, const TV (&kr)[LOADS], const TV (&vr)[LOADS], int st) {
+  auto compute_tile = [&](int b, const u32x4 (&kr)[LOADS], const u32x4 (&vr)[LOADS]) {
     const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     float sc[NPL];  // this lane's scores: one per pass
 #pragma unroll
@@ -1066,7 +992,6 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
           float a = 0.f;
 #pragma unroll
           for (int e = 0; e < E; ++e) a = __builtin_fmaf(qu[e], kf[jj][e], a);
-          if constexpr (Q8) a *= ksc[st][pass * RPP + jj];  // the lane's block scale
           v[u * RPP + jj] = a;
         }
       }
@@ -1112,8 +1037,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
       static_for<0, G>([&](auto hc) {
         constexpr int h = decltype(hc)::value;
         // (head h, row slot j): pass j / RPP, index h * RPP + j % RPP of it
-        float w = bcast16<S::src(h * RPP + j % RPP)>(p[j / RPP]);
-        if constexpr (Q8) w *= vsc[st][j];  // the V row's block scale for this lane
+        const float w = bcast16<S::src(h * RPP + j % RPP)>(p[j / RPP]);
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
       });
@@ -1128,29 +1052,29 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     int b = b0 + wave;
     if (b < b1) {
       if constexpr (STAGES == 3) {
-        TV k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS], k2[LOADS], v2[LOADS];
-        load_tile(b, k0, v0, 0);
-        load_tile(b + W, k1, v1, 1);
+        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS], k2[LOADS], v2[LOADS];
+        load_tile(b, k0, v0);
+        load_tile(b + W, k1, v1);
         for (;;) {
-          load_tile(b + 2 * W, k2, v2, 2);
-          compute_tile(b, k0, v0, 0);
+          load_tile(b + 2 * W, k2, v2);
+          compute_tile(b, k0, v0);
           if ((b += W) >= b1) break;
-          load_tile(b + 2 * W, k0, v0, 0);
-          compute_tile(b, k1, v1, 1);
+          load_tile(b + 2 * W, k0, v0);
+          compute_tile(b, k1, v1);
           if ((b += W) >= b1) break;
-          load_tile(b + 2 * W, k1, v1, 1);
-          compute_tile(b, k2, v2, 2);
+          load_tile(b + 2 * W, k1, v1);
+          compute_tile(b, k2, v2);
           if ((b += W) >= b1) break;
         }
       } else {
-        TV k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
-        load_tile(b, k0, v0, 0);
+        u32x4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
+        load_tile(b, k0, v0);
         for (;;) {
-          load_tile(b + W, k1, v1, 1);
-          compute_tile(b, k0, v0, 0);
+          load_tile(b + W, k1, v1);
+          compute_tile(b, k0, v0);
           if ((b += W) >= b1) break;
-          load_tile(b + W, k0, v0, 0);
-          compute_tile(b, k1, v1, 1);
+          load_tile(b + W, k0, v0);
+          compute_tile(b, k1, v1);
           if ((b += W) >= b1) break;
         }
       }
@@ -1250,24 +1174,26 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 4 with the scores on MFMA (f16 and q8_0 tiles). The per-element work
-// of the VALU kernels above, a G-way dot product per K element and a G-way
-// FMA per V element, keeps the VALU busy for most of the time the tile's
-// bytes take to arrive (and longer for 1-byte q8_0 elements). Here the score
-// product of a 16-token tile runs as HD/32 v_mfma_f32_16x16x32_f16:
-//   S^T[token][col] = K Q'^T   A = the K tile straight from the loads
-//                              (lane l: token l % 16, d = 32 ks + 8 (l / 16)),
-//                              B = Q' in registers, D lane l: tokens
-//                              4 (l / 16) + i of column l % 16.
-// Q is f32, split into f16 hi + lo parts held in two columns of Q' (head h
-// in column h, its lo part in column 15 - h), so one MFMA covers both and a
-// row_mirror DPP add sums them: scores keep f32 accuracy over the exact f16
-// (or int8) K elements. q8_0 tiles convert exactly to f16 and each k step
-// (one 32-element scale block) accumulates separately, scaled by its block
-// scale afterwards. The V side stays on the VALU in the D layout: lane
-// (l % 16, l / 16) holds HD/16 elements of tokens 4 (l / 16) + i, and takes
-// the weight of head h from lane h of its row (row_newbcast). Softmax state
-// is per lane row group, merged at the end as in attn16_kernel.
+// Kernel 4 on the matrix cores (f16 and q8_0 tiles). In the VALU kernels
+// every K element costs a G-way dot product and every V element a G-way
+// FMA; with 1-byte q8_0 elements (or G > 4) that keeps the VALU busy for
+// longer than the tile's bytes take to arrive. Here both products of a
+// 16-token tile run on MFMA, one wave per (query, kv head, partition):
+//   S^T[token][col] = K Q'^T   v_mfma_f32_16x16x32_f16, A = the K tile
+//                              (staged through LDS into the A layout),
+//                              B = Q' in registers;
+//   O^T[d][col]   += V^T P'^T  v_mfma_f32_16x16x16_f16, A = V^T read from
+//                              LDS with ds_read_b64_tr_b16, B = P' in the
+//                              D layout of S^T (lane: tokens 4 (l/16) + j).
+// Q' and P' hold f32 values as f16 hi + lo parts in mirrored columns (head
+// h in column h, its lo part in column 15 - h): one MFMA covers both and a
+// row_mirror DPP add joins them, so scores and sums keep f32 accuracy over
+// exact f16 (or int8) elements. q8_0 tiles convert exactly to f16; each
+// 32-element scale group is a k step of the score product, scaled after
+// it, and a separate P' (P times the V group scale) for the O tiles of the
+// group. The softmax reference per column is common to the four lane rows
+// and raised only when a score exceeds it by kDecodeSlack (ballot), so the
+// weights p = 2^(s - ref) <= 2^8 need no exchange on the fast path.
 // ----------------------------------------------------------------------------
 template <int B>
 struct BufVec;
@@ -1326,8 +1252,29 @@ __device__ __forceinline__ void unpack_row(const V &v, float (&f)[E]) {
   }
 }
 
-template <typename T, int HD, int G, int NW>
-__global__ void __launch_bounds__(64 * NW)
+constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
+
+// int8 x 4 -> f16 x 4, exact (as i8x8_to_h8).
+__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
+  constexpr uint32_t kHi = 0x64646464u;
+  const uint32_t a = w ^ 0x80808080u;
+  const h2 bias = {(_Float16)1152.f, (_Float16)1152.f};
+  const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04010400u)) - bias;
+  const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04030402u)) - bias;
+  return h4{p0.x, p0.y, p1.x, p1.y};
+}
+
+// f32 -> the f16 part this lane's column holds: hi (column < G), lo (column
+// >= 16 - G), zero otherwise.
+template <int G>
+__device__ __forceinline__ _Float16 column_part(float x, int col) {
+  const _Float16 h = (_Float16)x;
+  const _Float16 l = (_Float16)(x - (float)h);
+  return col < G ? h : (col >= 16 - G ? l : (_Float16)0.f);
+}
+
+template <typename T, int HD, int G>
+__global__ void __launch_bounds__(64)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
                  const int32_t *__restrict__ tables, int64_t table_stride,
                  const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
@@ -1337,23 +1284,26 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
                  const uint16_t *__restrict__ vscale) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
-  constexpr int KS = HD / 32;                  // MFMA k steps: one q8_0 scale group each
-  constexpr int E = HD / 16;                   // V elements per lane per token
-  constexpr int RB = HD * (int)sizeof(T);      // bytes of a head row
-  constexpr int CB = RB / 16;                  // bytes of a lane's slice of a row (16 lanes a row)
-  constexpr int KB = 8 * (int)sizeof(T);       // bytes of an MFMA A slice (8 elements)
-  constexpr int PITCH = RB + 16;               // LDS bytes per staged K row
+  constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
+  constexpr int DT = HD / 16;              // 16-row tiles of O^T
+  constexpr int E = HD / 16;               // elements of a row per lane (16 lanes a row)
+  constexpr int RB = HD * (int)sizeof(T);  // bytes of a head row
+  constexpr int CB = RB / 16;              // bytes of a lane's slice of a row
+  constexpr int KB = 8 * (int)sizeof(T);   // bytes of an A slice of the score product
+  constexpr int KPITCH = RB + 16;          // LDS bytes per staged K row
+  constexpr int VPITCH = HD * 2 + 16;      // LDS bytes per staged V row (f16)
   using CV = typename BufVec<CB>::type;
+  using KV = typename BufVec<KB>::type;
   static_assert(G >= 1 && G <= 8, "hi and lo columns of the group must fit 16");
-  static_assert(HD % 32 == 0 && (E == 4 || E == 8), "head_dim 64 or 128");
-  __shared__ __attribute__((aligned(16))) char sk_lds[NW][16 * PITCH];  // wave-private K tile
+  static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+  __shared__ __attribute__((aligned(16))) char sk[16 * KPITCH];
+  __shared__ __attribute__((aligned(16))) char sv[16 * VPITCH];
 
   const int kvh = (int)(blockIdx.x % n_kv_heads);
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
   const int64_t qx = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
   const int64_t qi = qmap ? qmap[qx] : qx;
   const int lane = threadIdx.x & 63;
-  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 15, lq = lane >> 4;
   const int n_heads = n_kv_heads * G;
 
@@ -1365,13 +1315,13 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
   const int pt = partition_tokens(len, part_tokens);
   const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
-  if (part >= np) return;  // uniform over the work-group
+  if (part >= np) return;
   const int64_t tok0 = (int64_t)part * pt;
   const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
-  // B operand Q'^T: column lr < G holds the hi part of head lr, column
-  // 15 - h the lo part of head h; the other columns are zero.
+  // B operand Q'^T of the score product: k slice 32 ks + 8 lq .. + 8 of
+  // column lr (hi part of head lr, or lo part of head 15 - lr).
   h8 qb[KS];
   {
     const bool hi = lr < G, lo = lr >= 16 - G;
@@ -1379,57 +1329,45 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     const float *qp = q + qi * (int64_t)n_heads * HD + ((int64_t)kvh * G + ((hi || lo) ? h : 0)) * HD + 8 * lq;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      float x[8];
       const f32x4 a = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
       const f32x4 b = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[e] = a[e] * qscale;
-        x[4 + e] = b[e] * qscale;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const _Float16 xh = (_Float16)x[e];
-        qb[ks][e] = hi ? xh : lo ? (_Float16)(x[e] - (float)xh) : (_Float16)0.f;
+        qb[ks][e] = column_part<G>(a[e] * qscale, lr);
+        qb[ks][4 + e] = column_part<G>(b[e] * qscale, lr);
       }
     }
   }
 
-  // Per-lane byte offsets. K and V are both loaded in row order, 16 lanes a
-  // row (lane (lr, lq) takes rows 4 lq + i, bytes [CB lr, CB lr + CB)): K is
-  // then staged through LDS into the MFMA A layout, V is used in place.
+  // Rows are loaded in order, 16 lanes a row: lane (lr, lq) takes bytes
+  // [CB lr, CB lr + CB) of rows 4 lq + i.
   const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
   uint32_t roff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) roff[i] = (uint32_t)(4 * lq + i) * row_bytes + (uint32_t)(lr * CB);
-  // q8_0 scales: the head's groups of a block are the run [HD / 32 groups][16
-  // slots]; a lane reads the four slots 4 lq .. 4 lq + 3 of a group at once.
+  // q8_0 scales: a kv head's groups of a block are the run [HD / 32][16
+  // slots]; a lane reads slots 4 lq .. 4 lq + 3 of every group.
   const int64_t sgroups = slot_stride >> 5;
   const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 32;
-  const uint32_t vsoff = (uint32_t)((lr * E) >> 5) * 32 + (uint32_t)(8 * lq);
   const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh * head_stride);
   const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh * head_stride);
   const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
-  char *sk = sk_lds[wave];
 
-  float m_own = -INFINITY, l_own = 0.f;  // softmax state of head lr (or 15 - lr), row group lq
-  float acc[G][E];
+  float m_ref = -INFINITY, l_run = 0.f;  // softmax reference and sum of this lane's column
+  f32x4 o[DT];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int32_t *tab = tables + qi * table_stride;
 
   struct Stage {
     CV k[4], v[4];
-    u32x2 ks[Q8 ? KS : 1];  // q8_0: K scales of slots 4 lq .. 4 lq + 3, per group
-    u32x2 vs;               // q8_0: V scales of the lane's group, slots 4 lq .. 4 lq + 3
+    u32x2 ks[Q8 ? KS : 1], vs[Q8 ? KS : 1];  // q8_0: slots 4 lq .. 4 lq + 3 of each group
   };
 
   // Loads go through buffer descriptors whose extent ends at the last row
   // inside the context: rows past it (and every row of a prefetch past the
-  // wave's last tile, extent 0) read as zeros without touching memory.
+  // last tile, extent 0) read as zeros without touching memory.
   auto load_tile = [&](int b, Stage &st) {
     const int bb = b < b1 ? b : b1 - 1;
     int32_t blk = tab[bb];
@@ -1454,35 +1392,45 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       const __amdgpu_buffer_rsrc_t svr = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) st.ks[ks] = BufVec<8>::template load<0>(skr, (uint32_t)(ks * 32 + 8 * lq));
-      st.vs = BufVec<8>::template load<0>(svr, vsoff);
+      for (int g = 0; g < KS; ++g) {
+        st.ks[g] = BufVec<8>::template load<0>(skr, (uint32_t)(g * 32 + 8 * lq));
+        st.vs[g] = BufVec<8>::template load<0>(svr, (uint32_t)(g * 32 + 8 * lq));
+      }
       if (rows < 16) {  // slots past the context may hold any scale (inf: d * 0 = NaN)
         typedef uint16_t s4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          s4 x = __builtin_bit_cast(s4, st.ks[ks]);
+        for (int g = 0; g < KS; ++g) {
+          s4 x = __builtin_bit_cast(s4, st.ks[g]), y = __builtin_bit_cast(s4, st.vs[g]);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (4 * lq + i >= rows) x[i] = 0;
-          st.ks[ks] = __builtin_bit_cast(u32x2, x);
+            if (4 * lq + i >= rows) x[i] = y[i] = 0;
+          st.ks[g] = __builtin_bit_cast(u32x2, x);
+          st.vs[g] = __builtin_bit_cast(u32x2, y);
         }
-        s4 y = __builtin_bit_cast(s4, st.vs);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (4 * lq + i >= rows) y[i] = 0;
-        st.vs = __builtin_bit_cast(u32x2, y);
       }
     }
   };
 
   auto compute_tile = [&](int b, const Stage &st) {
-    // K tile into the A layout: row lr, elements 32 ks + 8 lq .. + 8.
+    // Stage K (as loaded) and V (as f16) in LDS, row order.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<CV *>(sk + (4 * lq + i) * PITCH + lr * CB) = st.k[i];
-    typename BufVec<KB>::type ka[KS];
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<CV *>(sk + (4 * lq + i) * KPITCH + lr * CB) = st.k[i];
+      if constexpr (Q8) {
+        if constexpr (E == 8)
+          *reinterpret_cast<h8 *>(sv + (4 * lq + i) * VPITCH + lr * 16) = i8x8_to_h8(st.v[i]);
+        else
+          *reinterpret_cast<h4 *>(sv + (4 * lq + i) * VPITCH + lr * 8) = i8x4_to_h4(st.v[i]);
+      } else {
+        *reinterpret_cast<CV *>(sv + (4 * lq + i) * VPITCH + lr * CB) = st.v[i];
+      }
+    }
+    KV ka[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      ka[ks] = *reinterpret_cast<const typename BufVec<KB>::type *>(sk + lr * PITCH + (32 * ks + 8 * lq) * (int)sizeof(T));
+      ka[ks] = *reinterpret_cast<const KV *>(sk + lr * KPITCH + (32 * ks + 8 * lq) * (int)sizeof(T));
+
+    // Scores of tokens 4 lq + i, column lr.
     f32x4 s;
     if constexpr (Q8) {
       f32x4 c[KS];
@@ -1490,7 +1438,6 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       for (int ks = 0; ks < KS; ++ks)
         c[ks] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(ka[ks]), qb[ks], f32x4{0.f, 0.f, 0.f, 0.f},
                                                        0, 0, 0);
-      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const h4 d = __builtin_bit_cast(h4, st.ks[ks]);
@@ -1512,170 +1459,106 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       for (int i = 0; i < 4; ++i)
         if (4 * lq + i >= valid) sc[i] = -INFINITY;
     }
-    // Online softmax of this lane's head over its row group's tokens.
-    const float bm = __builtin_fmaxf(__builtin_fmaxf(sc[0], sc[1]), __builtin_fmaxf(sc[2], sc[3]));
-    const float mn = __builtin_fmaxf(m_own, bm);
-    const float mref = mn == -INFINITY ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m_own - mref);
+
+    // Softmax against the column's common reference, raised (with the
+    // accumulators rescaled) only when a score exceeds it by the slack.
+    const float lmax = __builtin_fmaxf(__builtin_fmaxf(sc[0], sc[1]), __builtin_fmaxf(sc[2], sc[3]));
+    if (__builtin_amdgcn_ballot_w64(lmax > m_ref + kDecodeSlack)) {
+      float mx = __builtin_fmaxf(lmax, __shfl_xor(lmax, 16));
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+      if (mx > m_ref + kDecodeSlack) {
+        const float alpha = __builtin_amdgcn_exp2f(m_ref - mx);
+        m_ref = mx;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      }
+    }
+    const float mref = m_ref == -INFINITY ? 0.f : m_ref;
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
-    l_own = l_own * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    const bool grew = mn > m_own;
-    m_own = mn;
-    if (__builtin_amdgcn_ballot_w64(grew)) {  // wave-uniform: some head's max grew
-      static_for<0, G>([&](auto hc) {
-        constexpr int h = decltype(hc)::value;
-        const float a = bcast16<h>(alpha);
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+
+    // O^T += V^T P'^T, per 16-row tile of d; q8_0: P' carries the V scale of
+    // the tile's 32-element group.
+    h4 pf = {};
+    if constexpr (!Q8) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[h][e] *= a;
-      });
+      for (int i = 0; i < 4; ++i) pf[i] = column_part<G>(p[i], lr);
     }
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    const h4 vsd = __builtin_bit_cast(h4, st.vs);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float vf[E];
-      unpack_row<T, E>(st.v[i], vf);
-      float vsc = 1.f;
-      if constexpr (Q8) vsc = (float)vsd[i];
-      static_for<0, G>([&](auto hc) {
-        constexpr int h = decltype(hc)::value;
-        float w = bcast16<h>(p[i]);
-        if constexpr (Q8) w *= vsc;
+    for (int g = 0; g < KS; ++g) {
+      h4 pb = pf;
+      if constexpr (Q8) {
+        const h4 d = __builtin_bit_cast(h4, st.vs[g]);
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[h][e] = __builtin_fmaf(w, vf[e], acc[h][e]);
-      });
+        for (int i = 0; i < 4; ++i) pb[i] = column_part<G>(p[i] * (float)d[i], lr);
+      }
+#pragma unroll
+      for (int dt = 2 * g; dt < 2 * g + 2; ++dt) {
+        const hf4 a = lds_read_tr(sv + (4 * lq + (lr >> 2)) * VPITCH + (dt * 16 + 4 * (lr & 3)) * 2);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), pb, o[dt], 0, 0, 0);
+      }
     }
   };
 
   // Software pipeline: two tiles in flight while one is computed. Loads
-  // past the wave's last tile read nothing (extent 0).
+  // past the last tile read nothing (extent 0).
   {
-    constexpr int W = NW;
-    int b = b0 + wave;
+    int b = b0;
     if (b < b1) {
       Stage s0, s1, s2;
       load_tile(b, s0);
-      load_tile(b + W, s1);
+      load_tile(b + 1, s1);
       for (;;) {
-        load_tile(b + 2 * W, s2);
+        load_tile(b + 2, s2);
         compute_tile(b, s0);
-        if ((b += W) >= b1) break;
-        load_tile(b + 2 * W, s0);
+        if (++b >= b1) break;
+        load_tile(b + 2, s0);
         compute_tile(b, s1);
-        if ((b += W) >= b1) break;
-        load_tile(b + 2 * W, s1);
+        if (++b >= b1) break;
+        load_tile(b + 2, s1);
         compute_tile(b, s2);
-        if ((b += W) >= b1) break;
+        if (++b >= b1) break;
       }
     }
   }
 
-  // Every lane takes the (max, sum) of all heads of its row group, then the
-  // four row groups of the wave are merged (lanes 16 and 32 apart).
-  float m[G], l[G];
-  static_for<0, G>([&](auto hc) {
-    constexpr int h = decltype(hc)::value;
-    m[h] = bcast16<h>(m_own);
-    l[h] = bcast16<h>(l_own);
-  });
+  // Column sums over the four lane rows; hi + lo parts of the numerators.
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
 #pragma unroll
-  for (int off = 16; off < 64; off <<= 1) {
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float mo = __shfl_xor(m[h], off);
-      const float lo = __shfl_xor(l[h], off);
-      const float mn = __builtin_fmaxf(m[h], mo);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float as = __builtin_amdgcn_exp2f(m[h] - mref);
-      const float ao = __builtin_amdgcn_exp2f(mo - mref);
-      l[h] = l[h] * as + lo * ao;
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[h][e] = acc[h][e] * as + __shfl_xor(acc[h][e], off) * ao;
-      m[h] = mn;
-    }
-  }
+    for (int i = 0; i < 4; ++i) o[dt][i] += dpp<0x140>(o[dt][i]);
 
-  const int64_t qh0 = qi * n_heads + (int64_t)kvh * G;
-  const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
-  if constexpr (NW == 1) {
-    // One wave: the lanes of row group 0 hold the merged numerators.
-    if (lq == 0) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        if (direct) {
-          const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
-          float *o = out + (qh0 + h) * HD + lr * E;
-#pragma unroll
-          for (int e = 0; e < E; ++e) o[e] = l[h] > 0.f ? acc[h][e] * inv : 0.f;
-        } else {
-          const int64_t pi = (qh0 + h) * max_parts + part;
-#pragma unroll
-          for (int e = 0; e < E; ++e) part_o[pi * HD + lr * E + e] = acc[h][e];
-          if (lr == 0) {
-            part_ml[2 * pi] = m[h];
-            part_ml[2 * pi + 1] = l[h];
-          }
-        }
-      }
-    }
-    return;
-  }
-
-  // Merge the waves through LDS.
-  __shared__ float sm_acc[NW][G][HD];
-  __shared__ float sm_m[NW][G], sm_l[NW][G];
-  if (lq == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-#pragma unroll
-      for (int e = 0; e < E; ++e) sm_acc[wave][h][lr * E + e] = acc[h][e];
-      if (lr == 0) {
-        sm_m[wave][h] = m[h];
-        sm_l[wave][h] = l[h];
-      }
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW) {
-    const int h = idx / HD, d = idx - h * HD;
-    float mx = sm_m[0][h];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, sm_m[w][h]);
-    const float mref = mx == -INFINITY ? 0.f : mx;
-    float lsum = 0.f, o = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float a = __builtin_amdgcn_exp2f(sm_m[w][h] - mref);
-      lsum += sm_l[w][h] * a;
-      o += sm_acc[w][h][d] * a;
-    }
+  if (lr < G) {  // lane (h, lq) holds rows d = 16 dt + 4 lq + i of head h
+    const int64_t qh = qi * n_heads + (int64_t)kvh * G + lr;
+    const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
     if (direct) {
-      out[(qh0 + h) * HD + d] = lsum > 0.f ? o / lsum : 0.f;
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4 *>(out + qh * HD + 16 * dt + 4 * lq) =
+            l_run > 0.f ? o[dt] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
-      const int64_t pi = (qh0 + h) * max_parts + part;
-      part_o[pi * HD + d] = o;
-      if (d == 0) {
-        part_ml[2 * pi] = mx;
-        part_ml[2 * pi + 1] = lsum;
+      const int64_t pi = qh * max_parts + part;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(part_o + pi * HD + 16 * dt + 4 * lq) = o[dt];
+      if (lq == 0) {
+        part_ml[2 * pi] = m_ref;
+        part_ml[2 * pi + 1] = l_run;
       }
     }
   }
 }
 
-// Which pools take the MFMA-score kernel: q8_0, whose 1-byte elements make
-// the VALU kernels VALU-bound (measured: 141 us for the Llama-3-8B batch of
-// 64 x 2-4k contexts against 113 us here). For f16 the VALU kernel already
-// streams at the rate of its access pattern and stays.
-constexpr bool kMfmaDecodeQ8 = true, kMfmaDecodeF16 = false;
-
-// One wave per work-group: each wave streams a whole partition, which for
-// the q8_0 pools measured 10% faster than four waves sharing it.
+// One wave per work-group: each wave streams a whole partition.
 template <typename T, int HD, int G>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
-  attn_mfma_kernel<T, HD, G, 1><<<grid, 64, 0, s>>>(
+  attn_mfma_kernel<T, HD, G><<<grid, 64, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts, a.pre_parts, a.qmap,
@@ -1686,24 +1569,11 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
 template <typename T, int HD, int G>
 hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
-  // Single-wave work-groups (short per-query contexts) exist for f16 x 128.
-  if constexpr (std::is_same_v<T, _Float16> && HD == 128) {
-    if (a.waves == 1) {
-      attn16_kernel<T, HD, G, 1><<<grid, 64, 0, s>>>(
-          static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
-          a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
-          g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens,
-          a.max_parts, a.pre_parts, a.qmap,
-      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
-      return launch_merge<HD>(a, s);
-    }
-  }
   attn16_kernel<T, HD, G, kAttnWaves><<<grid, 64 * kAttnWaves, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap,
-      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
+      a.pre_parts, a.qmap);
   return launch_merge<HD>(a, s);
 }
 
@@ -1714,19 +1584,19 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap,
-      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
+      a.pre_parts, a.qmap);
   return launch_merge<HD>(a, s);
 }
 
-// 16 lanes per row (f16 x 128, f32 x 64) take attn16_kernel; the other
-// shapes (8 or 32 lanes per row) take attn_kernel + attn_merge_kernel.
+// f16 and q8_0 pools take the matrix-core kernel. f32 pools (no f32 MFMA
+// form keeps the products exact at this rate) stay on the VALU: 16 lanes per
+// row (f32 x 64) take attn16_kernel, 32 lanes per row (f32 x 128) attn_kernel.
 template <typename T, int HD>
 constexpr bool kRow16 = HD / Tile<T>::E == 16;
 
 template <typename T, int HD, int G>
 hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  if constexpr ((kMfmaDecodeQ8 && std::is_same_v<T, int8_t>) || (kMfmaDecodeF16 && std::is_same_v<T, _Float16>))
+  if constexpr (!std::is_same_v<T, float>)
     return launch_attn_mfma_t<T, HD, G>(g, a, s);
   else if constexpr (kRow16<T, HD>)
     return launch_attn16_t<T, HD, G>(g, a, s);
@@ -1774,9 +1644,6 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 // ds_read_b64_tr_b16 within each 16-lane group: lane i, element j is element
 // i % 4 of the 8 bytes addressed by lane 4 j + i / 4.
 // ----------------------------------------------------------------------------
-typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) hf4 lds_hf4;
-typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr int kMqChunk = 32;       // tokens per staging step
 constexpr float kMqSlack = 8.f;    // log2 headroom of the softmax reference
@@ -1790,9 +1657,6 @@ __device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
   }
 }
 
-__device__ __forceinline__ hf4 lds_read_tr(const char *p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4 *)(lds_char *)p);
-}
 
 constexpr int kMqWaves = 4;  // waves per work-group
 
