@@ -436,20 +436,22 @@ def bench_rope_append(args):
     """Fused RoPE + append (model.rs:414-429 in one launch) at the Qwen2.5-7B
     continuous-batching step: 4216 tokens (8 prefill chunks x 512 + 120 decode
     tokens) at positions U[0, 8704), 28 q heads / 4 kv heads / 128, NeoX pairs;
-    and at the Llama-3-8B shape with 4096 tokens (interleaved pairs). Bytes per
-    token: K and V f32 read + f16 written, Q f32 read and written, slot and
-    position; the cos/sin table reads are not counted (cache-resident)."""
+    and at the Llama-3-8B shape with 4096 tokens (interleaved pairs), into f16
+    and into q8_0 cells. Bytes per token: K and V f32 read + f16 (or q8_0
+    quants and scales) written, Q f32 read and written, slot and position;
+    the cos/sin table reads are not counted (cache-resident)."""
     import torch
 
     from langtrain_studio_amd import KvCache
 
     rng = np.random.default_rng(args.seed)
     rows = []
-    for name, n_heads, n_kv, hd, n, neox, base in (("qwen2.5-7b", 28, 4, 128, 4216, True, 1e6),
-                                                     ("llama3-8b", 32, 8, 128, 4096, False, 5e5)):
+    for dtype, name, n_heads, n_kv, hd, n, neox, base in (
+            ("f16", "qwen2.5-7b", 28, 4, 128, 4216, True, 1e6), ("f16", "llama3-8b", 32, 8, 128, 4096, False, 5e5),
+            ("q8_0", "qwen2.5-7b", 28, 4, 128, 4216, True, 1e6), ("q8_0", "llama3-8b", 32, 8, 128, 4096, False, 5e5)):
         kvd = n_kv * hd
         n_blocks = n // BLOCK + 64
-        kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+        kv = KvCache(1, kvd, n_blocks * BLOCK, dtype=dtype, device=0, stream=torch.cuda.current_stream())
         kv.init_free_order(rng.permutation(n_blocks))
         kv.rope_init(base, hd, hd, neox, 8704)
         sm = torch.from_numpy(kv.append_batch(np.zeros(n, np.uint32), np.arange(n, dtype=np.uint64))).cuda()
@@ -459,8 +461,10 @@ def bench_rope_append(args):
         q = torch.randn((n, n_heads * hd), device="cuda")
         fused = _time_op(lambda: kv.write_rope(0, sm, pos, k, v, q=q, n_heads=n_heads), reps=20)
         plain = _time_op(lambda: kv.write_batch(0, sm, k, v), reps=20)
-        nbytes = n * (kvd * (4 + 2) * 2 + n_heads * hd * 8 + 8)
+        cell = 2 if dtype == "f16" else 1 + 2 / 32  # bytes written per K/V element (q8_0: quant + scale share)
+        nbytes = int(n * (kvd * (4 + cell) * 2 + n_heads * hd * 8 + 8))
         rows.append({"shape": f"{name}: {n} tokens, {n_heads}q/{n_kv}kv x {hd}, {'neox' if neox else 'interleaved'}",
+                     "dtype": dtype,
                      "fused_us": round(fused, 2), "bytes": nbytes,
                      "GBps": round(nbytes / (fused * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (fused * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),

@@ -70,8 +70,8 @@ enum {
  * bytes), scales in K/V scale pools ([n_blocks][kv_dim/32][16] f16: per
  * block, the 16 slots of each 32-element group are adjacent, so one kv
  * head's scales of a block are one contiguous run).
- * kv_dim must be a multiple of 32. Gather, rows and the RoPE append have no
- * Q8_0 form (LTKV_ERR_ARG). */
+ * kv_dim must be a multiple of 32 (head_dim too for the RoPE append). Gather
+ * and rows have no Q8_0 form (LTKV_ERR_ARG). */
 enum { LTKV_F16 = 0, LTKV_F32 = 1, LTKV_Q8_0 = 2 };
 
 /* Thread-local message of the last failing call on this thread. */
@@ -163,7 +163,8 @@ LTKV_API int ltkv_rope_init(ltkv_cache *c, float base, size_t rope_dim, size_t h
  * its cell as ltkv_write does) and, when d_q is not null, on its Q rows
  * ([n][q_stride], n_heads heads) in place; V appended unrotated. Tokens with
  * a position outside the table are skipped (nothing written). Bit-identical
- * to the reference's f32 rotation (no fused multiply-add) and f16 rounding. */
+ * to the reference's f32 rotation (no fused multiply-add) and f16 rounding
+ * (Q8_0 cells: the rotated K row quantised as ltkv_write does). */
 LTKV_API int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
                     const int32_t *d_positions, const float *d_k, const float *d_v, size_t src_stride,
                     float *d_q, size_t q_stride, size_t n_heads);

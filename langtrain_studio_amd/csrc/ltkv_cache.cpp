@@ -918,13 +918,14 @@ int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
   if (!c->rope) return fail(LTKV_ERR_ARG, "no RoPE table (ltkv_rope_init)");
-  if (c->q8()) return fail(LTKV_ERR_ARG, "the RoPE append has no Q8_0 form");
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
   if (n == 0) return LTKV_OK;
   if (!d_slot_mapping || !d_positions || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
   if (src_stride < c->kv_dim || src_stride % 4 != 0)
     return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
   const size_t hd = (size_t)c->rope_geom.head_dim;
+  if (c->q8() && hd % 32 != 0)
+    return fail(LTKV_ERR_ARG, "the Q8_0 RoPE append needs head_dim a multiple of 32 (whole scale groups per head)");
   if (d_q && (n_heads == 0 || q_stride < n_heads * hd || q_stride % 4 != 0))
     return fail(LTKV_ERR_ARG, "q_stride must be >= n_heads * head_dim and a multiple of 4");
   if (((uintptr_t)d_k | (uintptr_t)d_v | (uintptr_t)d_q) % 16 != 0)
@@ -933,10 +934,17 @@ int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot
   if ((uint64_t)n * per >= (1ull << 32) - 256) return fail(LTKV_ERR_ARG, "too many rows for one launch");
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  HIP_TRY(ltkv::launch_write_rope(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping,
-                                  d_positions, d_k, d_v, d_q, (int64_t)n, (int64_t)src_stride,
-                                  (int64_t)q_stride, (int)n_heads, c->rope_geom, c->stream),
-          "write_rope launch");
+  if (c->q8())
+    HIP_TRY(ltkv::launch_write_rope_q8(c->geom, c->k_layer(layer), c->v_layer(layer), c->k_scales(layer),
+                                       c->v_scales(layer), d_slot_mapping, d_positions, d_k, d_v, d_q,
+                                       (int64_t)n, (int64_t)src_stride, (int64_t)q_stride, (int)n_heads,
+                                       c->rope_geom, c->stream),
+            "write_rope launch");
+  else
+    HIP_TRY(ltkv::launch_write_rope(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping,
+                                    d_positions, d_k, d_v, d_q, (int64_t)n, (int64_t)src_stride,
+                                    (int64_t)q_stride, (int)n_heads, c->rope_geom, c->stream),
+            "write_rope launch");
   return LTKV_OK;
 }
 

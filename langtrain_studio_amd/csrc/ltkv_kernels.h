@@ -43,6 +43,13 @@ hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, co
                             int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
                             const RopeGeom &r, hipStream_t s);
 
+// The same for q8_0 cells: K rotated then quantised per 32 elements, V
+// quantised, Q rotated in place.
+hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale, void *v_scale,
+                               const int32_t *slots, const int32_t *positions, const float *k, const float *v,
+                               float *q, int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
+                               const RopeGeom &r, hipStream_t s);
+
 hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
                               const int32_t *pairs, int64_t n_pairs, hipStream_t s);
 

@@ -107,6 +107,35 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
 // -> 0, as `as i8`); the 32 quants go to the cell and d, rounded to f16, to
 // the scale pool (the Q8_0 block of quant.rs:188-193: f16 d + 32 int8).
 // ----------------------------------------------------------------------------
+// quant.rs:785-791 on one 32-element group: amax folded with fmaxf (a NaN
+// element is skipped, as f32::max), d = amax / 127, id = 1/d (0 when d is 0),
+// q = roundf(x * id) (half away from zero) saturated to int8 with NaN -> 0
+// (Rust's `as i8`); 32 quants to dq (16-byte aligned), d as f16 to *ds.
+__device__ __forceinline__ void quantize_store(const float (&x)[32], int8_t *__restrict__ dq,
+                                               uint16_t *__restrict__ ds) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
+  const float d = amax / 127.f;
+  const float id = d > 0.f ? 1.f / d : 0.f;
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float r = __builtin_roundf(x[4 * i + j] * id);  // half away from zero
+      int qv = 0;
+      if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
+      word |= (uint32_t)(qv & 0xff) << (8 * j);
+    }
+    w[i] = word;
+  }
+  *reinterpret_cast<u32x4 *>(dq) = u32x4{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<u32x4 *>(dq + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  *ds = (uint16_t)f16_bits(d);
+}
+
 __global__ void __launch_bounds__(256)
 write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
                 uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
@@ -131,31 +160,11 @@ write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t
     x[i + 2] = t.z;
     x[i + 3] = t.w;
   }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
-  const float d = amax / 127.f;
-  const float id = d > 0.f ? 1.f / d : 0.f;
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float r = __builtin_roundf(x[4 * i + j] * id);  // half away from zero
-      int qv = 0;
-      if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
-      word |= (uint32_t)(qv & 0xff) << (8 * j);
-    }
-    w[i] = word;
-  }
   const int64_t cell = (int64_t)s * kv_dim + blk * 32;
-  int8_t *dq = (is_v ? vpool : kpool) + cell;
-  *reinterpret_cast<u32x4 *>(dq) = u32x4{w[0], w[1], w[2], w[3]};
-  *reinterpret_cast<u32x4 *>(dq + 16) = u32x4{w[4], w[5], w[6], w[7]};
   // Scale pool layout [block][kv_dim / 32][16 slots]: the scales of one kv
   // head of a block are one contiguous run (HD / 32 x 16 x 2 bytes).
-  (is_v ? vscale : kscale)[(((int64_t)(s >> 4) * (kv_dim >> 5) + blk) << 4) + (s & 15)] = (uint16_t)f16_bits(d);
+  quantize_store(x, (is_v ? vpool : kpool) + cell,
+                 (is_v ? vscale : kscale) + ((((int64_t)(s >> 4) * (kv_dim >> 5) + blk) << 4) + (s & 15)));
 }
 
 // ----------------------------------------------------------------------------
@@ -178,6 +187,49 @@ __device__ __forceinline__ void rope_pairs(const float *__restrict__ cs, float (
   }
 }
 
+// One unit of a head row (4 rotation pairs, or 8 unrotated elements past
+// rope_dim): its element offsets e0 .. e0+3 and e1 .. e1+3 within the head
+// and the rotated values in o.
+__device__ __forceinline__ void rope_unit(const float *__restrict__ head, int w, int pos,
+                                          const float *__restrict__ table, int rope_dim, int neox,
+                                          int &e0, int &e1, float (&o)[8]) {
+  const int upr = rope_dim >> 3;
+  if (w >= upr) {  // past rope_dim: unrotated
+    e0 = (upr << 3) + ((w - upr) << 3);
+    e1 = e0 + 4;
+  } else if (neox) {
+    e0 = w << 2;
+    e1 = e0 + (rope_dim >> 1);
+  } else {
+    e0 = w << 3;
+    e1 = e0 + 4;
+  }
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(head + e0);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(head + e1);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  if (w < upr) {
+    const float *cs = table + ((int64_t)pos * (rope_dim >> 1)) * 2;
+    if (neox) {  // pairs (e0 + p, e1 + p), pair index e0 + p
+      float x0[4] = {o[0], o[1], o[2], o[3]}, x1[4] = {o[4], o[5], o[6], o[7]};
+      rope_pairs(cs + 2 * e0, x0, x1);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        o[p] = x0[p];
+        o[4 + p] = x1[p];
+      }
+    } else {  // pairs (e0 + 2p, e0 + 2p + 1), pair index e0 / 2 + p
+      float x0[4] = {o[0], o[2], o[4], o[6]}, x1[4] = {o[1], o[3], o[5], o[7]};
+      rope_pairs(cs + e0, x0, x1);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        o[2 * p] = x0[p];
+        o[2 * p + 1] = x1[p];
+      }
+    }
+  }
+}
+
 template <int ELEM>
 __global__ void __launch_bounds__(256)
 write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
@@ -186,7 +238,6 @@ write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
                   int64_t n, int64_t src_stride, int64_t q_stride, int kv_dim, int n_kv_heads,
                   int n_heads, int64_t n_slots, const float *__restrict__ table, int max_pos,
                   int rope_dim, int head_dim, int neox) {
-  const int upr = rope_dim >> 3;          // rotary units per head
   const int uph = head_dim >> 3;          // units per head
   const int ku = n_kv_heads * uph;        // K units per token
   const int vu = kv_dim >> 3;             // V units per token
@@ -226,41 +277,9 @@ write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
   const int h = u / uph, w = u - h * uph;
   const float *src = is_q ? q + row * q_stride : k + row * src_stride;
   const int hb = h * head_dim;
-  // Element offsets (within the head) of the unit's two halves of 4.
   int e0, e1;
-  if (w >= upr) {  // past rope_dim: unrotated
-    e0 = (upr << 3) + ((w - upr) << 3);
-    e1 = e0 + 4;
-  } else if (neox) {
-    e0 = w << 2;
-    e1 = e0 + (rope_dim >> 1);
-  } else {
-    e0 = w << 3;
-    e1 = e0 + 4;
-  }
-  const f32x4 a = *reinterpret_cast<const f32x4 *>(src + hb + e0);
-  const f32x4 b = *reinterpret_cast<const f32x4 *>(src + hb + e1);
-  float o[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};  // elements e0..e0+3, e1..e1+3
-  if (w < upr) {
-    const float *cs = table + ((int64_t)pos * (rope_dim >> 1)) * 2;
-    if (neox) {  // pairs (e0 + p, e1 + p), pair index e0 + p
-      float x0[4] = {o[0], o[1], o[2], o[3]}, x1[4] = {o[4], o[5], o[6], o[7]};
-      rope_pairs(cs + 2 * e0, x0, x1);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        o[p] = x0[p];
-        o[4 + p] = x1[p];
-      }
-    } else {  // pairs (e0 + 2p, e0 + 2p + 1), pair index e0 / 2 + p
-      float x0[4] = {o[0], o[2], o[4], o[6]}, x1[4] = {o[1], o[3], o[5], o[7]};
-      rope_pairs(cs + e0, x0, x1);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        o[2 * p] = x0[p];
-        o[2 * p + 1] = x1[p];
-      }
-    }
-  }
+  float o[8];
+  rope_unit(src + hb, w, pos, table, rope_dim, neox, e0, e1, o);
   if (is_q) {
     float *qd = q + row * q_stride + hb;
     *reinterpret_cast<f32x4 *>(qd + e0) = f32x4{o[0], o[1], o[2], o[3]};
@@ -277,6 +296,118 @@ write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
     *reinterpret_cast<f32x4 *>(kd + e0) = f32x4{o[0], o[1], o[2], o[3]};
     *reinterpret_cast<f32x4 *>(kd + e1) = f32x4{o[4], o[5], o[6], o[7]};
   }
+}
+
+// ----------------------------------------------------------------------------
+// Kernel 1 with RoPE for q8_0 cells: a thread owns one 32-element group of
+// K (rotated, then quantised as write_q8_kernel), one group of V
+// (quantised), or one 8-element unit of Q (rotated in place, as
+// write_rope_kernel). A K group rotates element by element with the same
+// products as rope_pairs: (2i, 2i+1) partners lie inside the group; NeoX
+// partners (i, i + rope_dim/2) are read as a second 32-element run when the
+// group lies on one side of rope_dim/2, else one by one.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void load32(const float *__restrict__ src, float (&x)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; i += 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4 *>(src + i);
+    x[i] = t.x;
+    x[i + 1] = t.y;
+    x[i + 2] = t.z;
+    x[i + 3] = t.w;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
+                     uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
+                     const int32_t *__restrict__ positions, const float *__restrict__ k,
+                     const float *__restrict__ v, float *__restrict__ q, int64_t n, int64_t src_stride,
+                     int64_t q_stride, int kv_dim, int n_heads, int64_t n_slots,
+                     const float *__restrict__ table, int max_pos, int rope_dim, int head_dim, int neox) {
+#pragma clang fp contract(off)
+  const int kg = kv_dim >> 5;             // K (and V) groups per token
+  const int uph = head_dim >> 3;          // Q units per head
+  const int qu = q ? n_heads * uph : 0;   // Q units per token
+  const int per = 2 * kg + qu;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / per;
+  if (row >= n) return;
+  int u = (int)(gid - row * per);
+  const int32_t pos = positions[row];
+  if (pos < 0 || pos >= max_pos) return;
+  const int32_t s = slots[row];
+  const bool cell = s >= 0 && (int64_t)s < n_slots;
+  if (u >= 2 * kg) {  // Q unit: rotated in place
+    u -= 2 * kg;
+    const int h = u / uph, w = u - h * uph;
+    float *qh = q + row * q_stride + (int64_t)h * head_dim;
+    int e0, e1;
+    float o[8];
+    rope_unit(qh, w, pos, table, rope_dim, neox, e0, e1, o);
+    *reinterpret_cast<f32x4 *>(qh + e0) = f32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<f32x4 *>(qh + e1) = f32x4{o[4], o[5], o[6], o[7]};
+    return;
+  }
+  if (!cell) return;
+  const bool is_v = u >= kg;
+  const int g = is_v ? u - kg : u;
+  float x[32];
+  if (is_v) {
+    load32(v + row * src_stride + g * 32, x);
+  } else {
+    const int h = (g * 32) / head_dim, eh = g * 32 - h * head_dim;  // head and offset in it
+    const float *head = k + row * src_stride + (int64_t)h * head_dim;
+    load32(head + eh, x);
+    if (eh < rope_dim) {
+      const float *cs = table + ((int64_t)pos * (rope_dim >> 1)) * 2;
+      const int half = rope_dim >> 1;
+      float y[32];  // rotated values
+      if (neox) {
+        float pr[32];  // partners
+        const bool below = eh + 32 <= half, above = eh >= half && eh + 32 <= rope_dim;
+        if (below || above) {
+          load32(head + (below ? eh + half : eh - half), pr);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) {
+            const int e = eh + i;
+            pr[i] = e < half ? head[e + half] : (e < rope_dim ? head[e - half] : 0.f);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int e = eh + i;
+          if (e < half) {  // pair (e, e + half): x0 = x[e], x1 = partner
+            const float c = cs[2 * e], sn = cs[2 * e + 1];
+            y[i] = x[i] * c - pr[i] * sn;
+          } else if (e < rope_dim) {  // pair (e - half, e): x0 = partner, x1 = x[e]
+            const float c = cs[2 * (e - half)], sn = cs[2 * (e - half) + 1];
+            y[i] = pr[i] * sn + x[i] * c;
+          } else {
+            y[i] = x[i];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; i += 2) {
+          const int e = eh + i;  // pair (e, e + 1), index e / 2
+          if (e < rope_dim) {
+            const float c = cs[e], sn = cs[e + 1];
+            y[i] = x[i] * c - x[i + 1] * sn;
+            y[i + 1] = x[i] * sn + x[i + 1] * c;
+          } else {
+            y[i] = x[i];
+            y[i + 1] = x[i + 1];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = y[i];
+    }
+  }
+  quantize_store(x, (is_v ? vpool : kpool) + (int64_t)s * kv_dim + g * 32,
+                 (is_v ? vscale : kscale) + ((((int64_t)(s >> 4) * kg + g) << 4) + (s & 15)));
 }
 
 // ----------------------------------------------------------------------------
@@ -1986,6 +2117,20 @@ hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, co
         static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, positions, k, v, q,
         n, src_stride, q_stride, g.kv_dim, n_kv_heads, n_heads, g.n_blocks * 16, r.table, r.max_pos,
         r.rope_dim, r.head_dim, r.neox);
+  return hipGetLastError();
+}
+
+hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale, void *v_scale,
+                               const int32_t *slots, const int32_t *positions, const float *k, const float *v,
+                               float *q, int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
+                               const RopeGeom &r, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t per = 2 * (int64_t)(g.kv_dim >> 5) + (q ? (int64_t)n_heads * (r.head_dim >> 3) : 0);
+  const int64_t blocks = (n * per + 255) / 256;
+  write_rope_q8_kernel<<<(unsigned)blocks, 256, 0, s>>>(
+      static_cast<int8_t *>(k_layer), static_cast<int8_t *>(v_layer), static_cast<uint16_t *>(k_scale),
+      static_cast<uint16_t *>(v_scale), slots, positions, k, v, q, n, src_stride, q_stride, g.kv_dim, n_heads,
+      g.n_blocks * 16, r.table, r.max_pos, r.rope_dim, r.head_dim, r.neox);
   return hipGetLastError();
 }
 

@@ -278,7 +278,47 @@ def test_q8_unsupported_ops_raise(gpu):
     out = torch.zeros((4, 64), dtype=torch.int8, device=gpu)
     with pytest.raises(KvError, match="Q8_0"):
         g.gather(0, t, l, off, out, out.clone())
-    g.rope_init(10000.0, 64, 64, False, 16)
-    x = torch.zeros((1, 64), device=gpu)
-    with pytest.raises(KvError, match="Q8_0"):
-        g.write_rope(0, t.reshape(1), t.reshape(1), x, x)
+    h = KvCache(1, 96, 4 * BLOCK, dtype="q8_0", device=0)
+    h.rope_init(10000.0, 48, 48, False, 16)  # head_dim 48: not whole scale groups
+    x = torch.zeros((1, 96), device=gpu)
+    with pytest.raises(KvError, match="multiple of 32"):
+        h.write_rope(0, t.reshape(1), t.reshape(1), x, x)
+
+
+# ---------------------------------------------------------------------------- fused RoPE append (f2 on q8_0)
+@pytest.mark.parametrize("n_heads,n_kv,head_dim,rope_dim,neox,base", [
+    (32, 8, 128, 128, False, 500000.0),   # Llama-3-8B
+    (28, 4, 128, 128, True, 1000000.0),   # Qwen2.5-7B (NeoX pairs)
+    (8, 2, 128, 64, True, 10000.0),       # partial rotary: groups on one side of rope_dim / 2
+    (4, 2, 64, 48, True, 10000.0),        # groups straddling rope_dim / 2 and rope_dim
+    (4, 2, 64, 48, False, 10000.0),       # interleaved pairs, a group straddling rope_dim
+])
+def test_q8_write_rope_bit_exact(gpu, n_heads, n_kv, head_dim, rope_dim, neox, base):
+    """K rotated (model.rs:291-308) then quantised per 32 elements, V
+    quantised, Q rotated in place: quants, scales and Q bit-identical to the
+    oracle (rotation, then quantize_block), skipped rows included."""
+    import torch
+
+    rng = np.random.default_rng(head_dim * 7 + rope_dim)
+    kv_dim = n_kv * head_dim
+    g, o = _caches(1, kv_dim, 300 * BLOCK, rng.permutation(300))
+    g.rope_init(base, rope_dim, head_dim, neox, 32768)
+    lens = {0: 700, 1: 900, 2: 33}
+    seqs = np.concatenate([np.full(n, s, dtype=np.uint32) for s, n in lens.items()])
+    pos = np.concatenate([np.arange(n, dtype=np.uint64) for n in lens.values()])
+    sm = g.append_batch(seqs, pos)
+    np.testing.assert_array_equal(o.append_batch(seqs, pos), sm)
+    sm[7] = -1
+    n = sm.size
+    k = q8_rows(rng, n, kv_dim)
+    k[~np.isfinite(k)] = 1.0  # rotation mixes elements: keep K finite (V keeps the special blocks)
+    v = q8_rows(rng, n, kv_dim)
+    q = rng.standard_normal((n, n_heads * head_dim), dtype=np.float32)
+    p32 = pos.astype(np.int32) * 37 % 32768
+    dq = torch.from_numpy(q).to(gpu)
+    g.write_rope(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(p32).to(gpu), torch.from_numpy(k).to(gpu),
+                 torch.from_numpy(v).to(gpu), q=dq, n_heads=n_heads)
+    qo = q.copy()
+    o.write_rope_batch(0, sm, p32, k, v, base, rope_dim, head_dim, neox, q=qo, n_heads=n_heads)
+    np.testing.assert_array_equal(dq.cpu().numpy().view(np.uint32), qo.view(np.uint32))
+    _assert_q8_equal(g, o, (0,))
