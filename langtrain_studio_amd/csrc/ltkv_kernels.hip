@@ -1404,6 +1404,25 @@ __device__ __forceinline__ _Float16 column_part(float x, int col) {
   return col < G ? h : (col >= 16 - G ? l : (_Float16)0.f);
 }
 
+// The weight operand's part for this lane: the lo part on lo lanes, else
+// the hi part (columns past the group are discarded, any finite value does).
+__device__ __forceinline__ _Float16 weight_part(float x, bool lo_lane) {
+  const _Float16 h = (_Float16)x;
+  const _Float16 l = (_Float16)(x - (float)h);
+  return lo_lane ? l : h;
+}
+
+// int8 x 8 -> f16 x 8 of 1152 + x (exact; the bias is taken out after the
+// product, where it costs one subtraction per score instead of one per
+// element).
+__device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
+  constexpr uint32_t kHi = 0x64646464u;
+  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
+  const u32x4 r = {__builtin_amdgcn_perm(kHi, a, 0x04010400u), __builtin_amdgcn_perm(kHi, a, 0x04030402u),
+                   __builtin_amdgcn_perm(kHi, b, 0x04010400u), __builtin_amdgcn_perm(kHi, b, 0x04030402u)};
+  return __builtin_bit_cast(h8, r);
+}
+
 template <typename T, int HD, int G>
 __global__ void __launch_bounds__(64)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
@@ -1469,6 +1488,22 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       }
     }
   }
+
+  // q8_0 K enters the score product as 1152 + k: 1152 times the column's
+  // sum of each k step of Q' comes off afterwards.
+  float qbias[KS];
+  if constexpr (Q8) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t += (float)qb[ks][e];
+      t += __shfl_xor(t, 16);
+      t += __shfl_xor(t, 32);
+      qbias[ks] = 1152.f * t;
+    }
+  }
+  const bool lo_lane = lr >= 16 - G;
 
   // Rows are loaded in order, 16 lanes a row: lane (lr, lq) takes bytes
   // [CB lr, CB lr + CB) of rows 4 lq + i.
@@ -1567,13 +1602,16 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       f32x4 c[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        c[ks] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(ka[ks]), qb[ks], f32x4{0.f, 0.f, 0.f, 0.f},
-                                                       0, 0, 0);
+        c[ks] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8_biased(ka[ks]), qb[ks],
+                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const h4 d = __builtin_bit_cast(h4, st.ks[ks]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] = ks == 0 ? (float)d[i] * c[0][i] : __builtin_fmaf((float)d[i], c[ks][i], s[i]);
+        for (int i = 0; i < 4; ++i) {
+          const float t = c[ks][i] - qbias[ks];
+          s[i] = ks == 0 ? (float)d[i] * t : __builtin_fmaf((float)d[i], t, s[i]);
+        }
       }
     } else {
       s = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1616,7 +1654,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     h4 pf = {};
     if constexpr (!Q8) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = column_part<G>(p[i], lr);
+      for (int i = 0; i < 4; ++i) pf[i] = weight_part(p[i], lo_lane);
     }
 #pragma unroll
     for (int g = 0; g < KS; ++g) {
@@ -1624,7 +1662,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       if constexpr (Q8) {
         const h4 d = __builtin_bit_cast(h4, st.vs[g]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = column_part<G>(p[i] * (float)d[i], lr);
+        for (int i = 0; i < 4; ++i) pb[i] = weight_part(p[i] * (float)d[i], lo_lane);
       }
 #pragma unroll
       for (int dt = 2 * g; dt < 2 * g + 2; ++dt) {
