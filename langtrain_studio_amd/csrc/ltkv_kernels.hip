@@ -101,70 +101,73 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 1 for q8_0 cells: one thread quantises one 32-element block of a K
-// or V row as quantize_block (quant.rs:785-791): d = max|x| / 127 (NaN
-// ignored, as f32::max), q = round-half-away(x / d) saturated to int8 (NaN
-// -> 0, as `as i8`); the 32 quants go to the cell and d, rounded to f16, to
-// the scale pool (the Q8_0 block of quant.rs:188-193: f16 d + 32 int8).
+// Kernel 1 for q8_0 cells: each 32-element group of a K or V row becomes 32
+// int8 quants in the cell and its scale d, rounded to f16, in the scale pool
+// (the Q8_0 block of quant.rs:188-193: f16 d + 32 int8).
 // ----------------------------------------------------------------------------
-// quant.rs:785-791 on one 32-element group: amax folded with fmaxf (a NaN
-// element is skipped, as f32::max), d = amax / 127, id = 1/d (0 when d is 0),
-// q = roundf(x * id) (half away from zero) saturated to int8 with NaN -> 0
-// (Rust's `as i8`); 32 quants to dq (16-byte aligned), d as f16 to *ds.
-__device__ __forceinline__ void quantize_store(const float (&x)[32], int8_t *__restrict__ dq,
-                                               uint16_t *__restrict__ ds) {
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
-  const float d = amax / 127.f;
-  const float id = d > 0.f ? 1.f / d : 0.f;
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float r = __builtin_roundf(x[4 * i + j] * id);  // half away from zero
-      int qv = 0;
-      if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
-      word |= (uint32_t)(qv & 0xff) << (8 * j);
-    }
-    w[i] = word;
-  }
-  *reinterpret_cast<u32x4 *>(dq) = u32x4{w[0], w[1], w[2], w[3]};
-  *reinterpret_cast<u32x4 *>(dq + 16) = u32x4{w[4], w[5], w[6], w[7]};
-  *ds = (uint16_t)f16_bits(d);
+// DPP move of x (row_mask and bank_mask all set).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
 }
 
+// quant.rs:785-791 on one 32-element group spread over 4 aligned lanes of
+// a wave, 8 elements each (lane j of the group holds elements 8j .. 8j+7):
+// amax folded with fmaxf from 0 (a NaN element is skipped, as f32::max; an
+// all-NaN group gives 0 as the sequential fold does), then across the 4
+// lanes with quad_perm DPP (max is order-free); d = amax / 127, id = 1/d (0
+// when d is 0), q = roundf(x * id) (half away from zero) saturated to int8
+// with NaN -> 0 (Rust's `as i8`); every lane stores its 8 quants, lane 0 d
+// as f16.
+__device__ __forceinline__ void quantize_store4(const float (&x)[8], int j, int8_t *__restrict__ dq,
+                                                uint16_t *__restrict__ ds) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
+  amax = __builtin_fmaxf(amax, dpp<0xB1>(amax));  // quad_perm [1,0,3,2]: lane ^ 1
+  amax = __builtin_fmaxf(amax, dpp<0x4E>(amax));  // quad_perm [2,3,0,1]: lane ^ 2
+  const float d = amax / 127.f;
+  const float id = d > 0.f ? 1.f / d : 0.f;
+  uint32_t w[2] = {0, 0};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float r = __builtin_roundf(x[i] * id);  // half away from zero
+    int qv = 0;
+    if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
+    w[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+  }
+  *reinterpret_cast<u32x2 *>(dq + 8 * j) = u32x2{w[0], w[1]};
+  if (j == 0) *ds = (uint16_t)f16_bits(d);
+}
+
+// Scale entry of (cell s, group g): layout [block][kv_dim / 32][16 slots],
+// so the scales of one kv head of a block are one contiguous run.
+__device__ __forceinline__ int64_t scale_index(int32_t s, int g, int kg) {
+  return (((int64_t)(s >> 4) * kg + g) << 4) + (s & 15);
+}
+
+// Kernel 1 for q8_0 cells: 4 lanes per 32-element group of K or V, two
+// 16-byte loads and one 8-byte store per lane.
 __global__ void __launch_bounds__(256)
 write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
                 uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
                 const float *__restrict__ k, const float *__restrict__ v, int64_t n, int64_t src_stride,
                 int kv_dim, int64_t n_slots) {
-  const int per = kv_dim >> 4;  // 32-element blocks of K and of V per row
+  const int e8 = kv_dim >> 3;  // 8-element eighths of a K (or V) row
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / per;
-  if (row >= n) return;
-  const int u = (int)(gid - row * per);
+  const int64_t row = gid / (2 * e8);
+  if (row >= n) return;  // whole 4-lane groups leave together (2 e8 is a multiple of 4)
+  const int u = (int)(gid - row * 2 * e8);
   const int32_t s = slots[row];
   if (s < 0 || (int64_t)s >= n_slots) return;
-  const bool is_v = u >= (per >> 1);
-  const int blk = is_v ? u - (per >> 1) : u;
-  const float *src = (is_v ? v : k) + row * src_stride + blk * 32;
-  float x[32];
-#pragma unroll
-  for (int i = 0; i < 32; i += 4) {
-    const f32x4 t = *reinterpret_cast<const f32x4 *>(src + i);
-    x[i] = t.x;
-    x[i + 1] = t.y;
-    x[i + 2] = t.z;
-    x[i + 3] = t.w;
-  }
-  const int64_t cell = (int64_t)s * kv_dim + blk * 32;
-  // Scale pool layout [block][kv_dim / 32][16 slots]: the scales of one kv
-  // head of a block are one contiguous run (HD / 32 x 16 x 2 bytes).
-  quantize_store(x, (is_v ? vpool : kpool) + cell,
-                 (is_v ? vscale : kscale) + ((((int64_t)(s >> 4) * (kv_dim >> 5) + blk) << 4) + (s & 15)));
+  const bool is_v = u >= e8;
+  const int e = (is_v ? u - e8 : u) << 3;  // element offset in the row
+  const f32x4 *src = reinterpret_cast<const f32x4 *>((is_v ? v : k) + row * src_stride + e);
+  const f32x4 t0 = src[0], t1 = src[1];
+  const float x[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+  quantize_store4(x, (e >> 3) & 3, (is_v ? vpool : kpool) + (int64_t)s * kv_dim + (e & ~31),
+                  (is_v ? vscale : kscale) + scale_index(s, e >> 5, kv_dim >> 5));
 }
 
 // ----------------------------------------------------------------------------
@@ -299,25 +302,14 @@ write_rope_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
 }
 
 // ----------------------------------------------------------------------------
-// Kernel 1 with RoPE for q8_0 cells: a thread owns one 32-element group of
-// K (rotated, then quantised as write_q8_kernel), one group of V
-// (quantised), or one 8-element unit of Q (rotated in place, as
-// write_rope_kernel). A K group rotates element by element with the same
-// products as rope_pairs: (2i, 2i+1) partners lie inside the group; NeoX
-// partners (i, i + rope_dim/2) are read as a second 32-element run when the
-// group lies on one side of rope_dim/2, else one by one.
+// Kernel 1 with RoPE for q8_0 cells: 4 lanes per 32-element group of K
+// (rotated, then quantised as write_q8_kernel) or of V (quantised), 8
+// elements a lane; and a thread per 8-element unit of Q (rotated in place,
+// as write_rope_kernel). A lane's K elements rotate with the products of
+// rope_pairs, 4 at a time: (2i, 2i+1) partners lie in the lane, NeoX
+// partners (i, i + rope_dim/2) are the 4 elements rope_dim/2 away (rope_dim
+// is a multiple of 8, so each 4 lie on one side).
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ void load32(const float *__restrict__ src, float (&x)[32]) {
-#pragma unroll
-  for (int i = 0; i < 32; i += 4) {
-    const f32x4 t = *reinterpret_cast<const f32x4 *>(src + i);
-    x[i] = t.x;
-    x[i + 1] = t.y;
-    x[i + 2] = t.z;
-    x[i + 3] = t.w;
-  }
-}
-
 __global__ void __launch_bounds__(256)
 write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
                      uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
@@ -326,20 +318,20 @@ write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uin
                      int64_t q_stride, int kv_dim, int n_heads, int64_t n_slots,
                      const float *__restrict__ table, int max_pos, int rope_dim, int head_dim, int neox) {
 #pragma clang fp contract(off)
-  const int kg = kv_dim >> 5;             // K (and V) groups per token
+  const int e8 = kv_dim >> 3;             // 8-element eighths of a K (or V) row
   const int uph = head_dim >> 3;          // Q units per head
   const int qu = q ? n_heads * uph : 0;   // Q units per token
-  const int per = 2 * kg + qu;
+  // Threads [0, n * 2 e8) take the K/V eighths, the rest the Q units, so a
+  // wave runs one of the two paths.
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / per;
-  if (row >= n) return;
-  int u = (int)(gid - row * per);
+  const int64_t n_kv = n * 2 * e8;
+  const bool q_unit = gid >= n_kv;
+  const int64_t row = q_unit ? (gid - n_kv) / (qu > 0 ? qu : 1) : gid / (2 * e8);
+  if (row >= n || (q_unit && qu == 0)) return;
+  const int u = (int)(q_unit ? gid - n_kv - row * qu : gid - row * 2 * e8);
   const int32_t pos = positions[row];
-  if (pos < 0 || pos >= max_pos) return;
-  const int32_t s = slots[row];
-  const bool cell = s >= 0 && (int64_t)s < n_slots;
-  if (u >= 2 * kg) {  // Q unit: rotated in place
-    u -= 2 * kg;
+  if (pos < 0 || pos >= max_pos) return;  // uniform over a token's 4-lane groups
+  if (q_unit) {  // Q unit: rotated in place
     const int h = u / uph, w = u - h * uph;
     float *qh = q + row * q_stride + (int64_t)h * head_dim;
     int e0, e1;
@@ -349,67 +341,46 @@ write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uin
     *reinterpret_cast<f32x4 *>(qh + e1) = f32x4{o[4], o[5], o[6], o[7]};
     return;
   }
-  if (!cell) return;
-  const bool is_v = u >= kg;
-  const int g = is_v ? u - kg : u;
-  float x[32];
-  if (is_v) {
-    load32(v + row * src_stride + g * 32, x);
-  } else {
-    const int h = (g * 32) / head_dim, eh = g * 32 - h * head_dim;  // head and offset in it
-    const float *head = k + row * src_stride + (int64_t)h * head_dim;
-    load32(head + eh, x);
-    if (eh < rope_dim) {
+  const int32_t s = slots[row];
+  if (s < 0 || (int64_t)s >= n_slots) return;
+  const bool is_v = u >= e8;
+  const int e = (is_v ? u - e8 : u) << 3;  // element offset in the row
+  const float *src = (is_v ? v : k) + row * src_stride;
+  const f32x4 t0 = *reinterpret_cast<const f32x4 *>(src + e), t1 = *reinterpret_cast<const f32x4 *>(src + e + 4);
+  float x[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+  if (!is_v) {
+    const int h = e / head_dim, eh0 = e - h * head_dim;  // head and offset in it
+    if (eh0 < rope_dim) {  // rope_dim is a multiple of 8: all 8 elements rotate
       const float *cs = table + ((int64_t)pos * (rope_dim >> 1)) * 2;
       const int half = rope_dim >> 1;
-      float y[32];  // rotated values
-      if (neox) {
-        float pr[32];  // partners
-        const bool below = eh + 32 <= half, above = eh >= half && eh + 32 <= rope_dim;
-        if (below || above) {
-          load32(head + (below ? eh + half : eh - half), pr);
+#pragma unroll
+      for (int qd = 0; qd < 2; ++qd) {  // the lane's two quads of 4 elements
+        const int eh = eh0 + 4 * qd;
+        if (neox) {
+          const bool lo = eh < half;  // first (lo) or second member of its pairs
+          const f32x4 pt = *reinterpret_cast<const f32x4 *>(src + e + 4 * qd + (lo ? half : -half));
+          const float pr[4] = {pt.x, pt.y, pt.z, pt.w};
+          const int i0 = lo ? eh : eh - half;  // pair index of the quad's element 0
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float c = cs[2 * (i0 + i)], sn = cs[2 * (i0 + i) + 1];
+            x[4 * qd + i] = lo ? x[4 * qd + i] * c - pr[i] * sn : pr[i] * sn + x[4 * qd + i] * c;
+          }
         } else {
 #pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            const int e = eh + i;
-            pr[i] = e < half ? head[e + half] : (e < rope_dim ? head[e - half] : 0.f);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int e = eh + i;
-          if (e < half) {  // pair (e, e + half): x0 = x[e], x1 = partner
-            const float c = cs[2 * e], sn = cs[2 * e + 1];
-            y[i] = x[i] * c - pr[i] * sn;
-          } else if (e < rope_dim) {  // pair (e - half, e): x0 = partner, x1 = x[e]
-            const float c = cs[2 * (e - half)], sn = cs[2 * (e - half) + 1];
-            y[i] = pr[i] * sn + x[i] * c;
-          } else {
-            y[i] = x[i];
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 32; i += 2) {
-          const int e = eh + i;  // pair (e, e + 1), index e / 2
-          if (e < rope_dim) {
-            const float c = cs[e], sn = cs[e + 1];
-            y[i] = x[i] * c - x[i + 1] * sn;
-            y[i + 1] = x[i] * sn + x[i + 1] * c;
-          } else {
-            y[i] = x[i];
-            y[i + 1] = x[i + 1];
+          for (int i = 0; i < 4; i += 2) {  // pair (eh + i, eh + i + 1), index (eh + i) / 2
+            const float c = cs[eh + i], sn = cs[eh + i + 1];
+            const float a = x[4 * qd + i], b = x[4 * qd + i + 1];
+            x[4 * qd + i] = a * c - b * sn;
+            x[4 * qd + i + 1] = a * sn + b * c;
           }
         }
       }
-#pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = y[i];
     }
   }
-  quantize_store(x, (is_v ? vpool : kpool) + (int64_t)s * kv_dim + g * 32,
-                 (is_v ? vscale : kscale) + ((((int64_t)(s >> 4) * kg + g) << 4) + (s & 15)));
+  quantize_store4(x, (e >> 3) & 3, (is_v ? vpool : kpool) + (int64_t)s * kv_dim + (e & ~31),
+                  (is_v ? vscale : kscale) + scale_index(s, e >> 5, kv_dim >> 5));
 }
-
 // ----------------------------------------------------------------------------
 // Kernel 2: block copy. Work item = (pair, layer, tensor, 16 KiB chunk); 256
 // threads each move 4 x 16 bytes, all loads issued before the stores.
@@ -502,11 +473,6 @@ gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpo
 // end. With one partition the work-group writes the normalised output, else
 // it writes (numerator, max, sum) for attn_merge_kernel.
 // ----------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
-}
 
 // Sum over each aligned group of L lanes (L in 4..32); every lane gets it.
 template <int L>
@@ -1448,6 +1414,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
   __shared__ __attribute__((aligned(16))) char sk[16 * KPITCH];
   __shared__ __attribute__((aligned(16))) char sv[16 * VPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t ssc[2][Q8 ? KS * 16 : 1];  // q8_0: K, V scales of a tile
 
   const int kvh = (int)(blockIdx.x % n_kv_heads);
   const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
@@ -1526,9 +1493,13 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   const int32_t *tab = tables + qi * table_stride;
 
+  // q8_0: the tile's K and V scales of this kv head are [KS groups][16 slots]
+  // runs; lane l loads entry l % (16 KS) of each (one register a stage) and
+  // the tile's scales reach their lanes through LDS.
+  const int sidx = lane % (KS * 16);
   struct Stage {
     CV k[4], v[4];
-    u32x2 ks[Q8 ? KS : 1], vs[Q8 ? KS : 1];  // q8_0: slots 4 lq .. 4 lq + 3 of each group
+    uint32_t ks, vs;  // q8_0: scale entry sidx of K and of V
   };
 
   // Loads go through buffer descriptors whose extent ends at the last row
@@ -1557,23 +1528,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
           (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
       const __amdgpu_buffer_rsrc_t svr = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
-#pragma unroll
-      for (int g = 0; g < KS; ++g) {
-        st.ks[g] = BufVec<8>::template load<0>(skr, (uint32_t)(g * 32 + 8 * lq));
-        st.vs[g] = BufVec<8>::template load<0>(svr, (uint32_t)(g * 32 + 8 * lq));
-      }
-      if (rows < 16) {  // slots past the context may hold any scale (inf: d * 0 = NaN)
-        typedef uint16_t s4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-        for (int g = 0; g < KS; ++g) {
-          s4 x = __builtin_bit_cast(s4, st.ks[g]), y = __builtin_bit_cast(s4, st.vs[g]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (4 * lq + i >= rows) x[i] = y[i] = 0;
-          st.ks[g] = __builtin_bit_cast(u32x2, x);
-          st.vs[g] = __builtin_bit_cast(u32x2, y);
-        }
-      }
+      st.ks = __builtin_amdgcn_raw_buffer_load_b16(skr, (uint32_t)(sidx * 2), 0, 0);
+      st.vs = __builtin_amdgcn_raw_buffer_load_b16(svr, (uint32_t)(sidx * 2), 0, 0);
+      if ((sidx & 15) >= rows) st.ks = st.vs = 0;  // slots past the context may hold any scale (inf: d * 0 = NaN)
     }
   };
 
@@ -1591,6 +1548,10 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         *reinterpret_cast<CV *>(sv + (4 * lq + i) * VPITCH + lr * CB) = st.v[i];
       }
     }
+    if constexpr (Q8) {
+      ssc[0][sidx] = (uint16_t)st.ks;
+      ssc[1][sidx] = (uint16_t)st.vs;
+    }
     KV ka[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
@@ -1606,7 +1567,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const h4 d = __builtin_bit_cast(h4, st.ks[ks]);
+        const h4 d = *reinterpret_cast<const h4 *>(&ssc[0][ks * 16 + 4 * lq]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float t = c[ks][i] - qbias[ks];
@@ -1660,7 +1621,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     for (int g = 0; g < KS; ++g) {
       h4 pb = pf;
       if constexpr (Q8) {
-        const h4 d = __builtin_bit_cast(h4, st.vs[g]);
+        const h4 d = *reinterpret_cast<const h4 *>(&ssc[1][g * 16 + 4 * lq]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) pb[i] = weight_part(p[i] * (float)d[i], lo_lane);
       }
@@ -2111,7 +2072,7 @@ hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void
                            void *v_scale, const int32_t *slots, const float *k, const float *v,
                            int64_t n, int64_t src_stride, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  const int64_t threads = n * (g.kv_dim >> 4);
+  const int64_t threads = n * (g.kv_dim >> 2);
   const int64_t blocks = (threads + 255) / 256;
   write_q8_kernel<<<(unsigned)blocks, 256, 0, s>>>(
       static_cast<int8_t *>(k_layer), static_cast<int8_t *>(v_layer), static_cast<uint16_t *>(k_scale),
@@ -2163,7 +2124,7 @@ hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer,
                                float *q, int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
                                const RopeGeom &r, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  const int64_t per = 2 * (int64_t)(g.kv_dim >> 5) + (q ? (int64_t)n_heads * (r.head_dim >> 3) : 0);
+  const int64_t per = 2 * (int64_t)(g.kv_dim >> 3) + (q ? (int64_t)n_heads * (r.head_dim >> 3) : 0);
   const int64_t blocks = (n * per + 255) / 256;
   write_rope_q8_kernel<<<(unsigned)blocks, 256, 0, s>>>(
       static_cast<int8_t *>(k_layer), static_cast<int8_t *>(v_layer), static_cast<uint16_t *>(k_scale),
