@@ -306,6 +306,7 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   a.scale = scale;
   a.part_tokens = part;
   a.max_parts = max_parts;
+  a.split = 1;
   return a;
 }
 
@@ -1016,8 +1017,9 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   // else is in the batch (the reference's property, engine/README.md:102).
   // table_stride only bounds the grid.
   const int part = (int)c->attn_part_tokens;  // 0: per-query policy
+  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim));
   const size_t max_parts =
-      (size_t)ltkv::max_partitions((int64_t)(table_stride * LTKV_BLOCK), part);
+      (size_t)ltkv::max_partitions((int64_t)(table_stride * LTKV_BLOCK), part) * split;
   if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
 
@@ -1028,6 +1030,7 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
   ltkv::AttnArgs a = attn_args(c, layer, n, n_heads, head_dim, scale, d_q, d_out, ws, part,
                                (int)max_parts);
+  a.split = split;
   a.tables = d_tables;
   a.table_stride = (int64_t)table_stride;
   a.lens = d_lens;
@@ -1072,7 +1075,8 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   // per-query policy.
   int part = (int)c->attn_part_tokens;
   if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) part = P.suffix_part;
-  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
+  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim));
+  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part) * split;
   if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
 
@@ -1088,6 +1092,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   const ltkv::PoolGeom g = head_geom(c, P.head_dim);
   ltkv::AttnArgs a = attn_args(c, layer, P.n, P.n_heads, P.head_dim, scale, d_q, d_out, ws, part,
                                (int)max_parts);
+  a.split = split;
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
   a.lens = d + P.off_slens;

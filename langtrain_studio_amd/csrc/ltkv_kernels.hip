@@ -733,7 +733,7 @@ template <int HD>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                   const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
-                  int part_tokens, int max_parts, int64_t max_len,
+                  int part_tokens, int split, int max_parts, int64_t max_len,
                   const int32_t *__restrict__ pre_parts, const float *__restrict__ pre_o,
                   const float *__restrict__ pre_ml, int max_pre_parts,
                   const int32_t *__restrict__ qmap, int64_t n_pairs) {
@@ -748,7 +748,7 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
-  const int pt = partition_tokens(len, part_tokens);
+  const int pt = partition_tokens(len, part_tokens) / split;
   const int npre = pre_parts ? pre_parts[qi] : 0;
   if (npre < 0) return;  // its group wrote the output
   // With group partials the context kernels wrote partials even for a
@@ -791,7 +791,7 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   constexpr int ppw = 256 / (HD / 4);
   const unsigned mgrid = (unsigned)((pairs + ppw - 1) / ppw);
   attn_merge_kernel<HD><<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
-                                              a.part_tokens, a.max_parts, a.table_stride * 16,
+                                              a.part_tokens, a.split, a.max_parts, a.table_stride * 16,
                                               a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
                                               a.qmap, pairs);
   return hipGetLastError();
@@ -1389,7 +1389,7 @@ __device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
   return __builtin_bit_cast(h8, r);
 }
 
-template <typename T, int HD, int G>
+template <typename T, int HD, int G, int NH>
 __global__ void __launch_bounds__(64)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
                  const int32_t *__restrict__ tables, int64_t table_stride,
@@ -1402,23 +1402,31 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
-  constexpr int E = HD / 16;               // elements of a row per lane (16 lanes a row)
-  constexpr int RB = HD * (int)sizeof(T);  // bytes of a head row
-  constexpr int CB = RB / 16;              // bytes of a lane's slice of a row
+  constexpr int RB = HD * (int)sizeof(T);  // bytes of one head's row
+  constexpr int HP = RB / 16;              // 16-byte pieces of a head row
+  constexpr int LPR = NH * HP;             // lanes per row segment (NH adjacent heads)
+  constexpr int RPI = 64 / LPR;            // rows per load instruction
+  constexpr int NLD = 16 / RPI;            // load instructions per tile, K or V
   constexpr int KB = 8 * (int)sizeof(T);   // bytes of an A slice of the score product
   constexpr int KPITCH = RB + 16;          // LDS bytes per staged K row
   constexpr int VPITCH = HD * 2 + 16;      // LDS bytes per staged V row (f16)
-  using CV = typename BufVec<CB>::type;
+  constexpr int NQ = NH * G;               // query heads of the wave
+  constexpr int NSC = NH * KS * 16;        // q8_0 scale entries of a tile, K or V
+  constexpr int STAGES = NH == 1 ? 3 : 2;  // tiles in flight + 1
   using KV = typename BufVec<KB>::type;
-  static_assert(G >= 1 && G <= 8, "hi and lo columns of the group must fit 16");
+  using SV = uint32_t;  // one or two b16 scale entries
+  static_assert(NQ <= 8, "hi and lo columns of the wave's query heads must fit 16");
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
-  __shared__ __attribute__((aligned(16))) char sk[16 * KPITCH];
-  __shared__ __attribute__((aligned(16))) char sv[16 * VPITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t ssc[2][Q8 ? KS * 16 : 1];  // q8_0: K, V scales of a tile
+  static_assert(LPR <= 64 && RPI * NLD == 16, "row segment must split over the wave");
+  __shared__ __attribute__((aligned(16))) char sk[NH][16 * KPITCH];
+  __shared__ __attribute__((aligned(16))) char sv[NH][16 * VPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t ssc[2][Q8 ? NSC : 1];  // q8_0: K, V scales of a tile
 
-  const int kvh = (int)(blockIdx.x % n_kv_heads);
-  const int part = (int)((blockIdx.x / n_kv_heads) % max_parts);
-  const int64_t qx = blockIdx.x / ((unsigned)n_kv_heads * max_parts);
+  // 1-D grid: (query, NH-head group, partition), the head group fastest.
+  const int n_groups = n_kv_heads / NH;
+  const int kvh0 = (int)(blockIdx.x % n_groups) * NH;
+  const int part = (int)((blockIdx.x / n_groups) % max_parts);
+  const int64_t qx = blockIdx.x / ((unsigned)n_groups * max_parts);
   const int64_t qi = qmap ? qmap[qx] : qx;
   const int lane = threadIdx.x & 63;
   const int lr = lane & 15, lq = lane >> 4;
@@ -1430,32 +1438,37 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // A query with group partials and nothing else to read (or whose group
   // wrote its output) has no work here.
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
-  const int pt = partition_tokens(len, part_tokens);
+  const int pt = partition_tokens(len, part_tokens) / NH;  // NH heads a wave: partitions NH x finer
   const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;
   const int64_t tok0 = (int64_t)part * pt;
   const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
   const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
 
-  // B operand Q'^T of the score product: k slice 32 ks + 8 lq .. + 8 of
-  // column lr (hi part of head lr, or lo part of head 15 - lr).
-  h8 qb[KS];
+  // B operands Q'_a^T of the score product, one per kv head a of the wave:
+  // column lr < NQ holds the hi part of query head lr of the wave, column
+  // 15 - j the lo part of query head j; a column is nonzero only in the
+  // operand of its query head's kv head (j / G).
+  const bool hi_lane = lr < NQ, lo_lane = lr >= 16 - NQ;
+  const int qj = hi_lane ? lr : (lo_lane ? 15 - lr : 0);  // the column's query head in the wave
+  const int my_head = qj / G;                             // its kv head in the wave
+  h8 qb[NH][KS];
   {
-    const bool hi = lr < G, lo = lr >= 16 - G;
-    const int h = hi ? lr : 15 - lr;
-    const float *qp = q + qi * (int64_t)n_heads * HD + ((int64_t)kvh * G + ((hi || lo) ? h : 0)) * HD + 8 * lq;
+    const float *qp = q + qi * (int64_t)n_heads * HD + ((int64_t)kvh0 * G + qj) * HD + 8 * lq;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const f32x4 a = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
-      const f32x4 b = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
+      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qb[ks][e] = column_part<G>(a[e] * qscale, lr);
-        qb[ks][4 + e] = column_part<G>(b[e] * qscale, lr);
+      for (int e = 0; e < 8; ++e) {
+        const float x = (e < 4 ? x0[e] : x1[e - 4]) * qscale;
+        const _Float16 h = (_Float16)x;
+        const _Float16 part_x = hi_lane ? h : (lo_lane ? (_Float16)(x - (float)h) : (_Float16)0.f);
+#pragma unroll
+        for (int a = 0; a < NH; ++a) qb[a][ks][e] = a == my_head ? part_x : (_Float16)0.f;
       }
     }
   }
-
   // q8_0 K enters the score product as 1152 + k: 1152 times the column's
   // sum of each k step of Q' comes off afterwards.
   float qbias[KS];
@@ -1464,26 +1477,31 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     for (int ks = 0; ks < KS; ++ks) {
       float t = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) t += (float)qb[ks][e];
+      for (int a = 0; a < NH; ++a)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += (float)qb[a][ks][e];
       t += __shfl_xor(t, 16);
       t += __shfl_xor(t, 32);
       qbias[ks] = 1152.f * t;
     }
   }
-  const bool lo_lane = lr >= 16 - G;
 
-  // Rows are loaded in order, 16 lanes a row: lane (lr, lq) takes bytes
-  // [CB lr, CB lr + CB) of rows 4 lq + i.
+  // Loads: lane l takes 16-byte piece l % LPR of rows RPI i + l / LPR of the
+  // wave's row segment (NH adjacent heads); piece p is head p / HP, bytes
+  // 16 (p % HP) of its row.
+  const int piece = lane % LPR, prow = lane / LPR;
+  const int ph = piece / HP, pc = piece % HP;
   const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
-  uint32_t roff[4];
+  uint32_t roff[NLD];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) roff[i] = (uint32_t)(4 * lq + i) * row_bytes + (uint32_t)(lr * CB);
-  // q8_0 scales: a kv head's groups of a block are the run [HD / 32][16
-  // slots]; a lane reads slots 4 lq .. 4 lq + 3 of every group.
+  for (int i = 0; i < NLD; ++i) roff[i] = (uint32_t)(RPI * i + prow) * row_bytes + (uint32_t)(piece * 16);
+  // q8_0 scales: the wave's heads' groups of a block are one run [NH KS
+  // groups][16 slots]; lane l loads entry l % NSC (or entries 2l, 2l + 1).
   const int64_t sgroups = slot_stride >> 5;
-  const int64_t shead = ((int64_t)kvh * head_stride >> 5) * 32;
-  const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh * head_stride);
-  const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh * head_stride);
+  const int64_t shead = ((int64_t)kvh0 * head_stride >> 5) * 32;
+  const int sidx = NSC <= 64 ? lane % NSC : 2 * lane;
+  const char *kbase = reinterpret_cast<const char *>(kpool + (int64_t)kvh0 * head_stride);
+  const char *vbase = reinterpret_cast<const char *>(vpool + (int64_t)kvh0 * head_stride);
   const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
 
   float m_ref = -INFINITY, l_run = 0.f;  // softmax reference and sum of this lane's column
@@ -1493,13 +1511,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   const int32_t *tab = tables + qi * table_stride;
 
-  // q8_0: the tile's K and V scales of this kv head are [KS groups][16 slots]
-  // runs; lane l loads entry l % (16 KS) of each (one register a stage) and
-  // the tile's scales reach their lanes through LDS.
-  const int sidx = lane % (KS * 16);
   struct Stage {
-    CV k[4], v[4];
-    uint32_t ks, vs;  // q8_0: scale entry sidx of K and of V
+    u32x4 k[NLD], v[NLD];
+    SV ks, vs;  // q8_0: scale entries sidx (.. sidx + 1) of K and of V
   };
 
   // Loads go through buffer descriptors whose extent ends at the last row
@@ -1511,66 +1525,80 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
     const int valid = b < b1 ? (int)(tok1 - (int64_t)b * 16) : 0;
     const int rows = valid < 16 ? valid : 16;
-    const int extent = rows > 0 ? (rows - 1) * (int)row_bytes + RB : 0;
+    const int extent = rows > 0 ? (rows - 1) * (int)row_bytes + NH * RB : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(kbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(vbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      st.k[i] = BufVec<CB>::template load<kNt>(rk, roff[i]);
-      st.v[i] = BufVec<CB>::template load<kNt>(rv, roff[i]);
+    for (int i = 0; i < NLD; ++i) {
+      st.k[i] = BufVec<16>::template load<kNt>(rk, roff[i]);
+      st.v[i] = BufVec<16>::template load<kNt>(rv, roff[i]);
     }
     if constexpr (Q8) {
-      const int sext = rows > 0 ? KS * 32 : 0;
+      const int sext = rows > 0 ? NSC * 2 : 0;
       const int64_t sblk = (int64_t)blk * sgroups * 32 + shead;
       const __amdgpu_buffer_rsrc_t skr = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(kscale) + sblk), (short)0, sext, kBufferWord3);
       const __amdgpu_buffer_rsrc_t svr = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(reinterpret_cast<const char *>(vscale) + sblk), (short)0, sext, kBufferWord3);
-      st.ks = __builtin_amdgcn_raw_buffer_load_b16(skr, (uint32_t)(sidx * 2), 0, 0);
-      st.vs = __builtin_amdgcn_raw_buffer_load_b16(svr, (uint32_t)(sidx * 2), 0, 0);
-      if ((sidx & 15) >= rows) st.ks = st.vs = 0;  // slots past the context may hold any scale (inf: d * 0 = NaN)
+      if constexpr (NSC <= 64) {
+        st.ks = __builtin_amdgcn_raw_buffer_load_b16(skr, (uint32_t)(sidx * 2), 0, 0);
+        st.vs = __builtin_amdgcn_raw_buffer_load_b16(svr, (uint32_t)(sidx * 2), 0, 0);
+        if ((sidx & 15) >= rows) st.ks = st.vs = 0;  // slots past the context may hold any scale
+      } else {
+        st.ks = __builtin_amdgcn_raw_buffer_load_b32(skr, (uint32_t)(sidx * 2), 0, 0);
+        st.vs = __builtin_amdgcn_raw_buffer_load_b32(svr, (uint32_t)(sidx * 2), 0, 0);
+        // entries sidx and sidx + 1 are slots (sidx & 15) and (sidx & 15) + 1 of one group
+        const uint32_t keep = ((sidx & 15) >= rows ? 0u : 0xffffu) | ((sidx & 15) + 1 >= rows ? 0u : 0xffff0000u);
+        st.ks &= keep;
+        st.vs &= keep;
+      }
     }
   };
 
   auto compute_tile = [&](int b, const Stage &st) {
-    // Stage K (as loaded) and V (as f16) in LDS, row order.
+    // Stage K (as loaded) and V (as f16) in LDS, row order, one region per head.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<CV *>(sk + (4 * lq + i) * KPITCH + lr * CB) = st.k[i];
+    for (int i = 0; i < NLD; ++i) {
+      const int r = RPI * i + prow;
+      *reinterpret_cast<u32x4 *>(sk[ph] + r * KPITCH + pc * 16) = st.k[i];
       if constexpr (Q8) {
-        if constexpr (E == 8)
-          *reinterpret_cast<h8 *>(sv + (4 * lq + i) * VPITCH + lr * 16) = i8x8_to_h8(st.v[i]);
-        else
-          *reinterpret_cast<h4 *>(sv + (4 * lq + i) * VPITCH + lr * 8) = i8x4_to_h4(st.v[i]);
+        *reinterpret_cast<h8 *>(sv[ph] + r * VPITCH + pc * 32) = i8x8_to_h8(u32x2{st.v[i].x, st.v[i].y});
+        *reinterpret_cast<h8 *>(sv[ph] + r * VPITCH + pc * 32 + 16) = i8x8_to_h8(u32x2{st.v[i].z, st.v[i].w});
       } else {
-        *reinterpret_cast<CV *>(sv + (4 * lq + i) * VPITCH + lr * CB) = st.v[i];
+        *reinterpret_cast<u32x4 *>(sv[ph] + r * VPITCH + pc * 16) = st.v[i];
       }
     }
     if constexpr (Q8) {
-      ssc[0][sidx] = (uint16_t)st.ks;
-      ssc[1][sidx] = (uint16_t)st.vs;
+      if constexpr (NSC <= 64) {
+        ssc[0][sidx] = (uint16_t)st.ks;
+        ssc[1][sidx] = (uint16_t)st.vs;
+      } else {
+        *reinterpret_cast<uint32_t *>(&ssc[0][sidx]) = st.ks;
+        *reinterpret_cast<uint32_t *>(&ssc[1][sidx]) = st.vs;
+      }
     }
-    KV ka[KS];
+    KV ka[NH][KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      ka[ks] = *reinterpret_cast<const KV *>(sk + lr * KPITCH + (32 * ks + 8 * lq) * (int)sizeof(T));
-
-    // Scores of tokens 4 lq + i, column lr.
-    f32x4 s;
-    if constexpr (Q8) {
-      f32x4 c[KS];
+    for (int a = 0; a < NH; ++a)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        c[ks] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8_biased(ka[ks]), qb[ks],
-                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        ka[a][ks] = *reinterpret_cast<const KV *>(sk[a] + lr * KPITCH + (32 * ks + 8 * lq) * (int)sizeof(T));
+
+    // Scores of tokens 4 lq + i, column lr: every kv head's product lands in
+    // the columns of its own query heads.
+    f32x4 s;
+    if constexpr (Q8) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const h4 d = *reinterpret_cast<const h4 *>(&ssc[0][ks * 16 + 4 * lq]);
+        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int a = 0; a < NH; ++a) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8_biased(ka[a][ks]), qb[a][ks], c, 0, 0, 0);
+        const h4 d = *reinterpret_cast<const h4 *>(&ssc[0][(my_head * KS + ks) * 16 + 4 * lq]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float t = c[ks][i] - qbias[ks];
+          const float t = c[i] - qbias[ks];
           s[i] = ks == 0 ? (float)d[i] * t : __builtin_fmaf((float)d[i], t, s[i]);
         }
       }
@@ -1578,7 +1606,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, ka[ks]), qb[ks], s, 0, 0, 0);
+#pragma unroll
+        for (int a = 0; a < NH; ++a)
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, ka[a][ks]), qb[a][ks], s, 0, 0, 0);
     }
     float sc[4];
 #pragma unroll
@@ -1610,8 +1640,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
-    // O^T += V^T P'^T, per 16-row tile of d; q8_0: P' carries the V scale of
-    // the tile's 32-element group.
+    // O^T += V_a^T P'_a^T for each kv head a of the wave, per 16-row tile
+    // of d; P'_a holds the weights of a's query heads (zero elsewhere) and,
+    // for q8_0, the V scale of the tile's 32-element group.
     h4 pf = {};
     if constexpr (!Q8) {
 #pragma unroll
@@ -1619,38 +1650,56 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
 #pragma unroll
     for (int g = 0; g < KS; ++g) {
-      h4 pb = pf;
+      h4 pw = pf;
       if constexpr (Q8) {
-        const h4 d = *reinterpret_cast<const h4 *>(&ssc[1][g * 16 + 4 * lq]);
+        const h4 d = *reinterpret_cast<const h4 *>(&ssc[1][(my_head * KS + g) * 16 + 4 * lq]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = weight_part(p[i] * (float)d[i], lo_lane);
+        for (int i = 0; i < 4; ++i) pw[i] = weight_part(p[i] * (float)d[i], lo_lane);
       }
+      h4 pb[NH];
 #pragma unroll
-      for (int dt = 2 * g; dt < 2 * g + 2; ++dt) {
-        const hf4 a = lds_read_tr(sv + (4 * lq + (lr >> 2)) * VPITCH + (dt * 16 + 4 * (lr & 3)) * 2);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), pb, o[dt], 0, 0, 0);
-      }
+      for (int a = 0; a < NH; ++a) pb[a] = (NH == 1 || a == my_head) ? pw : h4{};
+#pragma unroll
+      for (int dt = 2 * g; dt < 2 * g + 2; ++dt)
+#pragma unroll
+        for (int a = 0; a < NH; ++a) {
+          const hf4 v = lds_read_tr(sv[a] + (4 * lq + (lr >> 2)) * VPITCH + (dt * 16 + 4 * (lr & 3)) * 2);
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, v), pb[a], o[dt], 0, 0, 0);
+        }
     }
   };
 
-  // Software pipeline: two tiles in flight while one is computed. Loads
-  // past the last tile read nothing (extent 0).
+  // Software pipeline: STAGES - 1 tiles in flight while one is computed.
+  // Loads past the last tile read nothing (extent 0).
   {
     int b = b0;
     if (b < b1) {
-      Stage s0, s1, s2;
-      load_tile(b, s0);
-      load_tile(b + 1, s1);
-      for (;;) {
-        load_tile(b + 2, s2);
-        compute_tile(b, s0);
-        if (++b >= b1) break;
-        load_tile(b + 2, s0);
-        compute_tile(b, s1);
-        if (++b >= b1) break;
-        load_tile(b + 2, s1);
-        compute_tile(b, s2);
-        if (++b >= b1) break;
+      if constexpr (STAGES == 3) {
+        Stage s0, s1, s2;
+        load_tile(b, s0);
+        load_tile(b + 1, s1);
+        for (;;) {
+          load_tile(b + 2, s2);
+          compute_tile(b, s0);
+          if (++b >= b1) break;
+          load_tile(b + 2, s0);
+          compute_tile(b, s1);
+          if (++b >= b1) break;
+          load_tile(b + 2, s1);
+          compute_tile(b, s2);
+          if (++b >= b1) break;
+        }
+      } else {
+        Stage s0, s1;
+        load_tile(b, s0);
+        for (;;) {
+          load_tile(b + 1, s1);
+          compute_tile(b, s0);
+          if (++b >= b1) break;
+          load_tile(b + 1, s0);
+          compute_tile(b, s1);
+          if (++b >= b1) break;
+        }
       }
     }
   }
@@ -1663,8 +1712,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[dt][i] += dpp<0x140>(o[dt][i]);
 
-  if (lr < G) {  // lane (h, lq) holds rows d = 16 dt + 4 lq + i of head h
-    const int64_t qh = qi * n_heads + (int64_t)kvh * G + lr;
+  if (hi_lane) {  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
+    const int64_t qh = qi * n_heads + (int64_t)kvh0 * G + lr;
     const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
     if (direct) {
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -1684,11 +1733,11 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   }
 }
 
-// One wave per work-group: each wave streams a whole partition.
-template <typename T, int HD, int G>
+// One wave per work-group: each wave streams a whole partition of NH kv heads.
+template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  const unsigned grid = (unsigned)(a.n * a.n_kv_heads * a.max_parts);
-  attn_mfma_kernel<T, HD, G><<<grid, 64, 0, s>>>(
+  const unsigned grid = (unsigned)(a.n * (a.n_kv_heads / NH) * a.max_parts);
+  attn_mfma_kernel<T, HD, G, NH><<<grid, 64, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts, a.pre_parts, a.qmap,
@@ -1726,8 +1775,12 @@ constexpr bool kRow16 = HD / Tile<T>::E == 16;
 
 template <typename T, int HD, int G>
 hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  if constexpr (!std::is_same_v<T, float>)
-    return launch_attn_mfma_t<T, HD, G>(g, a, s);
+  if constexpr (!std::is_same_v<T, float>) {
+    if constexpr (G <= 4) {
+      if (a.split == 2) return launch_attn_mfma_t<T, HD, G, 2>(g, a, s);
+    }
+    return launch_attn_mfma_t<T, HD, G, 1>(g, a, s);
+  }
   else if constexpr (kRow16<T, HD>)
     return launch_attn16_t<T, HD, G>(g, a, s);
   else
@@ -2193,6 +2246,10 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
     if (a.head_dim == 128) return launch_attn_hd<float, 128>(g, a, s);
   }
   return hipErrorInvalidValue;
+}
+
+int attention_split(int elem, int group, int n_kv_heads) {
+  return (elem == 1 || elem == 2) && group <= 4 && n_kv_heads % 2 == 0 ? 2 : 1;
 }
 
 int mq_rows(int) { return 32 * kMqWaves; }

@@ -272,6 +272,16 @@ def test_attention_shapes(gpu, dtype, head_dim, group):
     attention_close(out, want, dtype)
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("group,n_kv", [(2, 2), (3, 4), (2, 3), (4, 5), (1, 1)])
+def test_attention_head_pairs_f16(gpu, head_dim, group, n_kv):
+    """f16 waves read two adjacent kv heads when the group has at most 4
+    query heads and the kv heads pair up (even count), one otherwise."""
+    lens = [1, 16, 33, 300, 1031, 2100]
+    out, want = _attention_case(gpu, "f16", head_dim, group, n_kv, lens, 0, seed=group * 7 + n_kv)
+    attention_close(out, want, "f16")
+
+
 @pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
 def test_attention_partitions(gpu, partition):
     lens = [5, 64, 65, 257, 700, 2049]
