@@ -72,9 +72,9 @@ struct AttnArgs {
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int part_tokens, max_parts;  // part_tokens 0: per-query partition_tokens(len)
-  // Kernels that read `split` adjacent kv heads per wave cut each partition
-  // into `split` (partition_tokens(len) / split tokens each); max_parts counts
-  // the finer partitions. attention_split gives it for a shape.
+  // The matrix-core decode kernel cuts each partition into `split`
+  // (partition_tokens(len) / split tokens each, split 1 or 2); max_parts
+  // counts the finer partitions. attention_split gives it for a shape.
   int split;
   // Group partials folded into each query's result (planned attention), or
   // pre_parts == nullptr: query i has pre_parts[i] partials at pre_o/pre_ml
@@ -115,10 +115,11 @@ struct AttnWorkspace {
 AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts,
                                   bool always = false);
 bool attention_supported(int elem, int head_dim, int group);
-// Kv heads one decode wave reads (1 or 2): 2 for f16 and q8_0 pools with
-// groups of at most 4 query heads and an even number of kv heads (the
-// wave's 2 x group query heads fill the 16 columns of its products).
-int attention_split(int elem, int group, int n_kv_heads);
+// Decode kernels on f16 and q8_0 pools read two adjacent kv heads per wave
+// when the group has at most 4 query heads and the kv heads pair up (the
+// wave's 2 x group query heads fill the 16 columns of its products). The
+// partition divisor (1 or 2) for n queries of such a shape: 1 otherwise.
+int attention_split(int elem, int group, int n_kv_heads, int64_t n);
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
 
 // One work-group of shared-prefix attention (mq_attn_kernel): the query rows

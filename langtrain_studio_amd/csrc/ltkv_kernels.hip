@@ -1396,7 +1396,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
                  float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
                  int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
-                 int max_parts, const int32_t *__restrict__ pre_parts,
+                 int split, int max_parts, const int32_t *__restrict__ pre_parts,
                  const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
                  const uint16_t *__restrict__ vscale) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
@@ -1412,7 +1412,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   constexpr int VPITCH = HD * 2 + 16;      // LDS bytes per staged V row (f16)
   constexpr int NQ = NH * G;               // query heads of the wave
   constexpr int NSC = NH * KS * 16;        // q8_0 scale entries of a tile, K or V
-  constexpr int STAGES = NH == 1 ? 3 : 2;  // tiles in flight + 1
+  constexpr int STAGES = NH == 2 && Q8 ? 2 : 3;  // tiles in flight + 1
   using KV = typename BufVec<KB>::type;
   using SV = uint32_t;  // one or two b16 scale entries
   static_assert(NQ <= 8, "hi and lo columns of the wave's query heads must fit 16");
@@ -1438,7 +1438,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // A query with group partials and nothing else to read (or whose group
   // wrote its output) has no work here.
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
-  const int pt = partition_tokens(len, part_tokens) / NH;  // NH heads a wave: partitions NH x finer
+  const int pt = partition_tokens(len, part_tokens) / split;
   const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   if (part >= np) return;
   const int64_t tok0 = (int64_t)part * pt;
@@ -1740,7 +1740,7 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
   attn_mfma_kernel<T, HD, G, NH><<<grid, 64, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
-      g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts, a.pre_parts, a.qmap,
+      g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
   return launch_merge<HD>(a, s);
 }
@@ -1777,7 +1777,7 @@ template <typename T, int HD, int G>
 hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   if constexpr (!std::is_same_v<T, float>) {
     if constexpr (G <= 4) {
-      if (a.split == 2) return launch_attn_mfma_t<T, HD, G, 2>(g, a, s);
+      if (a.n_kv_heads % 2 == 0) return launch_attn_mfma_t<T, HD, G, 2>(g, a, s);
     }
     return launch_attn_mfma_t<T, HD, G, 1>(g, a, s);
   }
@@ -2248,8 +2248,15 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
   return hipErrorInvalidValue;
 }
 
-int attention_split(int elem, int group, int n_kv_heads) {
-  return (elem == 1 || elem == 2) && group <= 4 && n_kv_heads % 2 == 0 ? 2 : 1;
+int attention_split(int elem, int group, int n_kv_heads, int64_t n) {
+  if (!((elem == 1 || elem == 2) && group <= 4 && n_kv_heads % 2 == 0)) return 1;
+  // Measured at the Llama-3-8B decode shape (64 queries): q8_0 waves of two
+  // heads (256 B rows of K and of V) run fastest with each partition cut in
+  // two; f16 waves of two heads (512 B rows, three tiles in flight) keep HBM
+  // busy at one wave per SIMD and run fastest uncut, so they are cut only
+  // when four partitions per query would leave SIMDs idle.
+  if (elem == 1) return 2;
+  return n * (n_kv_heads / 2) * 4 < 1024 ? 2 : 1;
 }
 
 int mq_rows(int) { return 32 * kMqWaves; }

@@ -282,6 +282,17 @@ def test_attention_head_pairs_f16(gpu, head_dim, group, n_kv):
     attention_close(out, want, "f16")
 
 
+@pytest.mark.parametrize("partition", [0, 64, 128])
+def test_attention_head_pairs_large_batch(gpu, partition):
+    """64 queries of the Llama-3-8B shape: f16 waves of two kv heads run with
+    uncut partitions (one wave per SIMD fills the chip); smaller batches cut
+    each partition in two. Both cuts must give the oracle's result."""
+    rng = np.random.default_rng(partition + 5)
+    lens = [int(x) for x in rng.integers(1, 400, size=64)]
+    out, want = _attention_case(gpu, "f16", 128, 4, 8, lens, partition, seed=partition + 6)
+    attention_close(out, want, "f16")
+
+
 @pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
 def test_attention_partitions(gpu, partition):
     lens = [5, 64, 65, 257, 700, 2049]
