@@ -1334,41 +1334,7 @@ __device__ __forceinline__ h8 i8x8_to_h8(const u32x2 &w) {
   return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-template <typename T, int E, typename V>
-__device__ __forceinline__ void unpack_row(const V &v, float (&f)[E]) {
-  if constexpr (std::is_same_v<T, _Float16>) {
-    typedef _Float16 hv __attribute__((ext_vector_type(E)));
-    const hv x = __builtin_bit_cast(hv, v);
-#pragma unroll
-    for (int i = 0; i < E; ++i) f[i] = (float)x[i];
-  } else {
-    typedef int8_t bv __attribute__((ext_vector_type(E)));
-    const bv x = __builtin_bit_cast(bv, v);
-#pragma unroll
-    for (int i = 0; i < E; ++i) f[i] = (float)x[i];
-  }
-}
-
 constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
-
-// int8 x 4 -> f16 x 4, exact (as i8x8_to_h8).
-__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
-  constexpr uint32_t kHi = 0x64646464u;
-  const uint32_t a = w ^ 0x80808080u;
-  const h2 bias = {(_Float16)1152.f, (_Float16)1152.f};
-  const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04010400u)) - bias;
-  const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04030402u)) - bias;
-  return h4{p0.x, p0.y, p1.x, p1.y};
-}
-
-// f32 -> the f16 part this lane's column holds: hi (column < G), lo (column
-// >= 16 - G), zero otherwise.
-template <int G>
-__device__ __forceinline__ _Float16 column_part(float x, int col) {
-  const _Float16 h = (_Float16)x;
-  const _Float16 l = (_Float16)(x - (float)h);
-  return col < G ? h : (col >= 16 - G ? l : (_Float16)0.f);
-}
 
 // The weight operand's part for this lane: the lo part on lo lanes, else
 // the hi part (columns past the group are discarded, any finite value does).
