@@ -236,7 +236,61 @@ LTKV_API int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, co
  * work-groups, [5] table width in blocks. */
 LTKV_API int ltkv_plan_stats(const ltkv_cache *c, uint64_t out[6]);
 
+/* ---- resident block tables: the device step descriptor ----------------- */
+/* The cache keeps every live sequence's block table in HBM as one row of a
+ * [rows][stride] int32 array, plus each row's length in blocks, and uploads
+ * only what changed since the last upload: the entries that append (a new
+ * block, a copy-on-write replacement), truncate and share touched (the
+ * engine's BatchToken / kv_remove / kv_copy traffic, native/src/lib.rs:163-198,
+ * scheduler.rs:356-413). No reference counterpart exists: the reference
+ * reads its tables in host memory (kv.rs:133-150); here they replace the
+ * per-step upload of every query's full table. */
+
+/* Row of each sequence in the resident tables, or -1 for a sequence holding
+ * no blocks. A row is assigned when a sequence gets its first block and is
+ * reused after the sequence is removed (truncate to 0). Host only; valid for
+ * the device after the next upload (which the device ops below enqueue
+ * themselves). */
+LTKV_API int ltkv_seq_rows(const ltkv_cache *c, size_t n, const uint32_t *seqs, int32_t *rows_out);
+
+/* Enqueues the upload of the table changes made since the last upload, on
+ * the cache stream (one small copy of (row, column, block) triples and one
+ * kernel). Growing the tables reallocates them and uploads every live row
+ * once (the stream is synchronised first). */
+LTKV_API int ltkv_sync_tables(ltkv_cache *c);
+
+/* Uploads pending changes, then returns the resident tables: d_tables
+ * [n_rows][stride] block ids and d_lengths [n_rows] table lengths in
+ * blocks (0 for a free row). Valid until a later call grows them. */
+LTKV_API int ltkv_resident_tables(ltkv_cache *c, const int32_t **d_tables, const int32_t **d_lengths,
+                                  size_t *stride, size_t *n_rows);
+
+/* Slot mapping of n tokens from the resident tables, on the device: token i
+ * at position d_pos[i] of the sequence in row d_rows[i] gets cell
+ * block * 16 + pos % 16 (block = its table entry pos / 16, as append
+ * returned it, kv.rs:95-121), or -1 when the row is not a live sequence or
+ * pos / 16 is past its table. Claim the cells first (ltkv_append_batch);
+ * the result feeds ltkv_write / ltkv_write_rope. */
+LTKV_API int ltkv_slot_mapping(ltkv_cache *c, size_t n, const int32_t *d_rows, const int64_t *d_pos,
+                               int32_t *d_slot_mapping);
+
+/* ltkv_decode_attention over the resident tables: query i reads positions
+ * [0, d_lens[i]) of the sequence in row d_rows[i] (device arrays). A row of
+ * -1 must come with length 0 (zeros). Same results, bit for bit, as
+ * ltkv_decode_attention with that sequence's table. */
+LTKV_API int ltkv_decode_attention_rows(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                                        size_t head_dim, float scale, const float *d_q,
+                                        const int32_t *d_rows, const int32_t *d_lens, float *d_out);
+
+/* Table entries uploaded so far (each (row, column, block) or length update
+ * counts one). */
+LTKV_API int ltkv_table_uploads(const ltkv_cache *c, uint64_t *entries);
+
 /* ---- host conveniences (synchronous on the stream) --------------------- */
+
+/* Copy the resident tables ([rows][stride] and [rows], the sizes
+ * ltkv_resident_tables reports) to host, after pending uploads. */
+LTKV_API int ltkv_read_resident_tables(ltkv_cache *c, int32_t *h_tables, int32_t *h_lengths);
 
 /* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */
 LTKV_API int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v);

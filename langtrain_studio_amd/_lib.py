@@ -56,6 +56,13 @@ SIGNATURES = {
     "ltkv_rows": (_int, [_vp, _sz, _u32, _sz, _vp, _vp]),
     "ltkv_write_row": (_int, [_vp, _sz, _u32, _u32, _vp, _vp]),
     "ltkv_synchronize": (_int, [_vp]),
+    "ltkv_seq_rows": (_int, [_vp, _sz, _vp, _vp]),
+    "ltkv_sync_tables": (_int, [_vp]),
+    "ltkv_resident_tables": (_int, [_vp, _P(_vp), _P(_vp), _P(_sz), _P(_sz)]),
+    "ltkv_slot_mapping": (_int, [_vp, _sz, _vp, _vp, _vp]),
+    "ltkv_decode_attention_rows": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _vp, _vp]),
+    "ltkv_table_uploads": (_int, [_vp, _P(_u64)]),
+    "ltkv_read_resident_tables": (_int, [_vp, _vp, _vp]),
 }
 
 _lib = None

@@ -133,6 +133,25 @@ struct ltkv_cache {
 
   int device_count_cu = 256;
 
+  // Resident block tables (the device step descriptor): one row per live
+  // sequence, [rt_rows][rt_width] block ids plus [rt_rows] table lengths, kept
+  // equal to `seqs` by uploading only the entries that changed (sync_tables).
+  int32_t *d_rt = nullptr, *d_rt_nb = nullptr;
+  size_t rt_rows = 0, rt_width = 0;             // device capacity
+  std::unordered_map<uint32_t, int32_t> rt_row;  // live sequence -> row
+  std::vector<uint32_t> rt_seq;                  // row -> sequence
+  std::vector<char> rt_live;                     // row holds a live sequence
+  std::vector<int32_t> rt_free;                  // released rows, reused last-in first-out
+  std::vector<uint32_t> rt_lo, rt_hi;            // per row: changed entries [lo, hi)
+  std::vector<char> rt_dirty;                    // per row: changed since the last sync
+  std::vector<int32_t> rt_dirty_rows;
+  std::vector<int32_t> rt_upd;                   // (row, col, value) triples being built
+  int32_t *h_rt_upd = nullptr, *d_rt_upd = nullptr;  // pinned staging -> device
+  size_t rt_upd_cap = 0;                         // triples
+  hipEvent_t rt_done = nullptr;
+  bool rt_in_flight = false;
+  uint64_t rt_uploaded = 0;                      // triples uploaded so far (statistics)
+
   size_t layer_elems() const { return n_blocks * LTKV_BLOCK * kv_dim; }
   uint8_t *k_layer(size_t l) const { return (uint8_t *)k + l * layer_elems() * elem; }
   uint8_t *v_layer(size_t l) const { return (uint8_t *)v + l * layer_elems() * elem; }
@@ -153,6 +172,54 @@ struct ltkv_cache {
     if (refs[b] == 0) free.push_back(b);
   }
 
+  // Row of a live sequence in the resident tables, assigned on first use.
+  int32_t rt_row_of(uint32_t seq) {
+    auto it = rt_row.find(seq);
+    if (it != rt_row.end()) return it->second;
+    int32_t r;
+    if (!rt_free.empty()) {
+      r = rt_free.back();
+      rt_free.pop_back();
+    } else {
+      r = (int32_t)rt_seq.size();
+      rt_seq.push_back(0);
+      rt_live.push_back(0);
+      rt_lo.push_back(0);
+      rt_hi.push_back(0);
+      rt_dirty.push_back(0);
+    }
+    rt_row.emplace(seq, r);
+    rt_seq[r] = seq;
+    rt_live[r] = 1;
+    return r;
+  }
+  void rt_touch(int32_t r, size_t lo, size_t hi) {  // entries [lo, hi) and the length changed
+    if (!rt_dirty[r]) {
+      rt_dirty[r] = 1;
+      rt_dirty_rows.push_back(r);
+      rt_lo[r] = (uint32_t)lo;
+      rt_hi[r] = (uint32_t)hi;
+    } else if (lo < hi) {
+      if (rt_lo[r] >= rt_hi[r]) {
+        rt_lo[r] = (uint32_t)lo;
+        rt_hi[r] = (uint32_t)hi;
+      } else {
+        rt_lo[r] = std::min<uint32_t>(rt_lo[r], (uint32_t)lo);
+        rt_hi[r] = std::max<uint32_t>(rt_hi[r], (uint32_t)hi);
+      }
+    }
+  }
+  void rt_mark(uint32_t seq, size_t lo, size_t hi) { rt_touch(rt_row_of(seq), lo, hi); }
+  void rt_remove(uint32_t seq) {  // the sequence is gone: its row reads as empty
+    auto it = rt_row.find(seq);
+    if (it == rt_row.end()) return;
+    const int32_t r = it->second;
+    rt_row.erase(it);
+    rt_live[r] = 0;
+    rt_touch(r, 0, 0);
+    rt_free.push_back(r);
+  }
+
   // kv.rs:85-121 without the device copy: a copy-on-write is recorded in
   // `pending` and launched by the caller before any later device work.
   int append_meta(uint32_t seq, size_t pos, uint32_t *block, uint32_t *slot) {
@@ -166,6 +233,7 @@ struct ltkv_cache {
       int32_t b;
       if (!alloc(&b)) return fail(LTKV_ERR_FULL, "KV cache full");
       s.blocks.push_back(b);
+      rt_mark(seq, s.blocks.size() - 1, s.blocks.size());
     } else {
       const int32_t last = s.blocks.back();
       if (refs[last] > 1) {  // the sequence diverges from a shared prefix
@@ -175,6 +243,7 @@ struct ltkv_cache {
         pending.push_back(nb);
         release(last);
         s.blocks.back() = nb;
+        rt_mark(seq, s.blocks.size() - 1, s.blocks.size());
         ++cow_copies;
       }
     }
@@ -235,7 +304,12 @@ struct ltkv_cache {
     for (size_t i = keep; i < s.blocks.size(); ++i) release(s.blocks[i]);
     s.blocks.resize(keep);
     s.len = from;
-    if (from == 0) seqs.erase(it);
+    if (from == 0) {
+      seqs.erase(it);
+      rt_remove(seq);
+    } else {
+      rt_mark(seq, 0, 0);  // the table length changed
+    }
   }
 
   void share(uint32_t src, uint32_t dst, size_t len) {  // kv.rs:172-183
@@ -247,7 +321,10 @@ struct ltkv_cache {
     const size_t nb = (len + LTKV_BLOCK - 1) / LTKV_BLOCK;
     std::vector<int32_t> blocks(it->second.blocks.begin(), it->second.blocks.begin() + nb);
     for (int32_t b : blocks) refs[b] += 1;
-    if (len > 0) seqs[dst] = Seq{std::move(blocks), len};
+    if (len > 0) {
+      seqs[dst] = Seq{std::move(blocks), len};
+      rt_mark(dst, 0, nb);
+    }
   }
 };
 
@@ -279,6 +356,94 @@ int ensure_workspace(ltkv_cache *c, size_t bytes) {
   HIP_TRY(hipMalloc((void **)&c->ws, bytes), "hipMalloc(workspace)");
   c->ws_bytes = bytes;
   return LTKV_OK;
+}
+
+// Uploads the resident-table changes made since the last call: only the
+// changed entries of changed rows, as (row, col, value) triples through
+// pinned staging, applied by one small kernel on the cache stream. Growing
+// the tables (more rows, or a table longer than the width) reallocates them
+// and uploads every live row once. Device of the cache current.
+int sync_tables(ltkv_cache *c) {
+  const size_t need_rows = c->rt_seq.size();
+  size_t need_w = c->rt_width;
+  for (int32_t r : c->rt_dirty_rows)
+    if (c->rt_live[r]) need_w = std::max(need_w, c->seqs.at(c->rt_seq[r]).blocks.size());
+  const bool grow = !c->d_rt || need_rows > c->rt_rows || need_w > c->rt_width;
+  if (!grow && c->rt_dirty_rows.empty()) return LTKV_OK;
+  std::vector<int32_t> &u = c->rt_upd;
+  u.clear();
+  auto row_updates = [&](int32_t r, size_t lo, size_t hi) {
+    if (!c->rt_live[r]) {  // released: an empty table
+      u.insert(u.end(), {r, -1, 0});
+      return;
+    }
+    const std::vector<int32_t> &blocks = c->seqs.at(c->rt_seq[r]).blocks;
+    hi = std::min(hi, blocks.size());
+    for (size_t j = lo; j < hi; ++j) u.insert(u.end(), {r, (int32_t)j, blocks[j]});
+    u.insert(u.end(), {r, -1, (int32_t)blocks.size()});
+  };
+  if (grow) {
+    const size_t rows = std::max<size_t>({need_rows, 2 * c->rt_rows, 64});
+    const size_t width = std::max<size_t>({need_w, 2 * c->rt_width, 64});
+    if ((uint64_t)rows * width > (uint64_t)INT32_MAX)
+      return fail(LTKV_ERR_ARG, "resident block tables too large (%zu rows x %zu blocks)", rows, width);
+    // The old tables may still be read by enqueued work.
+    HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+    if (c->d_rt) (void)hipFree(c->d_rt);
+    if (c->d_rt_nb) (void)hipFree(c->d_rt_nb);
+    c->d_rt = c->d_rt_nb = nullptr;
+    c->rt_rows = c->rt_width = 0;
+    HIP_TRY(hipMalloc((void **)&c->d_rt, rows * width * sizeof(int32_t)), "hipMalloc(resident tables)");
+    HIP_TRY(hipMalloc((void **)&c->d_rt_nb, rows * sizeof(int32_t)), "hipMalloc(resident table lengths)");
+    c->rt_rows = rows;
+    c->rt_width = width;
+    for (size_t r = 0; r < rows; ++r) {
+      if (r < need_rows) row_updates((int32_t)r, 0, SIZE_MAX);
+      else u.insert(u.end(), {(int32_t)r, -1, 0});
+    }
+  } else {
+    for (int32_t r : c->rt_dirty_rows) row_updates(r, c->rt_lo[r], c->rt_hi[r]);
+  }
+  for (int32_t r : c->rt_dirty_rows) c->rt_dirty[r] = 0;
+  c->rt_dirty_rows.clear();
+
+  const size_t n = u.size() / 3;
+  if (c->rt_in_flight) {  // the staging buffer may still be read by the last upload
+    HIP_TRY(hipEventSynchronize(c->rt_done), "hipEventSynchronize");
+    c->rt_in_flight = false;
+  }
+  if (n > c->rt_upd_cap) {
+    const size_t cap = std::max<size_t>({n, 2 * c->rt_upd_cap, 1024});
+    if (c->h_rt_upd) (void)hipHostFree(c->h_rt_upd);
+    if (c->d_rt_upd) {
+      HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+      (void)hipFree(c->d_rt_upd);
+    }
+    c->h_rt_upd = c->d_rt_upd = nullptr;
+    c->rt_upd_cap = 0;
+    HIP_TRY(hipHostMalloc((void **)&c->h_rt_upd, cap * 3 * sizeof(int32_t), hipHostMallocDefault),
+            "hipHostMalloc(table updates)");
+    HIP_TRY(hipMalloc((void **)&c->d_rt_upd, cap * 3 * sizeof(int32_t)), "hipMalloc(table updates)");
+    c->rt_upd_cap = cap;
+  }
+  std::memcpy(c->h_rt_upd, u.data(), n * 3 * sizeof(int32_t));
+  HIP_TRY(hipMemcpyAsync(c->d_rt_upd, c->h_rt_upd, n * 3 * sizeof(int32_t), hipMemcpyHostToDevice,
+                         c->stream),
+          "hipMemcpyAsync(table updates)");
+  HIP_TRY(hipEventRecord(c->rt_done, c->stream), "hipEventRecord");
+  c->rt_in_flight = true;
+  HIP_TRY(ltkv::launch_table_update(c->d_rt, c->d_rt_nb, (int64_t)c->rt_width, (int64_t)c->rt_rows,
+                                    c->d_rt_upd, (int64_t)n, c->stream),
+          "table update launch");
+  c->rt_uploaded += n;
+  return LTKV_OK;
+}
+
+// Longest table (blocks) of a live sequence.
+size_t max_table_blocks(const ltkv_cache *c) {
+  size_t m = 0;
+  for (const auto &kv : c->rt_row) m = std::max(m, c->seqs.at(kv.first).blocks.size());
+  return m;
 }
 
 ltkv::PoolGeom head_geom(const ltkv_cache *c, size_t head_dim) {
@@ -713,6 +878,8 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
   }
   if (rc == LTKV_OK && (e = hipEventCreateWithFlags(&c->pairs_done, hipEventDisableTiming)) != hipSuccess)
     rc = hip_fail(e, "hipEventCreate");
+  if (rc == LTKV_OK && (e = hipEventCreateWithFlags(&c->rt_done, hipEventDisableTiming)) != hipSuccess)
+    rc = hip_fail(e, "hipEventCreate");
   if (rc != LTKV_OK) {
     ltkv_destroy(c);
     return rc;
@@ -739,6 +906,11 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->v) (void)hipFree(c->v);
     if (c->ks) (void)hipFree(c->ks);
     if (c->vs) (void)hipFree(c->vs);
+    if (c->rt_done) (void)hipEventDestroy(c->rt_done);
+    if (c->h_rt_upd) (void)hipHostFree(c->h_rt_upd);
+    if (c->d_rt_upd) (void)hipFree(c->d_rt_upd);
+    if (c->d_rt) (void)hipFree(c->d_rt);
+    if (c->d_rt_nb) (void)hipFree(c->d_rt_nb);
   }
   delete c;
 }
@@ -999,6 +1171,43 @@ int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens) {
   return LTKV_OK;
 }
 
+namespace {
+
+// Decode attention over explicit tables (rows == nullptr: query i reads row
+// i) or over the resident tables (query i reads row rows[i]); lengths are cut
+// to max_len tokens, which sizes the grid.
+int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
+                     float scale, const float *d_q, const int32_t *d_tables, size_t table_stride,
+                     const int32_t *d_rows, size_t n_rows, size_t max_len, const int32_t *d_lens,
+                     float *d_out, size_t group) {
+  // A query's partition size depends on its own length only (or is fixed by
+  // ltkv_set_attention_partition), so its result is bit-identical whatever
+  // else is in the batch (the reference's property, engine/README.md:102).
+  // max_len only bounds the grid.
+  const int part = (int)c->attn_part_tokens;  // 0: per-query policy
+  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim), (int64_t)n);
+  const size_t max_parts = (size_t)ltkv::max_partitions((int64_t)max_len, part) * split;
+  if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
+    return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
+  const ltkv::AttnWorkspace ws =
+      ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
+  if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
+  ltkv::AttnArgs a = attn_args(c, layer, n, n_heads, head_dim, scale, d_q, d_out, ws, part,
+                               (int)max_parts);
+  a.split = split;
+  a.tables = d_tables;
+  a.table_stride = (int64_t)table_stride;
+  a.rows = d_rows;
+  a.n_rows = (int64_t)n_rows;
+  a.max_len = (int64_t)max_len;
+  a.lens = d_lens;
+  HIP_TRY(ltkv::launch_decode_attention(head_geom(c, head_dim), a, c->stream),
+          "decode attention launch");
+  return LTKV_OK;
+}
+
+}  // namespace
+
 int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                           float scale, const float *d_q, const int32_t *d_tables,
                           size_t table_stride, const int32_t *d_lens, float *d_out) {
@@ -1011,31 +1220,98 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (table_stride == 0) return fail(LTKV_ERR_ARG, "table_stride must be > 0");
   if (!d_q || !d_tables || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
   if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
-
-  // A query's partition size depends on its own length only (or is fixed by
-  // ltkv_set_attention_partition), so its result is bit-identical whatever
-  // else is in the batch (the reference's property, engine/README.md:102).
-  // table_stride only bounds the grid.
-  const int part = (int)c->attn_part_tokens;  // 0: per-query policy
-  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim), (int64_t)n);
-  const size_t max_parts =
-      (size_t)ltkv::max_partitions((int64_t)(table_stride * LTKV_BLOCK), part) * split;
-  if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
-    return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
-
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  const ltkv::AttnWorkspace ws =
-      ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
-  if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
-  ltkv::AttnArgs a = attn_args(c, layer, n, n_heads, head_dim, scale, d_q, d_out, ws, part,
-                               (int)max_parts);
-  a.split = split;
-  a.tables = d_tables;
-  a.table_stride = (int64_t)table_stride;
-  a.lens = d_lens;
-  HIP_TRY(ltkv::launch_decode_attention(head_geom(c, head_dim), a, c->stream),
-          "decode attention launch");
+  return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride, nullptr,
+                          0, table_stride * LTKV_BLOCK, d_lens, d_out, group);
+}
+
+int ltkv_decode_attention_rows(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                               size_t head_dim, float scale, const float *d_q, const int32_t *d_rows,
+                               const int32_t *d_lens, float *d_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  size_t group = 0;
+  if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
+  if (n == 0) return LTKV_OK;
+  if (!d_q || !d_rows || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (int rc = sync_tables(c)) return rc;
+  // No query reads past the longest live table.
+  const size_t max_len = std::max<size_t>(max_table_blocks(c), 1) * LTKV_BLOCK;
+  return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, c->d_rt, c->rt_width, d_rows,
+                          c->rt_rows, max_len, d_lens, d_out, group);
+}
+
+int ltkv_seq_rows(const ltkv_cache *c, size_t n, const uint32_t *seqs, int32_t *rows) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (n > 0 && (!seqs || !rows)) return fail(LTKV_ERR_ARG, "null argument");
+  for (size_t i = 0; i < n; ++i) {
+    const auto it = c->rt_row.find(seqs[i]);
+    rows[i] = it == c->rt_row.end() ? -1 : it->second;
+  }
+  return LTKV_OK;
+}
+
+int ltkv_sync_tables(ltkv_cache *c) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  return sync_tables(c);
+}
+
+int ltkv_resident_tables(ltkv_cache *c, const int32_t **d_tables, const int32_t **d_lengths,
+                         size_t *stride, size_t *n_rows) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (int rc = sync_tables(c)) return rc;
+  if (d_tables) *d_tables = c->d_rt;
+  if (d_lengths) *d_lengths = c->d_rt_nb;
+  if (stride) *stride = c->rt_width;
+  if (n_rows) *n_rows = c->rt_rows;
+  return LTKV_OK;
+}
+
+int ltkv_slot_mapping(ltkv_cache *c, size_t n, const int32_t *d_rows, const int64_t *d_pos,
+                      int32_t *d_slot_mapping) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (n == 0) return LTKV_OK;
+  if (!d_rows || !d_pos || !d_slot_mapping) return fail(LTKV_ERR_ARG, "null device pointer");
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (int rc = sync_tables(c)) return rc;
+  HIP_TRY(ltkv::launch_slot_mapping(c->d_rt, c->d_rt_nb, (int64_t)c->rt_width, (int64_t)c->rt_rows,
+                                    d_rows, d_pos, (int64_t)n, d_slot_mapping, c->stream),
+          "slot mapping launch");
+  return LTKV_OK;
+}
+
+int ltkv_read_resident_tables(ltkv_cache *c, int32_t *h_tables, int32_t *h_lengths) {
+  if (!c || !h_tables || !h_lengths) return fail(LTKV_ERR_ARG, "null argument");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  if (int rc = sync_tables(c)) return rc;
+  HIP_TRY(hipMemcpyAsync(h_tables, c->d_rt, c->rt_rows * c->rt_width * sizeof(int32_t),
+                         hipMemcpyDeviceToHost, c->stream),
+          "hipMemcpyAsync(resident tables)");
+  HIP_TRY(hipMemcpyAsync(h_lengths, c->d_rt_nb, c->rt_rows * sizeof(int32_t), hipMemcpyDeviceToHost,
+                         c->stream),
+          "hipMemcpyAsync(resident table lengths)");
+  HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  return LTKV_OK;
+}
+
+int ltkv_table_uploads(const ltkv_cache *c, uint64_t *entries) {
+  if (!c || !entries) return fail(LTKV_ERR_ARG, "null argument");
+  *entries = c->rt_uploaded;
   return LTKV_OK;
 }
 
@@ -1095,6 +1371,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   a.split = split;
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
+  a.max_len = (int64_t)(P.sstride * LTKV_BLOCK);
   a.lens = d + P.off_slens;
   if (P.n_pass < P.n) {  // only the queries that groups did not complete
     a.n = (int64_t)P.n_pass;

@@ -58,6 +58,14 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
                          const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
                          hipStream_t s);
 
+// Resident block tables: updates (row, col, value) triples (col -1: the
+// row's length in blocks), and the slot mapping of (row, position) tokens.
+hipError_t launch_table_update(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,
+                               const int32_t *upd, int64_t n, hipStream_t s);
+hipError_t launch_slot_mapping(const int32_t *tables, const int32_t *counts, int64_t width,
+                               int64_t n_rows, const int32_t *rows, const int64_t *pos, int64_t n,
+                               int32_t *out, hipStream_t s);
+
 struct AttnArgs {
   const void *k_layer, *v_layer;
   const void *k_scale, *v_scale;  // q8_0 pools: per-32 f16 scales of the layer, else null
@@ -76,6 +84,13 @@ struct AttnArgs {
   // (partition_tokens(len) / split tokens each, split 1 or 2); max_parts
   // counts the finer partitions. attention_split gives it for a shape.
   int split;
+  // Resident block tables: query i reads row rows[i] of `tables` (rows ==
+  // nullptr: row i); rows outside [0, n_rows) read row 0.
+  const int32_t *rows;
+  int64_t n_rows;
+  // Lengths are cut to max_len tokens (at most table_stride * 16); the grid's
+  // max_parts covers max_len.
+  int64_t max_len;
   // Group partials folded into each query's result (planned attention), or
   // pre_parts == nullptr: query i has pre_parts[i] partials at pre_o/pre_ml
   // slot (i * n_heads + head) * max_pre_parts + p; -1: its group wrote the

@@ -1,15 +1,26 @@
 // gfx950 (MI355X, CDNA4) kernels of the paged KV-cache path.
 //
-//   write_kernel       slot-mapped K/V append   (kv.rs:123-131 write, per model.rs:414-429)
-//   copy_blocks_kernel copy-on-write block copy (kv.rs:99-110)
-//   gather_kernel      block-table gather       (kv.rs:133-150 rows, collected)
-//   attn_kernel        GQA paged decode attention, split over context partitions
-//   attn_merge_kernel  log-sum-exp merge of the partitions (model.rs:431-475 semantics)
+//   write_kernel / write_q8_kernel      slot-mapped K/V append (kv.rs:123-131 write,
+//                                       per model.rs:414-429; q8_0 per quant.rs:785-791)
+//   write_rope_kernel / write_rope_q8_kernel  RoPE of K and Q (model.rs:291-308) fused
+//                                       into the append
+//   copy_blocks_kernel                  copy-on-write block copy (kv.rs:99-110)
+//   gather_kernel                       block-table gather (kv.rs:133-150 rows, collected)
+//   attn_mfma_kernel                    GQA paged decode attention on the matrix cores
+//                                       (f16 and q8_0 pools), split over context partitions
+//   attn16_kernel / attn_kernel         the same on the vector ALU (f32 pools)
+//   attn_merge_kernel                   log-sum-exp merge of the partitions (model.rs:431-475)
+//   mq_attn_kernel                      query rows that share K/V rows (prefix groups,
+//                                       prefill chunks) on the matrix cores
+//   table_update_kernel / slot_mapping_kernel  resident block tables and the slot
+//                                       mapping derived from them
 //
-// Every kernel is HBM-bandwidth bound: the data-movement kernels move each
-// byte once with 16-byte (dwordx4) accesses, and decode attention does ~4
-// flop per KV byte, far below the vector-ALU ridge point, so no MFMA is used.
-// Wavefronts are 64 lanes; reductions use DPP row permutations within a wave.
+// The data-movement kernels are HBM-bandwidth bound and move each byte once
+// with 16-byte accesses. Decode attention does ~4-7 flop per KV byte, but
+// its per-element work (a G-way dot product per K element, a G-way FMA per
+// V element) would keep the vector ALU busy for most of the time the bytes
+// take, so it runs its products on MFMA. Wavefronts are 64 lanes;
+// reductions use DPP row permutations within a wave.
 
 #include <hip/hip_runtime.h>
 
@@ -505,6 +516,19 @@ constexpr int kBufferWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9-f
 constexpr int kNt = 2;                    // buffer load cache policy: non-temporal
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Block table of query qi: row qi of `tables`, or, with resident tables, row
+// rows[qi] (a row outside [0, n_rows) reads row 0: such a query must have
+// length 0, and nothing is read then).
+__device__ __forceinline__ const int32_t *table_of(const int32_t *tables, int64_t stride,
+                                                   const int32_t *rows, int64_t n_rows, int64_t qi) {
+  int64_t r = qi;
+  if (rows) {
+    r = rows[qi];
+    if (r < 0 || r >= n_rows) r = 0;
+  }
+  return tables + r * stride;
+}
+
 template <typename T, int HD, int G>
 __global__ void __launch_bounds__(256)
 attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
@@ -513,7 +537,8 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
             int max_parts, const int32_t *__restrict__ pre_parts,
-            const int32_t *__restrict__ qmap) {
+            const int32_t *__restrict__ qmap, const int32_t *__restrict__ rows, int64_t n_rows,
+            int64_t max_len) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
   constexpr int RPL = 64 / L;      // rows per wave load
@@ -533,7 +558,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
 
   int64_t len = lens[qi];
   if (len < 0) len = 0;
-  if (len > table_stride * 16) len = table_stride * 16;
+  if (len > max_len) len = max_len;
   // A query with group partials and nothing else to read (or whose group
   // wrote its output) has no work here.
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
@@ -568,7 +593,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
     for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
   }
 
-  const int32_t *tab = tables + qi * table_stride;
+  const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
   const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
   const int64_t head_off = (int64_t)kvh * head_stride;
 
@@ -791,7 +816,7 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
   constexpr int ppw = 256 / (HD / 4);
   const unsigned mgrid = (unsigned)((pairs + ppw - 1) / ppw);
   attn_merge_kernel<HD><<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
-                                              a.part_tokens, a.split, a.max_parts, a.table_stride * 16,
+                                              a.part_tokens, a.split, a.max_parts, a.max_len,
                                               a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
                                               a.qmap, pairs);
   return hipGetLastError();
@@ -926,7 +951,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               float *__restrict__ part_ml, int n_kv_heads, int64_t n_blocks, int64_t block_stride,
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
               int max_parts, const int32_t *__restrict__ pre_parts,
-              const int32_t *__restrict__ qmap) {
+              const int32_t *__restrict__ qmap, const int32_t *__restrict__ rows, int64_t n_rows,
+            int64_t max_len) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
@@ -953,7 +979,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 
   int64_t len = lens[qi];
   if (len < 0) len = 0;
-  if (len > table_stride * 16) len = table_stride * 16;
+  if (len > max_len) len = max_len;
   // A query with group partials and nothing else to read (or whose group
   // wrote its output) has no work here.
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
@@ -1035,7 +1061,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
 
-  const int32_t *tab = tables + qi * table_stride;
+  const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
 
   // A tile is read through buffer descriptors whose extent ends at the last
   // row inside the context: rows past it (and every row of a prefetch past
@@ -1364,7 +1390,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
                  int split, int max_parts, const int32_t *__restrict__ pre_parts,
                  const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
-                 const uint16_t *__restrict__ vscale) {
+                 const uint16_t *__restrict__ vscale, const int32_t *__restrict__ rows, int64_t n_rows,
+                 int64_t max_len) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -1400,7 +1427,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   int64_t len = lens[qi];
   if (len < 0) len = 0;
-  if (len > table_stride * 16) len = table_stride * 16;
+  if (len > max_len) len = max_len;
   // A query with group partials and nothing else to read (or whose group
   // wrote its output) has no work here.
   if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
@@ -1475,7 +1502,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int32_t *tab = tables + qi * table_stride;
+  const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
 
   struct Stage {
     u32x4 k[NLD], v[NLD];
@@ -1707,7 +1734,8 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
-      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale));
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
+      a.max_len);
   return launch_merge<HD>(a, s);
 }
 
@@ -1718,7 +1746,7 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap);
+      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
   return launch_merge<HD>(a, s);
 }
 
@@ -1729,7 +1757,7 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap);
+      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
   return launch_merge<HD>(a, s);
 }
 
@@ -2085,6 +2113,46 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   }
 }
 
+// ----------------------------------------------------------------------------
+// Resident block tables (step descriptor): in-place updates and the slot
+// mapping of a batch's tokens.
+
+// Update i is (row, col, value): tables[row][col] = value, or, with col ==
+// -1, counts[row] = value (the row's table length in blocks). Entries outside
+// the arrays are skipped.
+__global__ void __launch_bounds__(256)
+table_update_kernel(int32_t *__restrict__ tables, int32_t *__restrict__ counts, int64_t width,
+                    int64_t n_rows, const int32_t *__restrict__ upd, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t r = upd[3 * i], c = upd[3 * i + 1], v = upd[3 * i + 2];
+  if (r < 0 || r >= n_rows) return;
+  if (c == -1)
+    counts[r] = v;
+  else if (c >= 0 && c < width)
+    tables[(int64_t)r * width + c] = v;
+}
+
+// Token i at position pos[i] of the sequence in row rows[i]: cell
+// block * 16 + pos % 16 with block = tables[row][pos / 16] (kv.rs:95-121's
+// (block, slot), flattened as the write kernels take it), or -1 when the row
+// is outside the tables or pos / 16 is past the row's table length.
+__global__ void __launch_bounds__(256)
+slot_mapping_kernel(const int32_t *__restrict__ tables, const int32_t *__restrict__ counts,
+                    int64_t width, int64_t n_rows, const int32_t *__restrict__ rows,
+                    const int64_t *__restrict__ pos, int64_t n, int32_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t r = rows[i];
+  const int64_t p = pos[i];
+  int32_t cell = -1;
+  if (r >= 0 && r < n_rows && p >= 0) {
+    const int64_t b = p >> 4;
+    if (b < counts[r] && b < width) cell = tables[(int64_t)r * width + b] * 16 + (int32_t)(p & 15);
+  }
+  out[i] = cell;
+}
+
 }  // namespace
 
 hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale,
@@ -2180,6 +2248,24 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
       static_cast<const uint8_t *>(k_layer), static_cast<const uint8_t *>(v_layer), tables,
       table_stride, lens, out_offsets, static_cast<uint8_t *>(k_out),
       static_cast<uint8_t *>(v_out), g.n_blocks, row_bytes, chunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_table_update(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,
+                               const int32_t *upd, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if ((n + 255) / 256 >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  table_update_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tables, counts, width, n_rows, upd, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_slot_mapping(const int32_t *tables, const int32_t *counts, int64_t width,
+                               int64_t n_rows, const int32_t *rows, const int64_t *pos, int64_t n,
+                               int32_t *out, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if ((n + 255) / 256 >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  slot_mapping_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tables, counts, width, n_rows, rows,
+                                                                  pos, n, out);
   return hipGetLastError();
 }
 

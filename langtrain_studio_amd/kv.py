@@ -298,6 +298,76 @@ class KvCache:
             _dev_ptr(out, torch.float32, "out", self.device)))
         return out
 
+    # ---- resident block tables (device step descriptor)
+    def seq_rows(self, seqs: Sequence[int]) -> np.ndarray:
+        """Row of each sequence in the resident tables (-1: no blocks)."""
+        seqs_a = np.ascontiguousarray(seqs, dtype=np.uint32)
+        out = np.empty(seqs_a.shape, dtype=np.int32)
+        _check(self._lib.ltkv_seq_rows(self._h, seqs_a.size, _np_ptr(seqs_a), _np_ptr(out)))
+        return out
+
+    def sync_tables(self) -> None:
+        """Enqueue the upload of the block-table changes since the last one."""
+        _check(self._lib.ltkv_sync_tables(self._h))
+
+    def resident_tables(self):
+        """(tables [rows][stride], lengths [rows]) of the resident tables,
+        copied to host after pending uploads (synchronous)."""
+        t, l = C.c_void_p(), C.c_void_p()
+        stride, rows = C.c_size_t(), C.c_size_t()
+        _check(self._lib.ltkv_resident_tables(self._h, C.byref(t), C.byref(l), C.byref(stride),
+                                              C.byref(rows)))
+        tables = np.empty((rows.value, stride.value), dtype=np.int32)
+        lengths = np.empty((rows.value,), dtype=np.int32)
+        _check(self._lib.ltkv_read_resident_tables(self._h, _np_ptr(tables), _np_ptr(lengths)))
+        return tables, lengths
+
+    def slot_mapping(self, rows, pos, out=None):
+        """Slot mapping of tokens (row, position) from the resident tables,
+        computed on the device; rows int32, pos int64 device tensors."""
+        import torch
+
+        n = rows.numel()
+        if pos.numel() != n:
+            raise ValueError("rows and pos must have equal length")
+        if out is None:
+            out = torch.empty((n,), dtype=torch.int32, device=rows.device)
+        _check(self._lib.ltkv_slot_mapping(self._h, n, _dev_ptr(rows, torch.int32, "rows", self.device),
+                                           _dev_ptr(pos, torch.int64, "pos", self.device),
+                                           _dev_ptr(out, torch.int32, "out", self.device)))
+        return out
+
+    def decode_attention_rows(self, layer: int, q, rows, lens, n_heads: int, head_dim: int,
+                              scale: Optional[float] = None, out=None):
+        """decode_attention over the resident tables: query i reads the
+        sequence in row rows[i] (device int32)."""
+        import torch
+
+        n = lens.numel()
+        if q.dim() != 2 or q.shape != (n, n_heads * head_dim):
+            raise ValueError("q must be [n][n_heads*head_dim]")
+        if rows.numel() != n:
+            raise ValueError("rows must have one entry per query")
+        if out is None:
+            out = torch.empty_like(q)
+        elif out.shape != q.shape:
+            raise ValueError("out must match q")
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)  # model.rs:402
+        _check(self._lib.ltkv_decode_attention_rows(
+            self._h, layer, n, n_heads, head_dim, float(scale),
+            _dev_ptr(q, torch.float32, "q", self.device),
+            _dev_ptr(rows, torch.int32, "rows", self.device),
+            _dev_ptr(lens, torch.int32, "lens", self.device),
+            _dev_ptr(out, torch.float32, "out", self.device)))
+        return out
+
+    def table_uploads(self) -> int:
+        """Resident-table entries uploaded so far."""
+        v = C.c_uint64()
+        _check(self._lib.ltkv_table_uploads(self._h, C.byref(v)))
+        return int(v.value)
+
     def plan_attention(self, seqs: Sequence[int], lens: Sequence[int], n_heads: int, head_dim: int,
                        shared_prefix: bool = True) -> dict:
         """Step descriptor for planned_attention: query i reads positions
