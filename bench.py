@@ -47,7 +47,7 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed", "prefill", "rope-append", "decode-q8"],
+                            "mixed", "prefill", "rope-append", "decode-q8", "descriptor"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -687,6 +687,135 @@ def bench_mixed(args):
         flush=True)
 
 
+def bench_descriptor(args):
+    """The step descriptor two ways, on the continuous-batching step of the
+    Qwen2.5-7B layer (120 decode sequences, contexts U[512, 8192], 2% finish
+    per step and arrivals take their slot, plus 8 prefill streams of 512-token
+    chunks). Per step the host claims the cells, then either
+      tables: builds every decode query's full block table and the slot
+              mapping on the host and uploads both (the engine-side path of
+              ltkv_decode_attention), or
+      resident: uploads the table entries that changed (ltkv_sync_tables),
+              the tokens' rows and positions, derives the slot mapping on
+              the device (ltkv_slot_mapping) and attends by row
+              (ltkv_decode_attention_rows).
+    A third mode, resident-slots, also derives the slot mapping on the
+    device from the tokens' rows and positions (what an engine that keeps
+    positions on the device for RoPE would upload) instead of uploading the
+    host's. All run the same appends and attention; timed per step on the
+    host clock (claim + descriptor + launches + stream synchronisation), and
+    the block tables' host-to-device bytes are counted."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_heads, n_kv, hd, n_dec, n_pre, chunk = 28, 4, 128, 120, 8, 512
+    steps = max(args.steps, 1)
+    kvd = n_kv * hd
+    dev = torch.device("cuda", 0)
+    stride = (8192 + steps + chunk) // BLOCK + 2
+    n_blocks = int((n_dec + n_pre) * 8192 // BLOCK * 1.1) + (n_dec + n_pre) * (steps // BLOCK + 2)
+    results = {}
+    for mode in ("tables", "resident", "resident-slots"):
+        rng = np.random.default_rng(args.seed)
+        kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+        kv.init_free_order(rng.permutation(n_blocks))
+        _fill_pool_random(kv, kvd, n_blocks, args.seed)
+        next_id = [0]
+
+        def new_seq(ctx):
+            sid = next_id[0]
+            next_id[0] += 1
+            if ctx:
+                kv.append_batch(np.full(ctx, sid, np.uint32), np.arange(ctx, dtype=np.uint64))
+            return sid
+
+        dec = [new_seq(int(rng.integers(512, 8193))) for _ in range(n_dec)]
+        pre = [(new_seq(0), int(rng.integers(512, 8193))) for _ in range(n_pre)]
+        kn = torch.randn((n_pre * chunk + n_dec, kvd), device=dev)
+        q = torch.randn((n_dec, n_heads * hd), device=dev)
+        out = torch.empty_like(q)
+        h_tab = torch.empty((n_dec, stride), dtype=torch.int32).pin_memory()
+        d_tab = torch.empty((n_dec, stride), dtype=torch.int32, device=dev)
+        if mode != "tables":
+            kv.sync_tables()
+        torch.cuda.synchronize()
+        up0 = 0
+        wall, table_bytes = [], 0
+        d_dec_rows = torch.empty((n_dec,), dtype=torch.int32, device=dev)
+        rows_stale = True
+        for s in range(steps + 3):
+            t0 = time.perf_counter()
+            seqs, pos, pre_counts = [], [], []
+            for sid, target in pre:
+                start = kv.len(sid)
+                n = min(chunk, target - start)
+                seqs += [sid] * n
+                pos += list(range(start, start + n))
+                pre_counts.append(n)
+            for sid in dec:
+                seqs.append(sid)
+                pos.append(kv.len(sid))
+            seqs_a = np.array(seqs, np.uint32)
+            pos_a = np.array(pos, np.uint64)
+            sm = kv.append_batch(seqs_a, pos_a)
+            lens = torch.from_numpy(np.array([kv.len(sid) for sid in dec], np.int32)).to(dev, non_blocking=True)
+            n_tok = len(seqs)
+            if mode == "tables":
+                d_sm = torch.from_numpy(sm).to(dev, non_blocking=True)
+                h_tab.numpy()[:] = kv.block_tables(np.array(dec, np.uint32), stride)
+                d_tab.copy_(h_tab, non_blocking=True)
+                kv.write_batch(0, d_sm, kn[:n_tok], kn[:n_tok])
+                kv.decode_attention(0, q, d_tab, lens, n_heads, hd, out=out)
+                if s >= 3:
+                    table_bytes += d_tab.numel() * 4
+            elif mode == "resident":
+                d_sm = torch.from_numpy(sm).to(dev, non_blocking=True)
+                if rows_stale:  # a decode sequence arrived: refresh the rows the step reads
+                    d_dec_rows.copy_(torch.from_numpy(kv.seq_rows(np.array(dec, np.uint32))))
+                    rows_stale = False
+                kv.write_batch(0, d_sm, kn[:n_tok], kn[:n_tok])
+                kv.decode_attention_rows(0, q, d_dec_rows, lens, n_heads, hd, out=out)
+            else:
+                # one row lookup per sequence, expanded to its tokens
+                srows = kv.seq_rows(np.array([sid for sid, _ in pre] + dec, np.uint32))
+                tok_rows = np.concatenate([np.repeat(srows[:n_pre], pre_counts), srows[n_pre:]])
+                d_rows = torch.from_numpy(tok_rows).to(dev, non_blocking=True)
+                d_pos = torch.from_numpy(pos_a.astype(np.int64)).to(dev, non_blocking=True)
+                d_sm = kv.slot_mapping(d_rows, d_pos)
+                kv.write_batch(0, d_sm, kn[:n_tok], kn[:n_tok])
+                kv.decode_attention_rows(0, q, d_rows[n_tok - n_dec:], lens, n_heads, hd, out=out)
+            if mode != "tables" and s == 2:
+                torch.cuda.synchronize()
+                up0 = kv.table_uploads()
+            torch.cuda.synchronize()
+            if s >= 3:
+                wall.append(time.perf_counter() - t0)
+            for i, (sid, target) in enumerate(pre):
+                if kv.len(sid) >= target:
+                    kv.truncate(sid, 0)
+                    pre[i] = (new_seq(0), int(rng.integers(512, 8193)))
+            for i, sid in enumerate(dec):
+                if rng.random() < 0.02:
+                    kv.truncate(sid, 0)
+                    dec[i] = new_seq(int(rng.integers(512, 8193)))
+                    rows_stale = True
+        if mode != "tables":
+            kv.sync_tables()
+            torch.cuda.synchronize()
+            table_bytes = (kv.table_uploads() - up0) * 12
+        results[mode] = {"step_wall_us": round(float(np.mean(wall)) * 1e6, 1),
+                         "step_wall_us_p50": round(float(np.median(wall)) * 1e6, 1),
+                         "table_h2d_bytes_per_step": round(table_bytes / steps)}
+        del kv
+    print(json.dumps({
+        "workload": f"descriptor qwen2.5-7b f16: 8x512 prefill append + 120 decode, 2% churn, {steps} steps",
+        "tables": results["tables"], "resident": results["resident"],
+        "resident_slots": results["resident-slots"],
+        "h2d_ratio": round(results["tables"]["table_h2d_bytes_per_step"]
+                           / max(results["resident"]["table_h2d_bytes_per_step"], 1), 1)}), flush=True)
+
+
 def _time_decode(w: Llama3Decode, steps: int, warmup: int):
     """Times `steps` decode steps (append then attention) with HIP events on
     the stream both run on: (µs per step, attention µs, append µs, wall s)."""
@@ -753,7 +882,8 @@ def main():
         sys.exit(1)
     extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
              "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
-             "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8}
+             "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8,
+             "descriptor": bench_descriptor}
     if args.workload in extra:
         extra[args.workload](args)
         return
