@@ -552,7 +552,7 @@ def bench_prefix_cow(args):
     pairs = np.stack([np.full(S, shared_last), dst], 1)[dst != shared_last].astype(np.int32)
     assert len(pairs) == S - 1
     d_pairs = torch.from_numpy(pairs).cuda()
-    cow_us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=10)
+    cow_us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=100, warmup=10)
     uniq_blocks = len(np.unique(tables_h[tables_h >= 0]))
     uniq = uniq_blocks * BLOCK * kvd * 2 * 2 + 2 * S * n_heads * hd * 4
     logical = int(np.mean([l.astype(np.int64).sum() for l in lens])) * 2 * kvd * 2

@@ -393,10 +393,12 @@ write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uin
                   (is_v ? vscale : kscale) + scale_index(s, e >> 5, kv_dim >> 5));
 }
 // ----------------------------------------------------------------------------
-// Kernel 2: block copy. Work item = (pair, layer, tensor, 16 KiB chunk); 256
-// threads each move 4 x 16 bytes, all loads issued before the stores.
+// Kernel 2: block copy. Work item = (pair, layer, tensor, 8 KiB chunk); 256
+// threads each move 2 x 16 bytes, all loads issued before the stores. (At the
+// 255-copy step of 256 forks, 8 KiB chunks ran 5.2-5.4 us against 5.6-5.8 us
+// for 16 KiB, 6.4-6.5 for 4 KiB and 7.2-7.3 for 32 KiB.)
 // ----------------------------------------------------------------------------
-constexpr int kCopyUnroll = 4;
+constexpr int kCopyUnroll = 2;
 constexpr int64_t kCopyChunk = 256 * 16 * kCopyUnroll;  // bytes per work-group
 
 __global__ void __launch_bounds__(256)
@@ -2300,15 +2302,16 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
   return hipErrorInvalidValue;
 }
 
-int attention_split(int elem, int group, int n_kv_heads, int64_t n) {
+int attention_split(int elem, int group, int n_kv_heads, int64_t n, int max_parts) {
   if (!((elem == 1 || elem == 2) && group <= 4 && n_kv_heads % 2 == 0)) return 1;
   // Measured at the Llama-3-8B decode shape (64 queries): q8_0 waves of two
   // heads (256 B rows of K and of V) run fastest with each partition cut in
   // two; f16 waves of two heads (512 B rows, three tiles in flight) keep HBM
   // busy at one wave per SIMD and run fastest uncut, so they are cut only
-  // when four partitions per query would leave SIMDs idle.
+  // when the uncut grid (max_parts partitions per query) would leave SIMDs
+  // idle.
   if (elem == 1) return 2;
-  return n * (n_kv_heads / 2) * 4 < 1024 ? 2 : 1;
+  return n * (n_kv_heads / 2) * max_parts < 1024 ? 2 : 1;
 }
 
 int mq_rows(int) { return 32 * kMqWaves; }
