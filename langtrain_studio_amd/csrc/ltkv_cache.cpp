@@ -1186,7 +1186,7 @@ int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size
   // max_len only bounds the grid.
   const int part = (int)c->attn_part_tokens;  // 0: per-query policy
   const int parts = ltkv::max_partitions((int64_t)max_len, part);
-  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim), (int64_t)n, parts);
+  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim));
   const size_t max_parts = (size_t)parts * split;
   if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
@@ -1353,7 +1353,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   int part = (int)c->attn_part_tokens;
   if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) part = P.suffix_part;
   const int parts = ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
-  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim), (int64_t)P.n, parts);
+  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim));
   const size_t max_parts = (size_t)parts * split;
   if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");

@@ -133,9 +133,9 @@ bool attention_supported(int elem, int head_dim, int group);
 // Decode kernels on f16 and q8_0 pools read two adjacent kv heads per wave
 // when the group has at most 4 query heads and the kv heads pair up (the
 // wave's 2 x group query heads fill the 16 columns of its products). The
-// partition divisor (1 or 2) for n queries of such a shape with at most
-// max_parts partitions each: 1 otherwise.
-int attention_split(int elem, int group, int n_kv_heads, int64_t n, int max_parts);
+// partition divisor (1 or 2) of such a shape, 1 otherwise. It never depends
+// on the batch: a query's result bits depend on its own inputs only.
+int attention_split(int elem, int group, int n_kv_heads);
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
 
 // One work-group of shared-prefix attention (mq_attn_kernel): the query rows

@@ -1303,7 +1303,11 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 // every K element costs a G-way dot product and every V element a G-way
 // FMA; with 1-byte q8_0 elements (or G > 4) that keeps the VALU busy for
 // longer than the tile's bytes take to arrive. Here both products of a
-// 16-token tile run on MFMA, one wave per (query, kv head, partition):
+// 16-token tile run on MFMA, one wave per (query, NH adjacent kv heads,
+// partition); NH = 2 when the 2 G query heads fit the 16 columns (G <= 4),
+// so each row segment read is two heads wide (512 B for f16), and each
+// product then runs once per kv head, its Q' / P' zero outside that head's
+// columns:
 //   S^T[token][col] = K Q'^T   v_mfma_f32_16x16x32_f16, A = the K tile
 //                              (staged through LDS into the A layout),
 //                              B = Q' in registers;
@@ -2302,16 +2306,15 @@ hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStre
   return hipErrorInvalidValue;
 }
 
-int attention_split(int elem, int group, int n_kv_heads, int64_t n, int max_parts) {
+int attention_split(int elem, int group, int n_kv_heads) {
   if (!((elem == 1 || elem == 2) && group <= 4 && n_kv_heads % 2 == 0)) return 1;
   // Measured at the Llama-3-8B decode shape (64 queries): q8_0 waves of two
   // heads (256 B rows of K and of V) run fastest with each partition cut in
   // two; f16 waves of two heads (512 B rows, three tiles in flight) keep HBM
-  // busy at one wave per SIMD and run fastest uncut, so they are cut only
-  // when the uncut grid (max_parts partitions per query) would leave SIMDs
-  // idle.
-  if (elem == 1) return 2;
-  return n * (n_kv_heads / 2) * max_parts < 1024 ? 2 : 1;
+  // busy at one wave per SIMD and run fastest uncut. The cut depends on the
+  // dtype and shape only, never on the batch, so a query's partitions (and
+  // its result bits) stay those of its own length.
+  return elem == 1 ? 2 : 1;
 }
 
 int mq_rows(int) { return 32 * kMqWaves; }

@@ -1,0 +1,165 @@
+"""Parity at the full sizes of the benchmarked workloads (Llama-3-8B layer:
+32 q heads / 8 kv heads / head_dim 128, f16, 16-token blocks over permuted
+pools), through the oracle where it finishes in seconds and through exact
+properties where it would not.
+
+* decode step, 64 sequences, contexts U[2048, 4096]: attention against the
+  oracle on the read-back pool (tolerance), batch invariance and attention by
+  resident rows (bit-exact);
+* long context, 32 x 32 768 tokens, fully permuted pool (4.3 GB): the gather
+  of every sequence equals the f16 rounding of the rows written, in order
+  (bit-exact), and attention matches the oracle;
+* prefix sharing, 256 forks of a 4088-token prefix with 64-token suffixes:
+  255 copy-on-write copies each equal to the shared block's prefix rows
+  (bit-exact), and planned (grouped) attention matches the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import BLOCK, attention_close
+
+pytestmark = pytest.mark.gpu
+
+N_HEADS, N_KV, HD = 32, 8, 128
+KVD = N_KV * HD
+
+
+def _cache(n_blocks, seed):
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    kv = KvCache(1, KVD, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(np.random.default_rng(seed).permutation(n_blocks))
+    return kv
+
+
+def _write_random(kv, sm, seed, chunk=1 << 15):
+    """Write N(0,1) K/V rows for slot mapping sm, chunk by chunk, from a
+    seeded generator (regenerable with _random_rows)."""
+    import torch
+
+    for i, (k, v) in enumerate(_random_rows(sm.size, seed, chunk)):
+        kv.write_batch(0, torch.from_numpy(sm[i * chunk:i * chunk + k.shape[0]]).cuda(), k, v)
+
+
+def _random_rows(n, seed, chunk):
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        yield (torch.randn((m, KVD), generator=gen, device="cuda"),
+               torch.randn((m, KVD), generator=gen, device="cuda"))
+
+
+def _oracle_with_pool(kv, n_blocks):
+    from oracle import OracleKv
+
+    o = OracleKv(1, KVD, n_blocks * BLOCK, dtype="f16")
+    o.load_pool(0, *kv.read_pool(0))
+    return o
+
+
+def test_llama3_decode_step_full_size(gpu):
+    import torch
+
+    rng = np.random.default_rng(2024)
+    B = 64
+    ctx = rng.integers(2048, 4097, B)
+    n_blocks = int(np.ceil(sum(-(-(int(c) + 1) // BLOCK) for c in ctx) * 1.1))
+    kv = _cache(n_blocks, 1)
+    seqs = np.repeat(np.arange(B, dtype=np.uint32), ctx)
+    pos = np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx])
+    _write_random(kv, kv.append_batch(seqs, pos), 3)
+    # the step: one appended token per sequence, then attention over len = ctx + 1
+    step_sm = kv.append_batch(np.arange(B, dtype=np.uint32), ctx.astype(np.uint64))
+    _write_random(kv, step_sm, 4)
+    lens = (ctx + 1).astype(np.int32)
+    tables = kv.block_tables(np.arange(B, dtype=np.uint32))
+    q = torch.randn((B, N_HEADS * HD), generator=torch.Generator(device="cuda").manual_seed(5), device="cuda")
+    d_tables, d_lens = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    out = kv.decode_attention(0, q, d_tables, d_lens, N_HEADS, HD).cpu().numpy()
+
+    o = _oracle_with_pool(kv, n_blocks)
+    want = o.attention_tables(0, tables, lens, q.cpu().numpy(), N_HEADS, HD, threads=16)
+    attention_close(out, want, "f16")
+
+    # a query's bits do not depend on the rest of the batch
+    sub = np.array([5, 17, 40, 63])
+    alone = kv.decode_attention(0, q[sub].contiguous(), d_tables[sub].contiguous(), d_lens[sub].contiguous(),
+                                N_HEADS, HD).cpu().numpy()
+    np.testing.assert_array_equal(alone.view(np.uint32), out[sub].view(np.uint32))
+    # the resident tables give the same bits
+    rows = torch.from_numpy(kv.seq_rows(np.arange(B, dtype=np.uint32))).cuda()
+    by_rows = kv.decode_attention_rows(0, q, rows, d_lens, N_HEADS, HD).cpu().numpy()
+    np.testing.assert_array_equal(by_rows.view(np.uint32), out.view(np.uint32))
+
+
+def test_long_context_full_size(gpu):
+    import torch
+
+    B, ctx = 32, 32768
+    n_blocks = B * ctx // BLOCK + 64
+    kv = _cache(n_blocks, 6)
+    sm = kv.append_batch(np.repeat(np.arange(B, dtype=np.uint32), ctx), np.tile(np.arange(ctx, dtype=np.uint64), B))
+    chunk = 1 << 16
+    _write_random(kv, sm, 7, chunk)
+    tables = kv.block_tables(np.arange(B, dtype=np.uint32), ctx // BLOCK)
+    d_tables = torch.from_numpy(tables).cuda()
+    lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    offs = torch.arange(B, dtype=torch.int64, device="cuda") * ctx
+    k_out = torch.empty((B * ctx, KVD), dtype=torch.float16, device="cuda")
+    v_out = torch.empty_like(k_out)
+    kv.gather(0, d_tables, lens, offs, k_out, v_out)
+    # rows were written sequence-major, so the gather must return the
+    # written rows in order, rounded to f16 (RNE), bit for bit
+    for i, (k, v) in enumerate(_random_rows(sm.size, 7, chunk)):
+        r = slice(i * chunk, i * chunk + k.shape[0])
+        assert torch.equal(k_out[r].view(torch.int16), k.half().view(torch.int16)), f"K rows {r}"
+        assert torch.equal(v_out[r].view(torch.int16), v.half().view(torch.int16)), f"V rows {r}"
+    del k_out, v_out
+
+    q = torch.randn((B, N_HEADS * HD), generator=torch.Generator(device="cuda").manual_seed(8), device="cuda")
+    out = kv.decode_attention(0, q, d_tables, lens, N_HEADS, HD).cpu().numpy()
+    o = _oracle_with_pool(kv, n_blocks)
+    want = o.attention_tables(0, tables, lens.cpu().numpy(), q.cpu().numpy(), N_HEADS, HD, threads=16)
+    attention_close(out, want, "f16")
+
+
+def test_prefix_sharing_full_size(gpu):
+    import torch
+
+    S, prefix, suffix = 256, 4088, 64
+    n_blocks = (prefix + 15) // BLOCK + S * ((suffix + 8) // BLOCK + 2) + 64
+    kv = _cache(n_blocks, 9)
+    root = S  # the prefix's own sequence, forked S times
+    _write_random(kv, kv.append_batch(np.full(prefix, root, np.uint32), np.arange(prefix, dtype=np.uint64)), 10)
+    for s in range(S):
+        kv.share(root, s, prefix)
+    kv.truncate(root, 0)  # the forks hold the prefix alone now
+    shared_last = int(kv.block_table(0)[prefix // BLOCK])
+    before = kv.read_pool(0)[0][shared_last].copy()
+    seqs = np.repeat(np.arange(S, dtype=np.uint32), suffix)
+    pos = np.tile(np.arange(prefix, prefix + suffix, dtype=np.uint64), S)
+    sm = kv.append_batch(seqs, pos)  # each fork's first append copies the partial block
+    assert kv.cow_copies() == S - 1
+    _write_random(kv, sm, 11)
+    pool_k, pool_v = kv.read_pool(0)
+    for s in range(S):
+        b = int(kv.block_table(s)[prefix // BLOCK])
+        # the prefix rows of the copied (or, for the last holder, original) block are the shared ones
+        np.testing.assert_array_equal(pool_k[b][:prefix % BLOCK], before[:prefix % BLOCK])
+    lens = np.full(S, prefix + suffix, dtype=np.int32)
+    q = torch.randn((S, N_HEADS * HD), generator=torch.Generator(device="cuda").manual_seed(12), device="cuda")
+    stats = kv.plan_attention(np.arange(S, dtype=np.uint32), lens, N_HEADS, HD)
+    assert stats["groups"] == 1 and stats["grouped"] == S
+    out = kv.planned_attention(0, q).cpu().numpy()
+    tables = kv.block_tables(np.arange(S, dtype=np.uint32))
+    o = _oracle_with_pool(kv, n_blocks)
+    want = o.attention_tables(0, tables, lens, q.cpu().numpy(), N_HEADS, HD, threads=16)
+    attention_close(out, want, "f16")

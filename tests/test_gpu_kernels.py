@@ -284,9 +284,9 @@ def test_attention_head_pairs_f16(gpu, head_dim, group, n_kv):
 
 @pytest.mark.parametrize("partition", [0, 64, 128])
 def test_attention_head_pairs_large_batch(gpu, partition):
-    """64 queries of the Llama-3-8B shape: f16 waves of two kv heads run with
-    uncut partitions (one wave per SIMD fills the chip); smaller batches cut
-    each partition in two. Both cuts must give the oracle's result."""
+    """64 queries of the Llama-3-8B shape (f16 waves of two kv heads, one
+    wave per SIMD) against the oracle, with the default and fixed
+    partitions."""
     rng = np.random.default_rng(partition + 5)
     lens = [int(x) for x in rng.integers(1, 400, size=64)]
     out, want = _attention_case(gpu, "f16", 128, 4, 8, lens, partition, seed=partition + 6)
@@ -428,23 +428,27 @@ def test_attention_physical_placement_invariance(gpu):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
-def test_attention_batch_independence(gpu):
+@pytest.mark.parametrize("dtype", ["f16", "q8_0", "f32"])
+@pytest.mark.parametrize("n_batch", [5, 300])
+def test_attention_batch_independence(gpu, dtype, n_batch):
     """A query's output is bit-identical alone and inside a batch (the
-    reference's batching property, engine/README.md:102)."""
+    reference's batching property, engine/README.md:102), for small batches
+    and for ones that fill every SIMD."""
     import torch
 
-    rng = np.random.default_rng(15)
-    lens = [2000, 9, 513, 4096, 77]
-    g, _ = _caches(1, 1024, 1000 * BLOCK, "f16", rng.permutation(1000))
+    rng = np.random.default_rng(15 + n_batch)
+    lens = [2000, 9, 513, 4096, 77] + [int(x) for x in rng.integers(1, 600, size=n_batch - 5)]
+    blocks = sum(-(-n // BLOCK) for n in lens) + 8
+    g, _ = _caches(1, 1024, blocks * BLOCK, dtype, rng.permutation(blocks))
     fill_sequences([("gpu", g)], dict(enumerate(lens)), rng, 1024)
-    q = rng.standard_normal((5, 32 * 128), dtype=np.float32)
-    tables, la = tables_and_lens(g, range(5), lens)
+    q = rng.standard_normal((n_batch, 32 * 128), dtype=np.float32)
+    tables, la = tables_and_lens(g, range(n_batch), lens)
     dq, dt, dl = (torch.from_numpy(x).to(gpu) for x in (q, tables, la))
     full = g.decode_attention(0, dq, dt, dl, 32, 128).cpu().numpy()
     for i in range(5):
         one = g.decode_attention(0, dq[i:i + 1].contiguous(), dt[i:i + 1, :-(-lens[i] // BLOCK)].contiguous(),
                                  dl[i:i + 1].contiguous(), 32, 128).cpu().numpy()
-        np.testing.assert_array_equal(one[0], full[i])
+        np.testing.assert_array_equal(one[0].view(np.uint32), full[i].view(np.uint32))
 
 
 def test_attention_workspace_reuse_across_shapes(gpu):
