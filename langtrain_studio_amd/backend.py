@@ -37,17 +37,31 @@ class StepPlan:
 
     n: int
     slot_mapping: "object"  # torch.int32 [n], cell block*16+slot per token
-    tables: "object"        # torch.int32 [n][stride], the token's sequence table
+    tables: "object"        # torch.int32 [n][stride], the token's sequence table ("tables")
     lens: "object"          # torch.int32 [n], pos+1 (positions attended, model.rs:437)
     slot_mapping_host: np.ndarray
+    rows: "object" = None   # torch.int32 [n], the token's resident table row ("resident")
+    planned: bool = False   # the cache holds this step's attention plan ("planned")
+
+DESCRIPTORS = ("tables", "resident", "planned")
 
 
 class PagedKvBackend:
+    """descriptor selects how a step's block tables reach the device:
+    "tables" uploads each token's full table per step; "resident" reads the
+    cache's device-resident tables by sequence row (only changed entries are
+    uploaded); "planned" builds one attention plan per step
+    (ltkv_plan_attention, shared-prefix and prefill-chunk groups on the
+    matrix cores) that every layer of the step reuses."""
+
     def __init__(self, n_layers: int, n_heads: int, n_kv_heads: int, head_dim: int, kv_tokens: int,
                  n_seq_max: int = 1, n_batch: int = 512, dtype: str = "f16", device: int = 0,
-                 stream=None):
+                 stream=None, descriptor: str = "tables"):
         if n_heads % n_kv_heads:
             raise ValueError("n_heads must be a multiple of n_kv_heads")
+        if descriptor not in DESCRIPTORS:
+            raise ValueError(f"descriptor must be one of {DESCRIPTORS}")
+        self.descriptor = descriptor
         self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim = n_layers, n_heads, n_kv_heads, head_dim
         self.kv = KvCache(n_layers, n_kv_heads * head_dim, kv_tokens, dtype=dtype, device=device,
                           stream=stream)
@@ -84,21 +98,28 @@ class PagedKvBackend:
         pos = np.array([b.pos for b in batch], dtype=np.uint64)
         sm = self.kv.append_batch(seqs, pos)
         lens = (pos + 1).astype(np.int32)
-        stride = max(1, int(math.ceil(lens.max() / BLOCK))) if len(batch) else 1
-        tables = self.kv.block_tables(seqs, stride)
         dev = torch.device("cuda", self.device)
-        return StepPlan(
-            n=len(batch),
-            slot_mapping=torch.from_numpy(sm).to(dev),
-            tables=torch.from_numpy(tables).to(dev),
-            lens=torch.from_numpy(lens).to(dev),
-            slot_mapping_host=sm,
-        )
+        plan = StepPlan(n=len(batch), slot_mapping=torch.from_numpy(sm).to(dev), tables=None,
+                        lens=torch.from_numpy(lens).to(dev), slot_mapping_host=sm)
+        if self.descriptor == "tables":
+            stride = max(1, int(math.ceil(lens.max() / BLOCK))) if len(batch) else 1
+            plan.tables = torch.from_numpy(self.kv.block_tables(seqs, stride)).to(dev)
+        elif self.descriptor == "resident":
+            plan.rows = torch.from_numpy(self.kv.seq_rows(seqs)).to(dev)
+        else:
+            self.kv.plan_attention(seqs, lens, self.n_heads, self.head_dim, shared_prefix=True)
+            plan.planned = True
+        return plan
 
     def layer(self, plan: StepPlan, layer: int, q, k, v, out: Optional[object] = None):
         """model.rs:414-475 for one layer: write k, v ([n][kv_dim] f32, RoPE
         already applied) into the claimed cells, then attention of q
         ([n][n_heads*head_dim] f32) over each token's sequence."""
         self.kv.write_batch(layer, plan.slot_mapping, k, v)
+        if plan.planned:
+            return self.kv.planned_attention(layer, q, self.scale, out=out)
+        if plan.rows is not None:
+            return self.kv.decode_attention_rows(layer, q, plan.rows, plan.lens, self.n_heads, self.head_dim,
+                                                 self.scale, out=out)
         return self.kv.decode_attention(layer, q, plan.tables, plan.lens, self.n_heads, self.head_dim,
                                         self.scale, out=out)
