@@ -366,18 +366,25 @@ int ensure_workspace(ltkv_cache *c, size_t bytes) {
 int sync_tables(ltkv_cache *c) {
   const size_t need_rows = c->rt_seq.size();
   size_t need_w = c->rt_width;
+  // Blocks of the live sequence in row r (0 for a free row).
+  auto row_blocks = [&](int32_t r) -> const std::vector<int32_t> * {
+    if (!c->rt_live[r]) return nullptr;
+    const auto it = c->seqs.find(c->rt_seq[r]);
+    return it == c->seqs.end() ? nullptr : &it->second.blocks;
+  };
   for (int32_t r : c->rt_dirty_rows)
-    if (c->rt_live[r]) need_w = std::max(need_w, c->seqs.at(c->rt_seq[r]).blocks.size());
+    if (const std::vector<int32_t> *b = row_blocks(r)) need_w = std::max(need_w, b->size());
   const bool grow = !c->d_rt || need_rows > c->rt_rows || need_w > c->rt_width;
   if (!grow && c->rt_dirty_rows.empty()) return LTKV_OK;
   std::vector<int32_t> &u = c->rt_upd;
   u.clear();
   auto row_updates = [&](int32_t r, size_t lo, size_t hi) {
-    if (!c->rt_live[r]) {  // released: an empty table
+    const std::vector<int32_t> *b = row_blocks(r);
+    if (!b) {  // released: an empty table
       u.insert(u.end(), {r, -1, 0});
       return;
     }
-    const std::vector<int32_t> &blocks = c->seqs.at(c->rt_seq[r]).blocks;
+    const std::vector<int32_t> &blocks = *b;
     hi = std::min(hi, blocks.size());
     for (size_t j = lo; j < hi; ++j) u.insert(u.end(), {r, (int32_t)j, blocks[j]});
     u.insert(u.end(), {r, -1, (int32_t)blocks.size()});
@@ -442,7 +449,10 @@ int sync_tables(ltkv_cache *c) {
 // Longest table (blocks) of a live sequence.
 size_t max_table_blocks(const ltkv_cache *c) {
   size_t m = 0;
-  for (const auto &kv : c->rt_row) m = std::max(m, c->seqs.at(kv.first).blocks.size());
+  for (const auto &kv : c->rt_row) {
+    const auto it = c->seqs.find(kv.first);
+    if (it != c->seqs.end()) m = std::max(m, it->second.blocks.size());
+  }
   return m;
 }
 
