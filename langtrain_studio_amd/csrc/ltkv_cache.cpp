@@ -70,6 +70,8 @@ struct AttnPlan {
   uint64_t groups = 0, grouped = 0, shared_blocks = 0;
   bool groups_only = false;  // every query completed by its group: no per-query pass
   size_t n_pass = 0;         // queries of the per-query pass (the rest are completed by groups)
+  size_t max_suffix = 0;     // longest remainder (tokens) of a per-query-pass query
+  bool empty_with_groups = false;  // a query with group partials and no remainder
   size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0, off_qmap = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
   std::vector<int32_t> host;  // the arrays above, in device layout
@@ -731,8 +733,15 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   if ((uint64_t)n * sstride + (uint64_t)groups.size() * gstride > (uint64_t)INT32_MAX / 2)
     return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
   std::vector<int32_t> qmap;  // queries left for the per-query pass
+  size_t max_suffix = 0;
+  bool empty_with_groups = false;
   for (size_t i = 0; i < n; ++i)
-    if (pre_parts[i] >= 0) qmap.push_back((int32_t)i);
+    if (pre_parts[i] >= 0) {
+      qmap.push_back((int32_t)i);
+      const size_t rem = lens[i] > pre_tokens[i] ? lens[i] - pre_tokens[i] : 0;
+      max_suffix = std::max(max_suffix, rem);
+      if (pre_parts[i] > 0 && rem == 0) empty_with_groups = true;
+    }
   const bool groups_only = qmap.empty();
 
   P.n = n;
@@ -747,6 +756,8 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.shared_blocks = shared_blocks;
   P.groups_only = groups_only;
   P.n_pass = qmap.size();
+  P.max_suffix = max_suffix;
+  P.empty_with_groups = empty_with_groups;
   P.off_tables = 0;
   P.off_stables = align8(P.off_tables + groups.size() * gstride);
   P.off_slens = align8(P.off_stables + n * sstride);
@@ -1381,6 +1392,9 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   ltkv::AttnArgs a = attn_args(c, layer, P.n, P.n_heads, P.head_dim, scale, d_q, d_out, ws, part,
                                (int)max_parts);
   a.split = split;
+  // Short remainders in one partition each and no group-only queries: the
+  // decode kernel writes every output itself (folding group partials).
+  a.merge_free = grouped && part > 0 && P.max_suffix <= (size_t)(part / split) && !P.empty_with_groups;
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
   a.max_len = (int64_t)(P.sstride * LTKV_BLOCK);

@@ -91,6 +91,10 @@ struct AttnArgs {
   // Lengths are cut to max_len tokens (at most table_stride * 16); the grid's
   // max_parts covers max_len.
   int64_t max_len;
+  // The caller knows no query needs the merge pass: every query has one
+  // partition, and none with group partials has an empty remainder (the
+  // matrix-core kernel folds group partials of single-partition queries).
+  bool merge_free;
   // Group partials folded into each query's result (planned attention), or
   // pre_parts == nullptr: query i has pre_parts[i] partials at pre_o/pre_ml
   // slot (i * n_heads + head) * max_pre_parts + p; -1: its group wrote the

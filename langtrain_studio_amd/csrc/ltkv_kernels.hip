@@ -763,7 +763,7 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
                   int part_tokens, int split, int max_parts, int64_t max_len,
                   const int32_t *__restrict__ pre_parts, const float *__restrict__ pre_o,
                   const float *__restrict__ pre_ml, int max_pre_parts,
-                  const int32_t *__restrict__ qmap, int64_t n_pairs) {
+                  const int32_t *__restrict__ qmap, int64_t n_pairs, int folded) {
   constexpr int TPP = HD / 4;     // threads per (query, head)
   constexpr int PPW = 256 / TPP;  // pairs per work-group
   const int64_t pair = (int64_t)blockIdx.x * PPW + threadIdx.x / TPP;
@@ -778,10 +778,12 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   const int pt = partition_tokens(len, part_tokens) / split;
   const int npre = pre_parts ? pre_parts[qi] : 0;
   if (npre < 0) return;  // its group wrote the output
-  // With group partials the context kernels wrote partials even for a
-  // single partition (none for an empty remainder).
+  // A single partition wrote its output directly; with group partials too
+  // when the context kernel folds them (`folded`), else it wrote a partial.
+  // An empty remainder (np == 0) leaves the group partials to this kernel.
   const int np = (int)((len + pt - 1) / pt);
-  if (np <= 1 && npre == 0) return;  // a single partition wrote its output directly
+  if (np <= 1 && npre == 0) return;
+  if (np == 1 && folded) return;
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
   const float *pml = npre > 0 ? pre_ml + qh * max_pre_parts * 2 : nullptr;
@@ -811,16 +813,16 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
 // Launch check of the attention kernel, then the partition merge when some
 // query may span several partitions.
 template <int HD>
-hipError_t launch_merge(const AttnArgs &a, hipStream_t s) {
+hipError_t launch_merge(const AttnArgs &a, hipStream_t s, bool folded) {
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || (a.max_parts == 1 && !a.pre_parts)) return e;
+  if (e != hipSuccess || (a.max_parts == 1 && !a.pre_parts) || (folded && a.merge_free)) return e;
   const int64_t pairs = a.n * a.n_heads;
   constexpr int ppw = 256 / (HD / 4);
   const unsigned mgrid = (unsigned)((pairs + ppw - 1) / ppw);
   attn_merge_kernel<HD><<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
                                               a.part_tokens, a.split, a.max_parts, a.max_len,
                                               a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
-                                              a.qmap, pairs);
+                                              a.qmap, pairs, folded ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -1397,7 +1399,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int split, int max_parts, const int32_t *__restrict__ pre_parts,
                  const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
                  const uint16_t *__restrict__ vscale, const int32_t *__restrict__ rows, int64_t n_rows,
-                 int64_t max_len) {
+                 int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
+                 int max_pre_parts) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -1713,8 +1716,41 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   if (hi_lane) {  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
     const int64_t qh = qi * n_heads + (int64_t)kvh0 * G + lr;
-    const bool direct = np == 1 && !(pre_parts && pre_parts[qi] > 0);  // else merged later
-    if (direct) {
+    if (np == 1) {  // one partition: this wave writes the output
+      const int npre = pre_parts ? pre_parts[qi] : 0;
+      if (npre > 0) {
+        // Fold the query's group partials (numerator, reference, sum), as
+        // attn_merge_kernel would, against their common maximum.
+        // Loads are issued four partials at a time (indices clamped to the
+        // last partial, with weight 0 past it) so their latencies overlap.
+        const float *pml = pre_ml + qh * max_pre_parts * 2;
+        float mx = m_ref;
+        for (int p0 = 0; p0 < npre; p0 += 4)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pml[2 * (p0 + u < npre ? p0 + u : npre - 1)]);
+        const float mref = mx == -INFINITY ? 0.f : mx;
+        const float a0 = __builtin_amdgcn_exp2f(m_ref - mref);
+        l_run *= a0;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
+        for (int p0 = 0; p0 < npre; p0 += 4) {
+          f32x4 po[4][DT];
+          float a[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int pc = p0 + u < npre ? p0 + u : npre - 1;
+            const float *src = pre_o + (qh * max_pre_parts + pc) * HD + 4 * lq;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) po[u][dt] = *reinterpret_cast<const f32x4 *>(src + 16 * dt);
+            a[u] = p0 + u < npre ? __builtin_amdgcn_exp2f(pml[2 * pc] - mref) : 0.f;
+            l_run += pml[2 * pc + 1] * a[u];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a[u];
+        }
+      }
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
@@ -1741,8 +1777,8 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
-      a.max_len);
-  return launch_merge<HD>(a, s);
+      a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts);
+  return launch_merge<HD>(a, s, true);
 }
 
 template <typename T, int HD, int G>
@@ -1753,7 +1789,7 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
       a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
-  return launch_merge<HD>(a, s);
+  return launch_merge<HD>(a, s, false);
 }
 
 template <typename T, int HD, int G>
@@ -1764,7 +1800,7 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
       a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
-  return launch_merge<HD>(a, s);
+  return launch_merge<HD>(a, s, false);
 }
 
 // f16 and q8_0 pools take the matrix-core kernel. f32 pools (no f32 MFMA
