@@ -42,6 +42,8 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--partition", type=int, default=0, help="attention partition tokens (0 = default)")
+    p.add_argument("--kv-dtype", default="f16", choices=["f16", "q8_0"],
+                   help="cache element type of the prefill and prefix-cow workloads")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0 = host share, max 16)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -398,7 +400,7 @@ def bench_prefill(args):
     rng = np.random.default_rng(args.seed)
     ctx = rng.integers(512, 8193, n_seq)
     n_blocks = int(sum(-(-int(c + chunk) // BLOCK) for c in ctx) * 1.1) + 16
-    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype=args.kv_dtype, device=0, stream=torch.cuda.current_stream())
     kv.init_free_order(rng.permutation(n_blocks))
     _fill_pool_random(kv, kvd, n_blocks, args.seed)
     kv.append_batch(np.repeat(np.arange(n_seq, dtype=np.uint32), ctx),
@@ -420,9 +422,10 @@ def bench_prefill(args):
     d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
     d_us = _time_op(lambda: kv.decode_attention(0, q, tables, d_lens, n_heads, hd, out=out), reps=reps)
     flops = 4.0 * n_heads * hd * float(lens.sum())
-    kv_bytes = int(sum(int(c) + chunk for c in ctx)) * 2 * kvd * 2  # K and V of each context once
+    eb = 2 if args.kv_dtype == "f16" else 1 + 2 / 32  # bytes per cached element (q8_0: quant + scale share)
+    kv_bytes = int(sum(int(c) + chunk for c in ctx) * 2 * kvd * eb)  # K and V of each context once
     print(json.dumps({
-        "workload": "prefill qwen2.5-7b f16: 8 chunks x 512 tokens, contexts U[512,8192]",
+        "workload": f"prefill qwen2.5-7b {args.kv_dtype}: 8 chunks x 512 tokens, contexts U[512,8192]",
         "attention_us": round(p_us, 2), "TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 1),
         "mfma_frac": round(flops / (p_us * 1e-6) / 1e12 / PEAK_F16_MFMA_TFLOPS, 4),
         "kv_bytes": kv_bytes, "flops": flops,
@@ -487,7 +490,8 @@ def bench_prefix_cow(args):
     rng = np.random.default_rng(args.seed)
     per_seq = -(-(prefix + suffix + steps) // BLOCK) - prefix // BLOCK + 1
     n_blocks = int((prefix // BLOCK + 1 + S * per_seq) * 1.1)
-    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype=args.kv_dtype, device=0, stream=torch.cuda.current_stream())
+    eb = 2 if args.kv_dtype == "f16" else 1 + 2 / 32  # bytes per cached element (q8_0: quant + scale share)
     kv.init_free_order(rng.permutation(n_blocks))
     _fill_pool_random(kv, kvd, n_blocks, args.seed)
     kv.append_batch(np.zeros(prefix, np.uint32), np.arange(prefix, dtype=np.uint64))
@@ -503,7 +507,7 @@ def bench_prefix_cow(args):
     torch.cuda.synchronize()
     assert kv.cow_copies() == S - 1, kv.cow_copies()
     app_us = _time_op(lambda: kv.write_batch(0, d_sm0, kn, kn), reps=10)
-    cow_bytes = (S - 1) * 2 * 2 * BLOCK * kvd * 2
+    cow_bytes = int((S - 1) * 2 * 2 * BLOCK * kvd * eb)
     seqs = np.arange(S, dtype=np.uint32)
     sms, lens = [], []
     for s in range(steps):
@@ -554,10 +558,10 @@ def bench_prefix_cow(args):
     d_pairs = torch.from_numpy(pairs).cuda()
     cow_us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=100, warmup=10)
     uniq_blocks = len(np.unique(tables_h[tables_h >= 0]))
-    uniq = uniq_blocks * BLOCK * kvd * 2 * 2 + 2 * S * n_heads * hd * 4
-    logical = int(np.mean([l.astype(np.int64).sum() for l in lens])) * 2 * kvd * 2
+    uniq = int(uniq_blocks * BLOCK * kvd * eb * 2) + 2 * S * n_heads * hd * 4
+    logical = int(np.mean([l.astype(np.int64).sum() for l in lens]) * 2 * kvd * eb)
     print(json.dumps({
-        "workload": "prefix-cow llama3-8b f16: 256 seqs x 4088 shared + 64 private, 32 decode steps",
+        "workload": f"prefix-cow llama3-8b {args.kv_dtype}: 256 seqs x 4088 shared + 64 private, 32 decode steps",
         "cow_copies": S - 1, "cow_us": round(cow_us, 2), "cow_GBps": round(cow_bytes / (cow_us * 1e-6) / 1e9, 1),
         "suffix_append_us": round(app_us, 2), "attention_us": round(att_us, 2),
         "attention_unique_bytes": uniq, "attention_logical_bytes": logical,

@@ -1411,6 +1411,8 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
     ltkv::MqArgs m{};
     m.k_layer = a.k_layer;
     m.v_layer = a.v_layer;
+    m.k_scale = a.k_scale;
+    m.v_scale = a.v_scale;
     m.q = d_q;
     m.tables = d + P.off_tables;
     m.jobs = reinterpret_cast<const ltkv::MqJob *>(d + P.off_jobs);

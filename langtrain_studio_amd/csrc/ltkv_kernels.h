@@ -162,6 +162,7 @@ struct MqArgs {
   const MqJob *jobs;
   int n_jobs;
   const int32_t *members;
+  const void *k_scale, *v_scale;  // q8_0 scale pools of the layer (nullptr for f16)
   float *pre_o, *pre_ml;  // partial slots, laid out as AttnArgs::pre_o/pre_ml
   float *out;             // outputs of direct jobs
   int n_heads, n_kv_heads, head_dim;

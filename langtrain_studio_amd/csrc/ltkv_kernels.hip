@@ -1879,24 +1879,37 @@ __device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
 
 constexpr int kMqWaves = 4;  // waves per work-group
 
-template <int HD>
-__global__ void __launch_bounds__(64 * kMqWaves, 2)  // two waves per SIMD: at most 256 registers
-mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool,
+// Waves per SIMD the kernel is built for (register budget 512 / waves): two,
+// except q8_0 rows of 128 (X = HD / element bytes = 128), whose scale
+// handling does not fit 256 registers.
+template <int X>
+constexpr int kMqMinWaves = X >= 128 ? 1 : 2;
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(64 * kMqWaves, kMqMinWaves<HD / (int)sizeof(T)>)
+mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
                const float *__restrict__ q, const int32_t *__restrict__ tables,
                const MqJob *__restrict__ jobs, int n_jobs, const int32_t *__restrict__ members,
                float *__restrict__ pre_o, float *__restrict__ pre_ml, float *__restrict__ out,
                int n_heads, int group,
                int64_t n_blocks, int64_t block_stride, int64_t slot_stride, float qscale,
-               int max_pre_parts) {
-  constexpr int KS = HD / 32;                // k steps of the score product
+               int max_pre_parts, const uint16_t *__restrict__ kscale,
+               const uint16_t *__restrict__ vscale) {
+  constexpr bool Q8 = std::is_same_v<T, int8_t>;
+  constexpr int KS = HD / 32;                // k steps of the score product (q8_0: scale groups)
   constexpr int DT = HD / 16;                // 16-wide d tiles of the output
-  constexpr int ROWB = HD * 2 + 16;          // LDS bytes per staged row (pad: no bank conflicts)
-  constexpr int VPR = HD / 8;                // 16-byte vectors per row
+  constexpr int ROWB = HD * 2 + 16;          // LDS bytes per staged row, f16 (pad: no bank conflicts)
+  constexpr int VPR = HD * (int)sizeof(T) / 16;  // 16-byte vectors per pool row
   constexpr int NT = 64 * kMqWaves;     // threads
-  constexpr int NPT = kMqChunk * VPR / NT;   // vectors per thread per chunk, K and V each
-  static_assert(NPT >= 1 && kMqChunk * VPR % NT == 0, "chunk must split over the threads");
+  constexpr int NV = kMqChunk * VPR;         // vectors per chunk, K and V each
+  constexpr int NPT = (NV + NT - 1) / NT;    // vectors per thread per chunk, K and V each
+  static_assert(NV % NT == 0 || NV < NT, "chunk must split over the threads");
   static_assert(64 / VPR <= 16, "a wave's rows of a chunk must lie in one block");
-  __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V]
+  constexpr int NSC = KS * kMqChunk;         // q8_0 scale entries of a chunk, K or V
+  static_assert(!Q8 || 2 * NSC <= NT, "one scale entry per thread");
+  __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V] as f16
+  // q8_0: [stage][K, V][group][token] scales of the staged chunk
+  __shared__ __attribute__((aligned(16))) uint16_t ssm[2][2][Q8 ? NSC : 1];
 
   // The job list is ordered by work-group id (XCD placement is the host's);
   // empty jobs pad it.
@@ -1946,27 +1959,60 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) split_hl(x[ks], qh[rt][ks], ql[rt][ks]);
   }
+  // q8_0 K is staged as 1152 + k (exact in f16): 1152 times the row's sum of
+  // each k step of Q (hi + lo) comes off every score of that step.
+  float qbias[2][KS];
+  if constexpr (Q8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += (float)qh[rt][ks][e] + (float)ql[rt][ks][e];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        qbias[rt][ks] = 1152.f * t;
+      }
+  }
 
   // Staging: token tok's row of this kv head is one contiguous HD-element
-  // run; tokens at or past t1 stage as zeros.
+  // run; tokens at or past t1 stage as zeros. q8_0 rows are converted to f16
+  // on the way into LDS (K biased as above, V exact), with their scales.
   const int32_t *tab = tables + jb.table;
   const int64_t head_off = (int64_t)jb.kvh * HD;
   // Chunks start on block boundaries (t0 % 32 == 0) and a wave's share of a
   // chunk lies in one block, so its table entry is one scalar load. K/V
   // rows go through buffer descriptors whose extent ends at t1: rows past it
   // load as zeros with no branch.
-  const uint32_t row_bytes = (uint32_t)(slot_stride * 2);
-  auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT]) {
+  const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
+  const int64_t sgroups = slot_stride >> 5;         // q8_0 scale groups per pool row
+  const int64_t shead = (int64_t)jb.kvh * (HD / 32);  // first scale group of this kv head
+  auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT], uint32_t &sc) {
+    if constexpr (Q8) {
+      // thread t < 2 NSC: entry t % NSC (group e / 32, token e % 32) of K (t < NSC) or V
+      sc = 0;
+      if ((int)threadIdx.x < 2 * NSC) {
+        const int e = (int)threadIdx.x % NSC, tok = c0 + e % kMqChunk;
+        const int bi = tok >> 4;
+        const int32_t blk = tok < jb.t1 ? tab[bi] : -1;
+        if (blk >= 0 && blk < n_blocks) {
+          const uint16_t *sp = (int)threadIdx.x < NSC ? kscale : vscale;
+          sc = sp[((int64_t)blk * sgroups + shead + e / kMqChunk) * 16 + (tok & 15)];
+        }
+      }
+    }
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       const int idx = threadIdx.x + NT * u;
+      if (NV < NT && idx >= NV) break;  // wave-uniform: NV is a multiple of 64
       const int row = idx / VPR, col = idx - row * VPR;
       const int wrow = __builtin_amdgcn_readfirstlane(row);  // first row of this wave's share
       const int bi = (c0 + wrow) >> 4;
       const int valid = jb.t1 - bi * 16;  // rows of the block inside the range
       int32_t blk = valid > 0 ? tab[bi] : -1;
       if (blk >= n_blocks) blk = -1;
-      const int extent = blk < 0 ? 0 : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * 2;
+      const int extent = blk < 0 ? 0 : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * (int)sizeof(T);
       const int64_t base = (int64_t)(blk < 0 ? 0 : blk) * block_stride + head_off;
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void *)(kpool + base), (short)0, extent, kBufferWord3);
@@ -1977,13 +2023,25 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
       vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
     }
   };
-  auto store_chunk = [&](int st, const u32x4 (&kr)[NPT], const u32x4 (&vr)[NPT]) {
+  auto store_chunk = [&](int st, const u32x4 (&kr)[NPT], const u32x4 (&vr)[NPT], uint32_t sc) {
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       const int idx = threadIdx.x + NT * u;
+      if (NV < NT && idx >= NV) break;
       const int row = idx / VPR, col = idx - row * VPR;
-      *reinterpret_cast<u32x4 *>(&sm[st][0][row * ROWB + col * 16]) = kr[u];
-      *reinterpret_cast<u32x4 *>(&sm[st][1][row * ROWB + col * 16]) = vr[u];
+      if constexpr (Q8) {
+        char *kd = &sm[st][0][row * ROWB + col * 32], *vd = &sm[st][1][row * ROWB + col * 32];
+        *reinterpret_cast<h8 *>(kd) = i8x8_to_h8_biased(u32x2{kr[u].x, kr[u].y});
+        *reinterpret_cast<h8 *>(kd + 16) = i8x8_to_h8_biased(u32x2{kr[u].z, kr[u].w});
+        *reinterpret_cast<h8 *>(vd) = i8x8_to_h8(u32x2{vr[u].x, vr[u].y});
+        *reinterpret_cast<h8 *>(vd + 16) = i8x8_to_h8(u32x2{vr[u].z, vr[u].w});
+      } else {
+        *reinterpret_cast<u32x4 *>(&sm[st][0][row * ROWB + col * 16]) = kr[u];
+        *reinterpret_cast<u32x4 *>(&sm[st][1][row * ROWB + col * 16]) = vr[u];
+      }
+    }
+    if constexpr (Q8) {
+      if ((int)threadIdx.x < 2 * NSC) ssm[st][(int)threadIdx.x / NSC][(int)threadIdx.x % NSC] = (uint16_t)sc;
     }
   };
 
@@ -2021,23 +2079,39 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
         a[tt] = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWB + (32 * ks + 8 * lq) * 2);
+      if constexpr (Q8) {
+        // each k step is one scale group: its product is scaled by the
+        // token's K scale d after the bias comes off, d (sum - bias)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < 2; ++tt) {
+          const h4 d = *reinterpret_cast<const h4 *>(&ssm[st][0][ks * kMqChunk + tt * 16 + 4 * lq]);
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], sc[tt][rt], 0, 0, 0);
+          for (int rt = 0; rt < 2; ++rt) {
+            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], c, 0, 0, 0);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+            for (int i = 0; i < 4; ++i) sc[tt][rt][i] = __builtin_fmaf((float)d[i], c[i] - qbias[rt][ks], sc[tt][rt][i]);
+          }
+        }
+      } else {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-          sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], sc[tt][rt], 0, 0, 0);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
+      }
     }
   };
 
   // Online softmax of one chunk's scores into the P^T operands. This lane
   // holds tokens 4 lq + i and 16 + 4 lq + i of its row; k slot j of P^T is
   // token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4.
-  auto softmax = [&](f32x4 (&sc)[2][2], int c0, h8 (&ph)[2], h8 (&pl)[2]) {
+  auto softmax = [&](f32x4 (&sc)[2][2], int c0, float (&pf)[2][8]) {
     float lmax[2];
     if (c0 + kMqChunk > lim_min) {  // wave-uniform: the chunk crosses a row's limit
 #pragma unroll
@@ -2079,24 +2153,44 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
-      float p[8], ps = 0.f;
+      float ps = 0.f;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[tt * 4 + i] = __builtin_amdgcn_exp2f(sc[tt][rt][i] - mref);
-          ps += p[tt * 4 + i];
+          pf[rt][tt * 4 + i] = __builtin_amdgcn_exp2f(sc[tt][rt][i] - mref);
+          ps += pf[rt][tt * 4 + i];
         }
       l_run[rt] += ps;
-      split_hl(p, ph[rt], pl[rt]);
     }
   };
 
   // O^T += V^T P^T over the V rows of LDS stage st.
-  auto pv = [&](int st, const h8 (&ph)[2], const h8 (&pl)[2]) {
+  auto pv = [&](int st, const float (&pf)[2][8]) {
     const char *vs_base = sm[st][1];
+    h8 ph[2], pl[2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
+      if constexpr (Q8) {
+        if (dt % 2 == 0) {  // a new scale group: P' = P times the token's V scale
+          const int g = dt / 2;
+          const h4 d0 = *reinterpret_cast<const h4 *>(&ssm[st][1][g * kMqChunk + 4 * lq]);
+          const h4 d1 = *reinterpret_cast<const h4 *>(&ssm[st][1][g * kMqChunk + 16 + 4 * lq]);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              x[j] = pf[rt][j] * (float)d0[j];
+              x[4 + j] = pf[rt][4 + j] * (float)d1[j];
+            }
+            split_hl(x, ph[rt], pl[rt]);
+          }
+        }
+      } else if (dt == 0) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) split_hl(pf[rt], ph[rt], pl[rt]);
+      }
       // V^T operand: d = 16 dt + lr, tokens 4 lq + j (j < 4) and 16 + 4 lq + j - 4.
       const int col = (dt * 16 + 4 * (lr & 3)) * 2;
       const u32x2 a0 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (4 * lq + (lr >> 2)) * ROWB + col));
@@ -2115,20 +2209,21 @@ mq_attn_kernel(const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ 
   // while the current one is computed.
   const int nch = (jb.t1 - jb.t0 + kMqChunk - 1) / kMqChunk;
   u32x4 kr[NPT], vr[NPT];
-  load_chunk(jb.t0, kr, vr);
-  store_chunk(0, kr, vr);
+  uint32_t scv = 0;
+  load_chunk(jb.t0, kr, vr, scv);
+  store_chunk(0, kr, vr, scv);
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
     const bool more = c + 1 < nch;
-    if (more) load_chunk(jb.t0 + (c + 1) * kMqChunk, kr, vr);
+    if (more) load_chunk(jb.t0 + (c + 1) * kMqChunk, kr, vr, scv);
     if (active) {
       f32x4 sc[2][2];
       score(c & 1, sc);
-      h8 ph[2], pl[2];
-      softmax(sc, jb.t0 + c * kMqChunk, ph, pl);
-      pv(c & 1, ph, pl);
+      float pf[2][8];
+      softmax(sc, jb.t0 + c * kMqChunk, pf);
+      pv(c & 1, pf);
     }
-    if (more) store_chunk((c + 1) & 1, kr, vr);
+    if (more) store_chunk((c + 1) & 1, kr, vr, scv);
     __syncthreads();
   }
 
@@ -2356,27 +2451,31 @@ int attention_split(int elem, int group, int n_kv_heads) {
 int mq_rows(int) { return 32 * kMqWaves; }
 
 bool mq_supported(int elem, int head_dim, int group) {
-  return elem == 2 && (head_dim == 64 || head_dim == 128) && group >= 1 && group <= mq_rows(head_dim);
+  return (elem == 2 || elem == 1) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
+         group <= mq_rows(head_dim);
 }
 
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s) {
   if (a.n_jobs <= 0) return hipSuccess;
   const unsigned grid = (unsigned)a.n_jobs;
   const int group = a.n_heads / a.n_kv_heads;
-  const auto *k = static_cast<const _Float16 *>(a.k_layer);
-  const auto *v = static_cast<const _Float16 *>(a.v_layer);
   const float qscale = a.scale * kLog2e;
-  if (a.head_dim == 128)
-    mq_attn_kernel<128><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
-                                             a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks,
-                                             g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
-  else if (a.head_dim == 64)
-    mq_attn_kernel<64><<<grid, 64 * kMqWaves, 0, s>>>(k, v, a.q, a.tables, a.jobs, a.n_jobs, a.members,
-                                            a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks,
-                                            g.block_stride, g.slot_stride, qscale, a.max_pre_parts);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const auto *ksc = static_cast<const uint16_t *>(a.k_scale);
+  const auto *vsc = static_cast<const uint16_t *>(a.v_scale);
+  auto run = [&](auto tag, auto hd) {
+    using T = decltype(tag);
+    constexpr int HD = decltype(hd)::value;
+    mq_attn_kernel<T, HD><<<grid, 64 * kMqWaves, 0, s>>>(
+        static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
+        a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
+        g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
+    return hipGetLastError();
+  };
+  if (g.elem == 2 && a.head_dim == 128) return run(_Float16{}, std::integral_constant<int, 128>{});
+  if (g.elem == 2 && a.head_dim == 64) return run(_Float16{}, std::integral_constant<int, 64>{});
+  if (g.elem == 1 && a.head_dim == 128) return run(int8_t{}, std::integral_constant<int, 128>{});
+  if (g.elem == 1 && a.head_dim == 64) return run(int8_t{}, std::integral_constant<int, 64>{});
+  return hipErrorInvalidValue;
 }
 
 }  // namespace ltkv

@@ -164,12 +164,12 @@ def test_f32_pools_plan_without_groups(gpu):
 
 
 # ---------------------------------------------------------------------------- chunked prefill
-def _prefill_state(rng, kv_dim, chunks, decode=()):
+def _prefill_state(rng, kv_dim, chunks, decode=(), dtype="f16"):
     """chunks: (seq, context, chunk_len) -- the sequence holds `context`
     tokens, then appends a chunk of chunk_len tokens (the step's prefill
     chunk, model.rs:380-429); decode: (seq, len) sequences appending one token."""
     need = sum(c + n + 32 for _, c, n in chunks) + sum(n + 32 for _, n in decode) + 64 * BLOCK
-    g, o = _caches(1, kv_dim, need, "f16", rng)
+    g, o = _caches(1, kv_dim, need, dtype, rng)
     both = [("gpu", g), ("oracle", o)]
     for s, ctx, _ in chunks:
         if ctx:
@@ -297,3 +297,47 @@ def test_continuous_batching_churn_matches_oracle(gpu):
         ok, ov = o.pool(0)
         np.testing.assert_array_equal(gk, ok)
         np.testing.assert_array_equal(gv, ov)
+
+
+# ---------------------------------------------------------------------------- q8_0 groups
+@pytest.mark.parametrize("n_kids,prefix", [(70, 2040), (3, 100)])
+def test_q8_prefix_sharing_forks(gpu, n_kids, prefix):
+    """Forks of one prefix on a q8_0 cache: the group kernel stages the int8
+    tiles as f16 with their scales; within the f32 bar of the oracle over the
+    dequantised rows."""
+    rng = np.random.default_rng(n_kids + prefix + 1)
+    kids = [(1 + i, int(rng.integers(1, 71))) for i in range(n_kids)]
+    g, o = _forked(rng, 1024, "q8_0", [(0, prefix, kids)])
+    seqs = [s for s, _ in kids]
+    lens = [g.len(s) for s in seqs]
+    stats, *_ = _run(gpu, g, o, seqs, lens, 32, 128, rng, dtype="q8_0")
+    assert stats["groups"] == 1 and stats["grouped"] == n_kids
+
+
+@pytest.mark.parametrize("head_dim,group", [(128, 1), (128, 4), (128, 8), (64, 4), (64, 8)])
+def test_q8_prefix_groups_shapes(gpu, head_dim, group):
+    """Two groups, roots, unshared sequences, a fork with an empty suffix and
+    an empty read, on q8_0 pools."""
+    rng = np.random.default_rng(head_dim * 10 + group + 1)
+    n_kv = 2
+    kv_dim = n_kv * head_dim
+    spec = [(0, 333, [(1, 5), (2, 0), (3, 40), (4, 16)]),
+            (10, 1200, [(11 + i, int(rng.integers(0, 50))) for i in range(20)])]
+    g, o = _forked(rng, kv_dim, "q8_0", spec, singles=[(50, 700), (51, 3)])
+    seqs = [0, 1, 2, 3, 4, 10] + [11 + i for i in range(20)] + [50, 51, 2]
+    lens = [g.len(s) for s in seqs]
+    lens[-1] = 0
+    stats, *_ = _run(gpu, g, o, seqs, lens, group * n_kv, head_dim, rng, dtype="q8_0")
+    assert stats["groups"] == 2
+
+
+@pytest.mark.parametrize("n_heads,n_kv,head_dim,ctx,chunk", [
+    (28, 4, 128, 1000, 512),
+    (32, 8, 128, 0, 300),
+    (32, 4, 64, 700, 100),
+])
+def test_q8_prefill_chunk_causal(gpu, n_heads, n_kv, head_dim, ctx, chunk):
+    rng = np.random.default_rng(ctx + chunk + head_dim + 1)
+    g, o, seqs, lens = _prefill_state(rng, n_kv * head_dim, [(0, ctx, chunk)], dtype="q8_0")
+    stats, *_ = _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, dtype="q8_0")
+    assert stats["groups"] == 1 and stats["grouped"] == chunk

@@ -243,8 +243,8 @@ def test_q8_attention_ignores_stale_nonfinite_slots(gpu, head_dim):
 
 
 def test_q8_planned_attention_equals_decode(gpu):
-    """The planned path on a q8_0 cache (no shared-prefix groups: the MFMA
-    group kernel reads f16 tiles) gives the decode kernel's bits."""
+    """The planned path on a q8_0 cache: without groups it gives the decode
+    kernel's bits; with the forks grouped it stays within the bar."""
     import torch
 
     rng = np.random.default_rng(31)
@@ -259,7 +259,7 @@ def test_q8_planned_attention_equals_decode(gpu):
     from helpers import append_rows
     append_rows([("gpu", g), ("oracle", o)], seqs, pos, rng, kv_dim)
     lens = [g.len(s) for s in seqs]
-    st = g.plan_attention(seqs, lens, n_heads, head_dim)
+    st = g.plan_attention(seqs, lens, n_heads, head_dim, shared_prefix=False)
     assert st["groups"] == 0
     q = torch.from_numpy(rng.standard_normal((8, n_heads * head_dim), dtype=np.float32)).to(gpu)
     got = g.planned_attention(0, q).cpu().numpy()
@@ -269,6 +269,9 @@ def test_q8_planned_attention_equals_decode(gpu):
     np.testing.assert_array_equal(got, ref)
     want = o.attention_tables(0, tables, la, q.cpu().numpy(), n_heads, head_dim, threads=8)
     attention_close(got, want, "q8_0")
+    st = g.plan_attention(seqs, lens, n_heads, head_dim)
+    assert st["groups"] == 1
+    attention_close(g.planned_attention(0, q).cpu().numpy(), want, "q8_0")
 
 
 def test_q8_unsupported_ops_raise(gpu):
