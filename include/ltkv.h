@@ -216,7 +216,7 @@ LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
  * With LTKV_PLAN_SHARED_PREFIX, queries whose tables begin with the same
  * blocks (sequences forked by ltkv_share) form groups: the query rows of a
  * group attend to its shared full blocks once, together, on the matrix
- * cores (f16 pools; f32 pools ignore the flag), and each query's own
+ * cores (f16 and q8_0 pools; f32 pools ignore the flag), and each query's own
  * remaining blocks as in ltkv_decode_attention; the two are merged by their
  * softmax statistics. Results agree with ltkv_decode_attention within the
  * attention tolerance (and bit for bit without the flag). A grouped query's
