@@ -847,6 +847,34 @@ def _time_decode(w: Llama3Decode, steps: int, warmup: int):
     return total_ms * 1e3 / steps, float(att_ms.mean() * 1e3), float(app_ms.mean() * 1e3), wall
 
 
+def _time_decode_graph(w: Llama3Decode, steps: int) -> float:
+    """The same steps, each captured once as a HIP graph (append + attention
+    with its merge) and replayed back to back: µs per step, HIP events around
+    the replays. Graph launches drop the per-kernel launch gaps an engine
+    that captures its decode loop would not pay."""
+    import torch
+
+    graphs = []
+    for s in range(steps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            w.kv.set_stream(torch.cuda.current_stream())  # the capture stream
+            w.append(s)
+            w.attend(s)
+        graphs.append(g)
+    w.kv.set_stream(torch.cuda.current_stream())
+    for g in graphs[:3]:
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for g in graphs:
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
 def bench_decode_q8(args):
     """The Llama-3-8B decode step on a q8_0 KV cache (int8 quants plus one f16
     scale per 32 elements: 1.06 bytes per element instead of 2)."""
@@ -894,6 +922,7 @@ def main():
     steps, warmup = args.steps, args.warmup
     w = Llama3Decode(max(steps, warmup, 1), args.seed, args.partition)
     us_step, att_us, app_us, wall = _time_decode(w, steps, warmup)
+    graph_us = _time_decode_graph(w, steps)
     att_bytes = float(np.mean([w.attention_bytes(s) for s in range(steps)]))
     att_gbps = att_bytes / (att_us * 1e-6) / 1e9
     app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9
@@ -932,6 +961,7 @@ def main():
         "append_us": round(app_us, 2),
         "append_GBps": round(app_gbps, 1),
         "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4),
+        "graph_step_us": round(graph_us, 2),
         "roofline": {"bound": "hbm", "achieved": round(att_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": _profiled_traffic(),
                      "traffic_source": TRAFFIC_PROFILE,
