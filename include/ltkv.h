@@ -194,6 +194,25 @@ LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t
                           float scale, const float *d_q, const int32_t *d_tables,
                           size_t table_stride, const int32_t *d_lens, float *d_out);
 
+/* A decode step's append and attention in one launch: KvCache::write of
+ * row i of d_k/d_v (f32, row stride src_stride) into cell d_slot_mapping[i]
+ * (kv.rs:123-131), then ltkv_decode_attention over the same tables and
+ * lengths (model.rs:414-475 for one layer). The cell must be position
+ * d_lens[i] - 1 of query i's table (the cell the step's claim returned for
+ * that query) and no two queries may read one sequence's new cells (one new
+ * token per sequence, as in a decode step); then results and pools are
+ * bit-identical to ltkv_write followed by ltkv_decode_attention. A negative
+ * or out-of-range cell is skipped, as by ltkv_write. On f16 pools the
+ * attention kernel writes and uses each new row itself; on f32 and Q8_0
+ * pools this is ltkv_write followed by ltkv_decode_attention. No reference
+ * counterpart: the reference writes then attends per layer. */
+LTKV_API int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                                          size_t head_dim, float scale, const float *d_q,
+                                          const int32_t *d_tables, size_t table_stride,
+                                          const int32_t *d_lens, const int32_t *d_slot_mapping,
+                                          const float *d_k, const float *d_v, size_t src_stride,
+                                          float *d_out);
+
 /* Tokens per context partition of the decode attention split (multiple of
  * 64), or 0 (the default) for the per-query policy: a query is split into
  * four partitions of ceil(len/4) rounded up to 64 tokens (at least 64) up to

@@ -47,6 +47,8 @@ SIGNATURES = {
     "ltkv_copy_blocks": (_int, [_vp, _sz, _vp]),
     "ltkv_gather": (_int, [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp]),
     "ltkv_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp]),
+    "ltkv_append_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp, _vp, _vp,
+                                            _sz, _vp]),
     "ltkv_set_attention_partition": (_int, [_vp, _sz]),
     "ltkv_plan_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _u32]),
     "ltkv_planned_attention": (_int, [_vp, _sz, _f32, _vp, _vp]),

@@ -1200,7 +1200,9 @@ namespace {
 int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                      float scale, const float *d_q, const int32_t *d_tables, size_t table_stride,
                      const int32_t *d_rows, size_t n_rows, size_t max_len, const int32_t *d_lens,
-                     float *d_out, size_t group) {
+                     float *d_out, size_t group, const int32_t *d_new_slots = nullptr,
+                     const float *d_new_k = nullptr, const float *d_new_v = nullptr,
+                     size_t new_stride = 0) {
   // A query's partition size depends on its own length only (or is fixed by
   // ltkv_set_attention_partition), so its result is bit-identical whatever
   // else is in the batch (the reference's property, engine/README.md:102).
@@ -1223,6 +1225,10 @@ int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size
   a.n_rows = (int64_t)n_rows;
   a.max_len = (int64_t)max_len;
   a.lens = d_lens;
+  a.new_slots = d_new_slots;
+  a.new_k = d_new_k;
+  a.new_v = d_new_v;
+  a.new_stride = (int64_t)new_stride;
   HIP_TRY(ltkv::launch_decode_attention(head_geom(c, head_dim), a, c->stream),
           "decode attention launch");
   return LTKV_OK;
@@ -1246,6 +1252,36 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride, nullptr,
                           0, table_stride * LTKV_BLOCK, d_lens, d_out, group);
+}
+
+int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                                 size_t head_dim, float scale, const float *d_q,
+                                 const int32_t *d_tables, size_t table_stride, const int32_t *d_lens,
+                                 const int32_t *d_slot_mapping, const float *d_k, const float *d_v,
+                                 size_t src_stride, float *d_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  size_t group = 0;
+  if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
+  if (n == 0) return LTKV_OK;
+  if (table_stride == 0) return fail(LTKV_ERR_ARG, "table_stride must be > 0");
+  if (!d_q || !d_tables || !d_lens || !d_out || !d_slot_mapping || !d_k || !d_v)
+    return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
+  if (src_stride < c->kv_dim || src_stride % 4 != 0)
+    return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
+  if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0) return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
+  if (c->elem != 2) {  // fused only on f16 pools: append, then attention, as two launches
+    if (int rc = ltkv_write(c, layer, n, d_slot_mapping, d_k, d_v, src_stride)) return rc;
+    return ltkv_decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride,
+                                 d_lens, d_out);
+  }
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride, nullptr,
+                          0, table_stride * LTKV_BLOCK, d_lens, d_out, group, d_slot_mapping, d_k, d_v,
+                          src_stride);
 }
 
 int ltkv_decode_attention_rows(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,

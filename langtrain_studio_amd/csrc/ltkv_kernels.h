@@ -95,6 +95,13 @@ struct AttnArgs {
   // partition, and none with group partials has an empty remainder (the
   // matrix-core kernel folds group partials of single-partition queries).
   bool merge_free;
+  // Fused append (f16 pools, matrix-core kernel): query i's new K/V row
+  // (new_k/new_v row i, f32, row stride new_stride) is written to cell
+  // new_slots[i], which must be position lens[i] - 1 of the query's table,
+  // and attended from registers. nullptr: no fused append.
+  const int32_t *new_slots;
+  const float *new_k, *new_v;
+  int64_t new_stride;
   // Group partials folded into each query's result (planned attention), or
   // pre_parts == nullptr: query i has pre_parts[i] partials at pre_o/pre_ml
   // slot (i * n_heads + head) * max_pre_parts + p; -1: its group wrote the

@@ -1400,7 +1400,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  const int32_t *__restrict__ qmap, const uint16_t *__restrict__ kscale,
                  const uint16_t *__restrict__ vscale, const int32_t *__restrict__ rows, int64_t n_rows,
                  int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
-                 int max_pre_parts) {
+                 int max_pre_parts, const int32_t *__restrict__ new_slots,
+                 const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
+                 T *kdst, T *vdst) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -1513,6 +1515,34 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
 
+  // Fused append (f16, decode steps): the wave of the query's last partition
+  // writes the query's new K/V row (position len - 1, cell new_slots[qi]) of
+  // its heads, rounded to f16 as write_kernel does, and uses those registers
+  // for that row of the last tile instead of loading it. The lanes that hold
+  // row r_new of the tile (load index r_new / RPI) own the row's pieces.
+  int b_new = -1, r_new = 0;
+  u32x4 nk = {0u, 0u, 0u, 0u}, nv = {0u, 0u, 0u, 0u};
+  if constexpr (!Q8) {
+    if (new_slots && part == np - 1 && len > 0) {  // uniform
+      const int32_t cell = new_slots[qi];
+      if (cell >= 0 && (int64_t)cell < n_blocks * 16) {
+        b_new = (int)((len - 1) >> 4);
+        r_new = (int)((len - 1) & 15);
+        if (prow == r_new % RPI) {
+          const float *ksrc = new_k + qi * new_stride + (int64_t)kvh0 * head_stride + 8 * piece;
+          const float *vsrc = new_v + qi * new_stride + (int64_t)kvh0 * head_stride + 8 * piece;
+          const f32x4 k0 = *reinterpret_cast<const f32x4 *>(ksrc), k1 = *reinterpret_cast<const f32x4 *>(ksrc + 4);
+          const f32x4 v0 = *reinterpret_cast<const f32x4 *>(vsrc), v1 = *reinterpret_cast<const f32x4 *>(vsrc + 4);
+          nk = u32x4{pack_f16x2(k0.x, k0.y), pack_f16x2(k0.z, k0.w), pack_f16x2(k1.x, k1.y), pack_f16x2(k1.z, k1.w)};
+          nv = u32x4{pack_f16x2(v0.x, v0.y), pack_f16x2(v0.z, v0.w), pack_f16x2(v1.x, v1.y), pack_f16x2(v1.z, v1.w)};
+          const int64_t dst = (int64_t)cell * slot_stride + (int64_t)kvh0 * head_stride + 8 * piece;
+          *reinterpret_cast<u32x4 *>(kdst + dst) = nk;
+          *reinterpret_cast<u32x4 *>(vdst + dst) = nv;
+        }
+      }
+    }
+  }
+
   struct Stage {
     u32x4 k[NLD], v[NLD];
     SV ks, vs;  // q8_0: scale entries sidx (.. sidx + 1) of K and of V
@@ -1527,7 +1557,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
     const int valid = b < b1 ? (int)(tok1 - (int64_t)b * 16) : 0;
     const int rows = valid < 16 ? valid : 16;
-    const int extent = rows > 0 ? (rows - 1) * (int)row_bytes + NH * RB : 0;
+    // the fused new row (the tile's last valid row) is not loaded
+    const int lrows = b == b_new ? r_new : rows;
+    const int extent = lrows > 0 ? (lrows - 1) * (int)row_bytes + NH * RB : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(kbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -1570,6 +1602,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         *reinterpret_cast<h8 *>(sv[ph] + r * VPITCH + pc * 32 + 16) = i8x8_to_h8(u32x2{st.v[i].z, st.v[i].w});
       } else {
         *reinterpret_cast<u32x4 *>(sv[ph] + r * VPITCH + pc * 16) = st.v[i];
+      }
+    }
+    if constexpr (!Q8) {
+      // The fused new row (loaded as zeros: outside the tile's extent) is
+      // overwritten from registers by the lanes that own it.
+      if (b == b_new && prow == r_new % RPI) {
+        *reinterpret_cast<u32x4 *>(sk[ph] + r_new * KPITCH + pc * 16) = nk;
+        *reinterpret_cast<u32x4 *>(sv[ph] + r_new * VPITCH + pc * 16) = nv;
       }
     }
     if constexpr (Q8) {
@@ -1777,7 +1817,8 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
-      a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts);
+      a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts, a.new_slots, a.new_k, a.new_v, a.new_stride,
+      static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)));
   return launch_merge<HD>(a, s, true);
 }
 

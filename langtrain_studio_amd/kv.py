@@ -368,6 +368,36 @@ class KvCache:
         _check(self._lib.ltkv_table_uploads(self._h, C.byref(v)))
         return int(v.value)
 
+    def append_decode_attention(self, layer: int, slot_mapping, k, v, q, tables, lens, n_heads: int,
+                                head_dim: int, scale: Optional[float] = None, out=None):
+        """write_batch(layer, slot_mapping, k, v) then decode_attention in one
+        launch (f16 pools): slot_mapping[i] must be position lens[i] - 1 of
+        query i's table, one new token per sequence."""
+        import torch
+
+        n = lens.numel()
+        if q.dim() != 2 or q.shape != (n, n_heads * head_dim):
+            raise ValueError("q must be [n][n_heads*head_dim]")
+        if tables.dim() != 2 or tables.shape[0] != n:
+            raise ValueError("tables must be [n][stride]")
+        if k.shape != (n, self.kv_dim) or v.shape != k.shape or slot_mapping.numel() != n:
+            raise ValueError("k, v must be [n][kv_dim] and slot_mapping [n]")
+        if out is None:
+            out = torch.empty_like(q)
+        elif out.shape != q.shape:
+            raise ValueError("out must match q")
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)  # model.rs:402
+        _check(self._lib.ltkv_append_decode_attention(
+            self._h, layer, n, n_heads, head_dim, float(scale),
+            _dev_ptr(q, torch.float32, "q", self.device),
+            _dev_ptr(tables, torch.int32, "tables", self.device), tables.shape[1],
+            _dev_ptr(lens, torch.int32, "lens", self.device),
+            _dev_ptr(slot_mapping, torch.int32, "slot_mapping", self.device),
+            _dev_ptr(k, torch.float32, "k", self.device), _dev_ptr(v, torch.float32, "v", self.device),
+            k.stride(0), _dev_ptr(out, torch.float32, "out", self.device)))
+        return out
+
     def plan_attention(self, seqs: Sequence[int], lens: Sequence[int], n_heads: int, head_dim: int,
                        shared_prefix: bool = True) -> dict:
         """Step descriptor for planned_attention: query i reads positions
