@@ -42,6 +42,7 @@ class StepPlan:
     slot_mapping_host: np.ndarray
     rows: "object" = None   # torch.int32 [n], the token's resident table row ("resident")
     planned: bool = False   # the cache holds this step's attention plan ("planned")
+    decode_only: bool = False  # one token per sequence: write and attention fuse into one launch
 
 DESCRIPTORS = ("tables", "resident", "planned")
 
@@ -104,6 +105,7 @@ class PagedKvBackend:
         if self.descriptor == "tables":
             stride = max(1, int(math.ceil(lens.max() / BLOCK))) if len(batch) else 1
             plan.tables = torch.from_numpy(self.kv.block_tables(seqs, stride)).to(dev)
+            plan.decode_only = len(batch) > 0 and np.unique(seqs).size == len(batch)
         elif self.descriptor == "resident":
             plan.rows = torch.from_numpy(self.kv.seq_rows(seqs)).to(dev)
         else:
@@ -115,6 +117,9 @@ class PagedKvBackend:
         """model.rs:414-475 for one layer: write k, v ([n][kv_dim] f32, RoPE
         already applied) into the claimed cells, then attention of q
         ([n][n_heads*head_dim] f32) over each token's sequence."""
+        if plan.decode_only:  # ltkv_append_decode_attention: bit-identical to write + attention
+            return self.kv.append_decode_attention(layer, plan.slot_mapping, k, v, q, plan.tables, plan.lens,
+                                                   self.n_heads, self.head_dim, self.scale, out=out)
         self.kv.write_batch(layer, plan.slot_mapping, k, v)
         if plan.planned:
             return self.kv.planned_attention(layer, q, self.scale, out=out)
