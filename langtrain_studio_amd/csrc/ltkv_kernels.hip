@@ -786,6 +786,35 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   if (np == 1 && folded) return;
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
+  if (npre == 0 && np <= 4) {
+    // The common case (a query of up to four partitions): every load is
+    // issued up front (indices clamped, weight 0 past np), one round trip.
+    float m4[4], l4[4];
+    f32x4 o4[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int pc = p < np ? p : np - 1;
+      m4[p] = ml[2 * pc];
+      l4[p] = ml[2 * pc + 1];
+      o4[p] = *reinterpret_cast<const f32x4 *>(part_o + (qh * max_parts + pc) * HD + d);
+    }
+    float mx = m4[0];
+#pragma unroll
+    for (int p = 1; p < 4; ++p) mx = __builtin_fmaxf(mx, m4[p]);  // clamped copies change nothing
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float a = p < np ? __builtin_amdgcn_exp2f(m4[p] - mref) : 0.f;
+      lsum += l4[p] * a;
+      o += o4[p] * a;
+    }
+    f32x4 r = {0.f, 0.f, 0.f, 0.f};
+    if (lsum > 0.f) r = f32x4{o.x / lsum, o.y / lsum, o.z / lsum, o.w / lsum};
+    *reinterpret_cast<f32x4 *>(out + qh * HD + d) = r;
+    return;
+  }
   const float *pml = npre > 0 ? pre_ml + qh * max_pre_parts * 2 : nullptr;
   float mx = -INFINITY;
   for (int p = 0; p < np; ++p) mx = __builtin_fmaxf(mx, ml[2 * p]);
