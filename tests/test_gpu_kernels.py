@@ -273,7 +273,8 @@ def test_attention_shapes(gpu, dtype, head_dim, group):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("group,n_kv", [(2, 2), (3, 4), (2, 3), (4, 5), (1, 1)])
+@pytest.mark.parametrize("group,n_kv", [(2, 2), (3, 4), (2, 3), (4, 5), (1, 1), (5, 4), (6, 2),
+                                         (7, 4), (7, 3), (8, 2)])
 def test_attention_head_pairs_f16(gpu, head_dim, group, n_kv):
     """f16 waves read two adjacent kv heads when the group has at most 4
     query heads and the kv heads pair up (even count), one otherwise."""

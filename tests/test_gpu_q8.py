@@ -202,10 +202,10 @@ def test_q8_attention_shapes(gpu, head_dim, group):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("group,n_kv", [(2, 2), (3, 4), (2, 3), (4, 5)])
+@pytest.mark.parametrize("group,n_kv", [(2, 2), (3, 4), (2, 3), (4, 5), (6, 2), (7, 4), (7, 3)])
 def test_q8_attention_head_pairs(gpu, head_dim, group, n_kv):
     """q8_0 waves over two adjacent kv heads (even count, group at most 4)
-    and over one (odd count)."""
+    and over one (odd count or larger group)."""
     lens = [1, 16, 33, 300, 1031, 2100]
     out, want = _q8_attention(gpu, head_dim, group, n_kv, lens, 0, seed=group * 7 + n_kv)
     attention_close(out, want, "q8_0")
