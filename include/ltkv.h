@@ -311,7 +311,9 @@ LTKV_API int ltkv_table_uploads(const ltkv_cache *c, uint64_t *entries);
  * ltkv_resident_tables reports) to host, after pending uploads. */
 LTKV_API int ltkv_read_resident_tables(ltkv_cache *c, int32_t *h_tables, int32_t *h_lengths);
 
-/* Copy one layer's raw K and V pools ([n_blocks][16][kv_dim]) to host. */
+/* Copy one layer's K and V pools ([n_blocks][16][kv_dim]) to host: f16 bits,
+ * f32, or Q8_0 int8 quants (stored on the device offset by 128, one byte
+ * q + 128 each; this copy gives back q). */
 LTKV_API int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v);
 
 /* Copy one layer's K and V scale pools ([n_blocks][kv_dim/32][16] f16 bits)

@@ -887,8 +887,9 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
   if (bytes > 0) {
     if ((e = hipMalloc(&c->k, bytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(K pool)");
     else if ((e = hipMalloc(&c->v, bytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(V pool)");
-    else if ((e = hipMemset(c->k, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K pool)");
-    else if ((e = hipMemset(c->v, 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
+    // zero cells; q8_0 quants are stored offset by 128, so a zero quant is 0x80
+    else if ((e = hipMemset(c->k, c->q8() ? 0x80 : 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K pool)");
+    else if ((e = hipMemset(c->v, c->q8() ? 0x80 : 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
   }
   const size_t sbytes = c->q8() ? n_layers * c->layer_scales() * 2 : 0;
   if (rc == LTKV_OK && sbytes > 0) {
@@ -1504,6 +1505,10 @@ int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v) {
   HIP_TRY(hipMemcpyAsync(h_k, c->k_layer(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read K pool");
   HIP_TRY(hipMemcpyAsync(h_v, c->v_layer(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read V pool");
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  if (c->q8()) {  // stored bytes q + 128 back to int8 quants
+    for (uint8_t *p : {static_cast<uint8_t *>(h_k), static_cast<uint8_t *>(h_v)})
+      for (size_t i = 0; i < bytes; ++i) p[i] ^= 0x80;
+  }
   return LTKV_OK;
 }
 

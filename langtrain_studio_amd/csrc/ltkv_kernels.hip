@@ -130,7 +130,8 @@ __device__ __forceinline__ float dpp(float x) {
 // lanes with quad_perm DPP (max is order-free); d = amax / 127, id = 1/d (0
 // when d is 0), q = roundf(x * id) (half away from zero) saturated to int8
 // with NaN -> 0 (Rust's `as i8`); every lane stores its 8 quants, lane 0 d
-// as f16.
+// as f16. Quants are stored offset by 128 (byte q + 128, so int8 -128..127
+// is 0..255): the readers turn a byte into an f16 without a sign fix-up.
 __device__ __forceinline__ void quantize_store4(const float (&x)[8], int j, int8_t *__restrict__ dq,
                                                 uint16_t *__restrict__ ds) {
   float amax = 0.f;
@@ -146,7 +147,7 @@ __device__ __forceinline__ void quantize_store4(const float (&x)[8], int j, int8
     const float r = __builtin_roundf(x[i] * id);  // half away from zero
     int qv = 0;
     if (r == r) qv = r > 127.f ? 127 : (r < -128.f ? -128 : (int)r);
-    w[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+    w[i >> 2] |= (uint32_t)((qv + 128) & 0xff) << (8 * (i & 3));
   }
   *reinterpret_cast<u32x2 *>(dq + 8 * j) = u32x2{w[0], w[1]};
   if (j == 0) *ds = (uint16_t)f16_bits(d);
@@ -1382,13 +1383,13 @@ struct BufVec<4> {
   }
 };
 
-// int8 x 8 -> f16 x 8, exact: each byte, biased to u = x + 128 in [0, 255],
-// becomes the mantissa of an f16 in [1024, 2048) (bits 0x6400 | u, value
+// Stored quants x 8 (bytes u = x + 128) -> f16 x 8 of x, exact: each byte
+// becomes the mantissa of an f16 in [1024, 1280) (bits 0x6400 | u, value
 // 1024 + u), and 1152 is subtracted: two v_perm_b32 and two packed f16
 // subtractions per four elements.
 __device__ __forceinline__ h8 i8x8_to_h8(const u32x2 &w) {
   constexpr uint32_t kHi = 0x64646464u;
-  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
+  const uint32_t a = w.x, b = w.y;
   const h2 bias = {(_Float16)1152.f, (_Float16)1152.f};
   const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04010400u)) - bias;
   const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kHi, a, 0x04030402u)) - bias;
@@ -1407,12 +1408,12 @@ __device__ __forceinline__ _Float16 weight_part(float x, bool lo_lane) {
   return lo_lane ? l : h;
 }
 
-// int8 x 8 -> f16 x 8 of 1152 + x (exact; the bias is taken out after the
-// product, where it costs one subtraction per score instead of one per
-// element).
+// Stored quants x 8 -> f16 x 8 of 1152 + x (exact; the bias is taken out
+// after the product, where it costs one subtraction per score instead of
+// one per element).
 __device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
   constexpr uint32_t kHi = 0x64646464u;
-  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
+  const uint32_t a = w.x, b = w.y;
   const u32x4 r = {__builtin_amdgcn_perm(kHi, a, 0x04010400u), __builtin_amdgcn_perm(kHi, a, 0x04030402u),
                    __builtin_amdgcn_perm(kHi, b, 0x04010400u), __builtin_amdgcn_perm(kHi, b, 0x04030402u)};
   return __builtin_bit_cast(h8, r);
