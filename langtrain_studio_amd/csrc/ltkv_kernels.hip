@@ -1789,36 +1789,42 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     if (np == 1) {  // one partition: this wave writes the output
       const int npre = pre_parts ? pre_parts[qi] : 0;
       if (npre > 0) {
-        // Fold the query's group partials (numerator, reference, sum), as
-        // attn_merge_kernel would, against their common maximum.
-        // Loads are issued four partials at a time (indices clamped to the
-        // last partial, with weight 0 past it) so their latencies overlap.
+        // Fold the query's group partials (numerator, reference, sum) into
+        // the wave's own, four partials per round (indices clamped to the
+        // last partial, with weight 0 past it): one round of loads brings
+        // their references, sums and numerators together, and the running
+        // reference is raised to the round's maximum as it goes (the
+        // accumulators rescaled), so no separate pass finds the maximum.
         const float *pml = pre_ml + qh * max_pre_parts * 2;
-        float mx = m_ref;
-        for (int p0 = 0; p0 < npre; p0 += 4)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pml[2 * (p0 + u < npre ? p0 + u : npre - 1)]);
-        const float mref = mx == -INFINITY ? 0.f : mx;
-        const float a0 = __builtin_amdgcn_exp2f(m_ref - mref);
-        l_run *= a0;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
+        float mref = m_ref;
         for (int p0 = 0; p0 < npre; p0 += 4) {
           f32x4 po[4][DT];
-          float a[4];
+          float pm[4], pl[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int pc = p0 + u < npre ? p0 + u : npre - 1;
             const float *src = pre_o + (qh * max_pre_parts + pc) * HD + 4 * lq;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) po[u][dt] = *reinterpret_cast<const f32x4 *>(src + 16 * dt);
-            a[u] = p0 + u < npre ? __builtin_amdgcn_exp2f(pml[2 * pc] - mref) : 0.f;
-            l_run += pml[2 * pc + 1] * a[u];
+            pm[u] = pml[2 * pc];
+            pl[u] = pml[2 * pc + 1];
           }
+          float mx = mref;
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pm[u]);  // clamped: a repeat, harmless
+          const float nref = mx == -INFINITY ? 0.f : mx;
+          const float a0 = __builtin_amdgcn_exp2f(mref - nref);
+          l_run *= a0;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a[u];
+          for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
+          mref = nref;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float a = p0 + u < npre ? __builtin_amdgcn_exp2f(pm[u] - mref) : 0.f;
+            l_run += pl[u] * a;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a;
+          }
         }
       }
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
