@@ -99,8 +99,12 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
     vo.y = pack_f16x2(v0.z, v0.w);
     vo.z = pack_f16x2(v1.x, v1.y);
     vo.w = pack_f16x2(v1.z, v1.w);
-    *reinterpret_cast<u32x4 *>(kpool + dst * 2) = ko;
-    *reinterpret_cast<u32x4 *>(vpool + dst * 2) = vo;
+    // non-temporal: the cells are not read again before they leave the
+    // caches, and the attention after the append keeps its cache lines
+    // (continuous-batching step of 4216 tokens: append 4%, attention 2%
+    // faster; bulk appends unchanged)
+    __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kpool + dst * 2));
+    __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vpool + dst * 2));
   } else {
     f32x4 *kd = reinterpret_cast<f32x4 *>(kpool + dst * 4);
     f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
