@@ -163,3 +163,114 @@ def test_prefix_sharing_full_size(gpu):
     o = _oracle_with_pool(kv, n_blocks)
     want = o.attention_tables(0, tables, lens, q.cpu().numpy(), N_HEADS, HD, threads=16)
     attention_close(out, want, "f16")
+
+
+def test_qwen_mixed_step_full_size(gpu):
+    """The continuous-batching mixed step at its own size (Qwen2.5-7B layer:
+    28 q heads / 4 kv heads / head_dim 128, f16): 120 decode sequences with
+    contexts U[512, 8192] and 8 prefill streams over a permuted pool; one churn
+    round (finished sequences release their blocks, kv.rs:76-81, and arrivals
+    allocate from the fragmented pool); then the step model.rs:380-475 runs on
+    8 chunks of 512 tokens plus one token per decode sequence (4216 tokens),
+    driven as scheduler.rs:389-407 batches them:
+    * the claim gives the oracle's slot mapping and tables, and the fused RoPE
+      append gives the oracle's pool and rotated Q, bit for bit;
+    * decode attention of the 120 decode queries (the per-query kernel: G = 7,
+      up to 9 partitions of 1024 tokens), per-query attention over all 4216
+      tokens, and the planned step (each chunk a causal group) all match the
+      oracle within the f16 tolerance;
+    * the planned step's decode rows equal the per-query kernel's bit for bit."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+    from oracle import OracleKv
+
+    n_heads, n_kv, hd = 28, 4, 128
+    kvd = n_kv * hd
+    n_dec, n_pre, chunk = 120, 8, 512
+    rng = np.random.default_rng(4004)
+    n_blocks = int((n_dec + n_pre) * 8192 // BLOCK * 1.1)
+    g = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    o = OracleKv(1, kvd, n_blocks * BLOCK, dtype="f16")
+    order = rng.permutation(n_blocks)
+    g.init_free_order(order)
+    o.init_free_order(order)
+    history = []  # (slot mapping) of every claim, written with random rows below
+
+    def claim(seqs, pos):
+        seqs, pos = np.asarray(seqs, np.uint32), np.asarray(pos, np.uint64)
+        sm = g.append_batch(seqs, pos)
+        np.testing.assert_array_equal(sm, o.append_batch(seqs, pos))
+        return sm
+
+    def new_seq(sid, ctx):
+        if ctx:
+            history.append(claim(np.full(ctx, sid), np.arange(ctx)))
+
+    dec = list(range(n_dec))
+    for sid in dec:
+        new_seq(sid, int(rng.integers(512, 8193)))
+    # prefill streams: a prompt of U[512, 8192] tokens, some 512-token chunks done
+    pre = []
+    for i in range(n_pre):
+        sid, target = 1000 + i, int(rng.integers(512, 8193))
+        new_seq(sid, chunk * int(rng.integers(0, (target - chunk) // chunk + 1)))
+        pre.append(sid)
+    # churn: finished decode sequences free their blocks, arrivals take them
+    finished = np.flatnonzero(rng.random(n_dec) < 0.05)
+    assert finished.size >= 3
+    for j, i in enumerate(finished):
+        g.truncate(dec[i], 0)
+        o.truncate(dec[i], 0)
+        dec[i] = 2000 + j
+        new_seq(dec[i], int(rng.integers(512, 8193)))
+    assert g.free_blocks() == o.free_blocks()
+    for sid in dec + pre:
+        np.testing.assert_array_equal(g.block_table(sid), o.block_table(sid))
+    for i, sm in enumerate(history):
+        _write_random(g, sm, 100 + i)
+    o.load_pool(0, *g.read_pool(0))
+
+    # the mixed step: 8 chunks of 512 tokens, then one token per decode sequence
+    seqs, pos = [], []
+    for sid in pre:
+        start = g.len(sid)
+        seqs += [sid] * chunk
+        pos += list(range(start, start + chunk))
+    for sid in dec:
+        seqs.append(sid)
+        pos.append(g.len(sid))
+    n = len(seqs)
+    assert n == n_pre * chunk + n_dec
+    sm = claim(seqs, pos)
+    g.rope_init(1e6, hd, hd, True, 8192 + chunk + 1)
+    k = rng.standard_normal((n, kvd), dtype=np.float32)
+    v = rng.standard_normal((n, kvd), dtype=np.float32)
+    q = rng.standard_normal((n, n_heads * hd), dtype=np.float32)
+    pos32 = np.array(pos, np.int32)
+    dq = torch.from_numpy(q.copy()).cuda()
+    g.write_rope(0, torch.from_numpy(sm).cuda(), torch.from_numpy(pos32).cuda(), torch.from_numpy(k).cuda(),
+                 torch.from_numpy(v).cuda(), q=dq, n_heads=n_heads)
+    o.write_rope_batch(0, sm, pos32, k, v, 1e6, hd, hd, True, q=q, n_heads=n_heads)
+    np.testing.assert_array_equal(dq.cpu().numpy().view(np.uint32), q.view(np.uint32))
+    gk, gv = g.read_pool(0)
+    ok, ov = o.pool(0)
+    np.testing.assert_array_equal(gk, ok)
+    np.testing.assert_array_equal(gv, ov)
+    del gk, gv, ok, ov
+
+    lens = pos32 + 1
+    tables, la = g.block_tables(np.array(seqs, np.uint32)), lens.astype(np.int32)
+    want = o.attention_tables(0, tables, la, q, n_heads, hd, threads=16)
+    d_tables, d_lens = torch.from_numpy(tables).cuda(), torch.from_numpy(la).cuda()
+    dsel = slice(n_pre * chunk, n)
+    dec_out = g.decode_attention(0, dq[dsel].contiguous(), d_tables[dsel].contiguous(), d_lens[dsel].contiguous(),
+                                 n_heads, hd).cpu().numpy()
+    assert int(la[dsel].max()) > 7168  # the longest decode queries span 8+ partitions
+    attention_close(dec_out, want[dsel], "f16")
+    attention_close(g.decode_attention(0, dq, d_tables, d_lens, n_heads, hd).cpu().numpy(), want, "f16")
+    stats = g.plan_attention(np.array(seqs, np.uint32), la, n_heads, hd)
+    assert stats["groups"] == n_pre and stats["grouped"] == n_pre * chunk
+    planned = g.planned_attention(0, dq).cpu().numpy()
+    attention_close(planned, want, "f16")
+    np.testing.assert_array_equal(planned[dsel].view(np.uint32), dec_out.view(np.uint32))
