@@ -194,6 +194,30 @@ LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t
                           float scale, const float *d_q, const int32_t *d_tables,
                           size_t table_stride, const int32_t *d_lens, float *d_out);
 
+/* Bytes of the per-device static scratch of ltkv_decode_attention_noalloc. */
+#define LTKV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* ltkv_decode_attention that allocates nothing: same arguments, same
+ * kernels, same results bit for bit, but the partition partials go to a
+ * static device array of LTKV_NOALLOC_SCRATCH_BYTES on each device (held
+ * until the process ends) instead of the cache's workspace, which
+ * ltkv_decode_attention grows with hipMalloc on demand. A launch whose
+ * partials need more fails with LTKV_ERR_ARG before anything is enqueued:
+ * they take n * n_heads * P * (head_dim + 2) * 4 bytes, P counted for the
+ * longest context the tables hold (T = table_stride * 16 tokens): 4 up to
+ * 4096 tokens, ceil(T / 1024) beyond (or ceil(T / the size fixed with
+ * ltkv_set_attention_partition)), doubled on Q8_0 pools whose kv heads
+ * pair up with at most 4 query heads each. Every
+ * call on a device shares that device's scratch: calls that overlap on one
+ * device (other streams, other threads, caches on the same device) race.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+LTKV_API int ltkv_decode_attention_noalloc(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                                           size_t head_dim, float scale, const float *d_q,
+                                           const int32_t *d_tables, size_t table_stride,
+                                           const int32_t *d_lens, float *d_out);
+
 /* A decode step's append and attention in one launch: KvCache::write of
  * row i of d_k/d_v (f32, row stride src_stride) into cell d_slot_mapping[i]
  * (kv.rs:123-131), then ltkv_decode_attention over the same tables and

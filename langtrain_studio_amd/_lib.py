@@ -15,6 +15,7 @@ OK, ERR_FULL, ERR_NONCONTIG, ERR_RANGE, ERR_HIP, ERR_ARG = 0, 1, 2, 3, 4, 5
 F16, F32, Q8_0 = 0, 1, 2
 NO_DEVICE = -1
 BLOCK = 16
+NOALLOC_SCRATCH_BYTES = 32 << 20  # LTKV_NOALLOC_SCRATCH_BYTES
 
 _sz, _u32, _i32, _u64, _vp, _int, _f32 = (C.c_size_t, C.c_uint32, C.c_int32, C.c_uint64, C.c_void_p,
                                           C.c_int, C.c_float)
@@ -47,6 +48,7 @@ SIGNATURES = {
     "ltkv_copy_blocks": (_int, [_vp, _sz, _vp]),
     "ltkv_gather": (_int, [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp]),
     "ltkv_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp]),
+    "ltkv_decode_attention_noalloc": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp]),
     "ltkv_append_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp, _vp, _vp,
                                             _sz, _vp]),
     "ltkv_set_attention_partition": (_int, [_vp, _sz]),

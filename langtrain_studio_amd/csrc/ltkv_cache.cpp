@@ -22,18 +22,20 @@
 #include "../../include/ltkv.h"
 #include "ltkv_kernels.h"
 
+static_assert(LTKV_NOALLOC_SCRATCH_BYTES == ltkv::kScratchBytes, "scratch size of ltkv.h and the kernels");
+
 namespace {
 
-thread_local std::string g_err;
+// Message of the last failing call on this thread: a fixed buffer, so that
+// reporting an error never allocates.
+thread_local char g_err[512];
 
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
-  char buf[512];
   va_list ap;
   va_start(ap, fmt);
-  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  std::vsnprintf(g_err, sizeof g_err, fmt, ap);
   va_end(ap);
-  g_err = buf;
   return code;
 }
 
@@ -123,6 +125,9 @@ struct ltkv_cache {
   // Attention workspace (partition partials), grown on demand.
   uint8_t *ws = nullptr;
   size_t ws_bytes = 0;
+  // The device's static scratch (ltkv_decode_attention_noalloc), looked up at
+  // creation; shared by every cache on the device.
+  uint8_t *scratch = nullptr;
   size_t attn_part_tokens = 0;  // 0 = automatic
 
   // RoPE table (ltkv_rope_init): [max_pos][rope_dim / 2] of (cos, sin).
@@ -466,7 +471,7 @@ ltkv::PoolGeom head_geom(const ltkv_cache *c, size_t head_dim) {
 
 ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                          float scale, const float *d_q, float *d_out, const ltkv::AttnWorkspace &ws,
-                         int part, int max_parts) {
+                         int part, int max_parts, uint8_t *ws_base) {
   ltkv::AttnArgs a{};
   a.k_layer = c->k_layer(layer);
   a.v_layer = c->v_layer(layer);
@@ -474,8 +479,8 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   a.v_scale = c->v_scales(layer);
   a.q = d_q;
   a.out = d_out;
-  a.part_o = ws.bytes ? (float *)(c->ws + ws.part_o_off) : nullptr;
-  a.part_ml = ws.bytes ? (float *)(c->ws + ws.part_ml_off) : nullptr;
+  a.part_o = ws.bytes ? (float *)(ws_base + ws.part_o_off) : nullptr;
+  a.part_ml = ws.bytes ? (float *)(ws_base + ws.part_ml_off) : nullptr;
   a.n = (int64_t)n;
   a.n_heads = (int)n_heads;
   a.n_kv_heads = (int)(c->kv_dim / head_dim);
@@ -823,7 +828,7 @@ int upload_plan(ltkv_cache *c) {
 
 extern "C" {
 
-const char *ltkv_last_error(void) { return g_err.c_str(); }
+const char *ltkv_last_error(void) { return g_err; }
 
 int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int device,
                 ltkv_cache **out) {
@@ -880,6 +885,15 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
     c->device_count_cu = prop.multiProcessorCount;
+  {
+    void *p = nullptr;
+    const hipError_t e = ltkv::scratch_address(device, &p);
+    if (e != hipSuccess) {
+      delete c;
+      return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    }
+    c->scratch = static_cast<uint8_t *>(p);
+  }
 
   const size_t bytes = n_layers * c->layer_elems() * c->elem;
   int rc = LTKV_OK;
@@ -981,13 +995,14 @@ int ltkv_append_batch(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint6
     slot_mapping[i] = (int32_t)(b * LTKV_BLOCK + s);
   }
   if (n_done) *n_done = i;
-  const std::string err = g_err;
-  const int frc = c->flush_pending();
-  if (rc != LTKV_OK) {
-    g_err = err;
+  if (rc != LTKV_OK) {  // the claim's error wins over a copy launch failure
+    char err[sizeof g_err];
+    std::memcpy(err, g_err, sizeof err);
+    (void)c->flush_pending();
+    std::memcpy(g_err, err, sizeof err);
     return rc;
   }
-  return frc;
+  return c->flush_pending();
 }
 
 void ltkv_truncate(ltkv_cache *c, uint32_t seq, size_t from) {
@@ -1198,12 +1213,15 @@ namespace {
 // Decode attention over explicit tables (rows == nullptr: query i reads row
 // i) or over the resident tables (query i reads row rows[i]); lengths are cut
 // to max_len tokens, which sizes the grid.
+// The partials go to the cache's workspace (grown on demand), or with
+// use_scratch to the device's static scratch, which is never grown: a launch
+// that needs more fails with LTKV_ERR_ARG and nothing is allocated.
 int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                      float scale, const float *d_q, const int32_t *d_tables, size_t table_stride,
                      const int32_t *d_rows, size_t n_rows, size_t max_len, const int32_t *d_lens,
                      float *d_out, size_t group, const int32_t *d_new_slots = nullptr,
                      const float *d_new_k = nullptr, const float *d_new_v = nullptr,
-                     size_t new_stride = 0) {
+                     size_t new_stride = 0, bool use_scratch = false) {
   // A query's partition size depends on its own length only (or is fixed by
   // ltkv_set_attention_partition), so its result is bit-identical whatever
   // else is in the batch (the reference's property, engine/README.md:102).
@@ -1216,9 +1234,20 @@ int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
   const ltkv::AttnWorkspace ws =
       ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
-  if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
+  uint8_t *base = nullptr;
+  if (use_scratch) {
+    if ((size_t)ws.bytes > ltkv::kScratchBytes)
+      return fail(LTKV_ERR_ARG,
+                  "attention needs %lld bytes of partition partials, more than the %zu bytes of the "
+                  "no-allocation scratch",
+                  (long long)ws.bytes, ltkv::kScratchBytes);
+    base = c->scratch;
+  } else {
+    if (int rc = ensure_workspace(c, (size_t)ws.bytes)) return rc;
+    base = c->ws;
+  }
   ltkv::AttnArgs a = attn_args(c, layer, n, n_heads, head_dim, scale, d_q, d_out, ws, part,
-                               (int)max_parts);
+                               (int)max_parts, base);
   a.split = split;
   a.tables = d_tables;
   a.table_stride = (int64_t)table_stride;
@@ -1253,6 +1282,27 @@ int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride, nullptr,
                           0, table_stride * LTKV_BLOCK, d_lens, d_out, group);
+}
+
+int ltkv_decode_attention_noalloc(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
+                                  size_t head_dim, float scale, const float *d_q,
+                                  const int32_t *d_tables, size_t table_stride, const int32_t *d_lens,
+                                  float *d_out) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (c->device == LTKV_NO_DEVICE) return no_device();
+  if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
+  size_t group = 0;
+  if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
+  if (n == 0) return LTKV_OK;
+  if (table_stride == 0) return fail(LTKV_ERR_ARG, "table_stride must be > 0");
+  if (!d_q || !d_tables || !d_lens || !d_out) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (((uintptr_t)d_q) % 16 != 0) return fail(LTKV_ERR_ARG, "q must be 16-byte aligned");
+  if (!c->scratch) return fail(LTKV_ERR_HIP, "no-allocation scratch unavailable on device %d", c->device);
+  DeviceGuard dg(c->device);
+  if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+  return decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride, nullptr,
+                          0, table_stride * LTKV_BLOCK, d_lens, d_out, group, nullptr, nullptr, nullptr, 0,
+                          true);
 }
 
 int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
@@ -1427,7 +1477,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   const int32_t *d = reinterpret_cast<const int32_t *>(P.d);
   const ltkv::PoolGeom g = head_geom(c, P.head_dim);
   ltkv::AttnArgs a = attn_args(c, layer, P.n, P.n_heads, P.head_dim, scale, d_q, d_out, ws, part,
-                               (int)max_parts);
+                               (int)max_parts, c->ws);
   a.split = split;
   // Short remainders in one partition each and no group-only queries: the
   // decode kernel writes every output itself (folding group partials).

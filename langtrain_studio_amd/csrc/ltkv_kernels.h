@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <cstddef>
 #include <cstdint>
 
 namespace ltkv {
@@ -178,5 +179,14 @@ struct MqArgs {
 };
 bool mq_supported(int elem, int head_dim, int group);
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s);
+
+// Scratch of the allocation-free decode attention: a static device array of
+// kScratchBytes on every device the library runs on. scratch_address gives
+// its address on `device`, which must be the current device on the first
+// call for that device (looked up once per device with hipGetSymbolAddress,
+// then kept).
+constexpr size_t kScratchBytes = size_t{32} << 20;
+constexpr int kMaxScratchDevices = 64;
+hipError_t scratch_address(int device, void **ptr);
 
 }  // namespace ltkv

@@ -25,9 +25,18 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
 
 #include "ltkv_kernels.h"
+
+// Scratch of the allocation-free decode attention (ltkv_decode_attention_noalloc):
+// the partition partials live in this static device array instead of a
+// workspace allocated on demand. Each device holds its own copy, at its own
+// address, until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: host code uses only the address that
+// hipGetSymbolAddress returns on each device (scratch_address below).
+static __device__ __align__(256) uint8_t scratch[ltkv::kScratchBytes];
 
 namespace ltkv {
 namespace {
@@ -2557,6 +2566,30 @@ hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s
   if (g.elem == 1 && a.head_dim == 128) return run(int8_t{}, std::integral_constant<int, 128>{});
   if (g.elem == 1 && a.head_dim == 64) return run(int8_t{}, std::integral_constant<int, 64>{});
   return hipErrorInvalidValue;
+}
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+hipError_t scratch_address(int device, void **ptr) {
+  *ptr = nullptr;
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != device) return hipErrorInvalidDevice;  // the lookup needs `device` current
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
 }
 
 }  // namespace ltkv

@@ -275,8 +275,10 @@ class KvCache:
             _dev_ptr(k_out, dt, "k_out", self.device), _dev_ptr(v_out, dt, "v_out", self.device)))
 
     def decode_attention(self, layer: int, q, tables, lens, n_heads: int, head_dim: int,
-                         scale: Optional[float] = None, out=None):
-        """Kernel 4: GQA paged decode attention; q, out are [n][n_heads*head_dim] f32."""
+                         scale: Optional[float] = None, out=None, noalloc: bool = False):
+        """Kernel 4: GQA paged decode attention; q, out are [n][n_heads*head_dim] f32.
+        noalloc: ltkv_decode_attention_noalloc (partials in the device's static
+        scratch; nothing allocated, same result bits)."""
         import torch
 
         n = lens.numel()
@@ -290,7 +292,8 @@ class KvCache:
             raise ValueError("out must match q")
         if scale is None:
             scale = 1.0 / math.sqrt(head_dim)  # model.rs:402
-        _check(self._lib.ltkv_decode_attention(
+        fn = self._lib.ltkv_decode_attention_noalloc if noalloc else self._lib.ltkv_decode_attention
+        _check(fn(
             self._h, layer, n, n_heads, head_dim, float(scale),
             _dev_ptr(q, torch.float32, "q", self.device),
             _dev_ptr(tables, torch.int32, "tables", self.device), tables.shape[1],
