@@ -48,10 +48,11 @@ def _args():
     p.add_argument("--kv-dtype", default="f16", choices=["f16", "q8_0"],
                    help="cache element type of the prefill and prefix-cow workloads")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
-    p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0 = host share, max 16)")
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="CPU baseline threads (0 = every CPU of this process's share)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "copy", "append-sweep", "long-context", "tinyllama", "prefix-cow",
+                   choices=["decode", "copy", "copy-bulk", "append-sweep", "long-context", "tinyllama", "prefix-cow",
                             "mixed", "prefill", "rope-append", "decode-q8", "descriptor"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
@@ -96,14 +97,106 @@ def _host_cpus() -> str:
     return f"{usable} of {logical or '?'} logical CPUs usable, {len(sockets) or '?'} socket(s), {model}"
 
 
-def _cpu_threads(req: int) -> int:
-    if req > 0:
-        return req
+def _cpu_share() -> tuple[int, str]:
+    """CPUs this process may run on: the affinity mask, bounded by the
+    cgroup's CPU quota when one is set (the lease's real share of the host)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        aff = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        aff = os.cpu_count() or 1
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(period))
+    except (OSError, ValueError):
+        try:
+            q = int(open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read())
+            period = int(open("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read())
+            if q > 0:
+                quota = max(1, q // period)
+        except (OSError, ValueError):
+            pass
+    n = min(aff, quota) if quota else aff
+    return n, f"{aff} CPUs in the affinity mask, cgroup CPU quota {quota if quota else 'none'}"
+
+
+_CPU = None
+
+
+def _oracle_calibration_ms(path: str) -> float:
+    """One-thread time of a fixed attention job (4 queries x 2048 tokens,
+    Llama-3-8B heads) on the oracle library at `path`: best of three."""
+    from oracle import oracle as ora
+
+    ora.use_library(path)
+    rng = np.random.default_rng(0)
+    kvd, n = 1024, 4 * 2048
+    o = ora.OracleKv(1, kvd, n)
+    sm = o.append_batch(np.repeat(np.arange(4, dtype=np.uint32), 2048), np.tile(np.arange(2048, dtype=np.uint64), 4))
+    k = rng.standard_normal((n, kvd), dtype=np.float32)
+    o.write_batch(0, sm, k, k)
+    q = rng.standard_normal((4, 32 * 128), dtype=np.float32)
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        o.attention(0, np.arange(4, dtype=np.uint32), np.full(4, 2047, np.uint64), q, 32, 128, threads=1)
+        best = min(best, time.perf_counter() - t0)
+    return best * 1e3
+
+
+def _cpu_setup(args) -> dict:
+    """Once per run: the oracle built twice for this host's CPU (the prebuilt
+    x86-64-v3 library, AVX2 + F16C, and a -march=native build made here), the
+    faster of the two on a calibration job kept for the baseline; the thread
+    count (every CPU of this process's share unless --cpu-threads) and a host
+    description."""
+    global _CPU
+    if _CPU is None:
+        import tempfile
+
+        from oracle import oracle as ora
+
+        builds = {"x86-64-v3 (prebuilt)": ora._LIB_PATH}
+        note = ""
+        try:
+            builds["native (built on this host)"] = ora.build_native(tempfile.mkdtemp(prefix="ltkv_oracle_"))
+        except Exception as e:  # noqa: BLE001 - the baseline still runs on the prebuilt library
+            note = f"; -march=native build failed: {str(e)[:100]}"
+        cal = {name: _oracle_calibration_ms(path) for name, path in builds.items()}
+        best = min(cal, key=cal.get)
+        ora.use_library(builds[best])
+        build = (f"g++ -O3 -ffp-contract=off -march={best}, the faster on a one-thread calibration job ("
+                 + ", ".join(f"{k}: {v:.1f} ms" for k, v in cal.items()) + ")" + note)
+        threads, share = _cpu_share()
+        if args.cpu_threads > 0:
+            threads = args.cpu_threads
+        _CPU = {"threads": threads, "host": f"{_host_cpus()}; {share}", "build": build}
+    return _CPU
+
+
+def _cpu_record(args, value: float, unit: str, sample: str, threads: int, **extra) -> dict:
+    """The cpu_baseline object of a JSON line: the oracle (the C++ restatement
+    of the reference CPU path) timed on this host."""
+    cpu = _cpu_setup(args)
+    rec = {"value": round(value, 1), "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+           "build": cpu["build"], "host": cpu["host"]}
+    rec.update(extra)
+    return rec
+
+
+def _cpu_time(fn, n_max: int, budget_s: float, at_least: int = 1) -> tuple[float, int]:
+    """Mean seconds of fn(i) for i = 0, 1, ... until n_max calls or the budget
+    is spent (at least `at_least` calls)."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    i = 0
+    while i < n_max and (i < at_least or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    return float(np.mean(times)), i
 
 
 class Llama3Decode:
@@ -195,7 +288,7 @@ class Llama3Decode:
 
 def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
     """The oracle (C++ restatement of kv.rs + model.rs attention + pool.rs)
-    running the same decode steps on the same cache state."""
+    running the same decode steps on the same cache state: (µs per step, steps)."""
     from oracle import OracleKv
 
     o = OracleKv(1, w.kvd, w.n_blocks * BLOCK, dtype=w.dtype)
@@ -212,15 +305,8 @@ def cpu_baseline(w: Llama3Decode, threads: int, budget_s: float):
         o.write_batch(0, sm, w.k_new[s], w.v_new[s])
         o.attention(0, seqs, (w.ctx + s).astype(np.uint64), w.q[s], w.n_heads, w.head_dim, threads=threads)
 
-    times = []
-    t_end = time.perf_counter() + budget_s
-    s = 0
-    while s < w.steps and (s < 2 or time.perf_counter() < t_end):
-        t0 = time.perf_counter()
-        step(s)
-        times.append(time.perf_counter() - t0)
-        s += 1
-    return float(np.mean(times) * 1e6), s
+    sec, n = _cpu_time(step, w.steps, budget_s, at_least=2)
+    return sec * 1e6, n
 
 
 def _time_op(fn, reps: int, warmup: int = 2) -> float:
@@ -251,6 +337,44 @@ def bench_copy(args):
     us = _time_op(lambda: dst.copy_(src), reps=max(args.steps, 1))
     print(json.dumps({"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
                       "GBps": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
+def bench_copy_bulk(args):
+    """Kernel 2, the copy-on-write body (kv.rs:99-110), on distinct blocks:
+    131 072 (src, dst) pairs drawn from a permutation of a 262 144-block pool at
+    the Llama-3-8B layer shape (K and V, 32 KiB each per block), so every
+    source block is read once from HBM and every destination written once:
+    8.6 GB read + 8.6 GB written per launch."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_pairs, kvd = 131072, 1024
+    n_blocks = 2 * n_pairs
+    rng = np.random.default_rng(args.seed)
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    _fill_pool_random(kv, kvd, n_blocks, args.seed)
+    pairs = rng.permutation(n_blocks).astype(np.int32).reshape(n_pairs, 2)
+    d_pairs = torch.from_numpy(pairs).cuda()
+    us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=max(min(args.steps, 20), 5))
+    nbytes = n_pairs * 2 * 2 * BLOCK * kvd * 2  # K and V, read and written
+    line = {"workload": "copy-bulk llama3-8b f16: 131072 distinct (src, dst) block pairs, 1 layer",
+            "copy_us": round(us, 1), "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+    if not args.no_cpu:
+        # the oracle's copy (memmove per block, one thread as the reference's
+        # copy_within) over a sample of the same pairs, scaled to all of them
+        from oracle import OracleKv
+
+        n_s = 8192
+        o = OracleKv(1, kvd, 2 * n_s * BLOCK, dtype="f16")
+        sample = np.arange(2 * n_s, dtype=np.int32).reshape(n_s, 2)
+        sec, n = _cpu_time(lambda _: o.copy_blocks(sample), 1 << 20, min(args.cpu_seconds, 5.0), at_least=2)
+        per_pair = sec / n_s
+        line["cpu_baseline"] = _cpu_record(
+            args, per_pair * n_pairs * 1e6, "µs/launch", f"{n} passes over {n_s} block pairs, scaled to "
+            f"{n_pairs}", 1, GBps=round(nbytes / (per_pair * n_pairs) / 1e9, 2))
+    print(json.dumps(line), flush=True)
 
 
 def bench_append_sweep(args):
@@ -298,9 +422,11 @@ def bench_long_context(args):
     kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
     if args.partition:
         kv.set_attention_partition(args.partition)
-    kv.init_free_order(rng.permutation(n_blocks))
-    sm = kv.append_batch(np.repeat(np.arange(B, dtype=np.uint32), ctx),
-                         np.tile(np.arange(ctx, dtype=np.uint64), B))
+    order = rng.permutation(n_blocks)
+    kv.init_free_order(order)
+    seqs_all = np.repeat(np.arange(B, dtype=np.uint32), ctx)
+    pos_all = np.tile(np.arange(ctx, dtype=np.uint64), B)
+    sm = kv.append_batch(seqs_all, pos_all)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed)
     chunk = 1 << 16
@@ -320,18 +446,41 @@ def bench_long_context(args):
     out = torch.empty_like(q)
     a_us = _time_op(lambda: kv.decode_attention(0, q, tables, lens, n_heads, hd, out=out), reps=10)
     a_bytes = B * ctx * 2 * kvd * 2 + 2 * q.numel() * 4 + tables.numel() * 4 + B * 4
-    print(json.dumps({
+    line = {
         "workload": "long-context 32x32768 llama3-8b f16, random tables",
         "gather_us": round(g_us, 1), "gather_GBps": round(g_bytes / (g_us * 1e-6) / 1e9, 1),
         "gather_frac": round(g_bytes / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "gather_bytes": g_bytes,
         "attention_us": round(a_us, 1), "attention_GBps": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
         "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "attention_bytes": a_bytes,
-    }), flush=True)
+        "tokens_per_s": round(B / (a_us * 1e-6), 1),
+    }
+    del k_out, v_out
+    if not args.no_cpu:
+        # the oracle on the same state: same allocator order and claims, pool read back
+        from oracle import OracleKv
+
+        threads = _cpu_setup(args)["threads"]
+        o = OracleKv(1, kvd, n_blocks * BLOCK, dtype="f16")
+        o.init_free_order(order)
+        o.append_batch(seqs_all, pos_all)
+        o.load_pool(0, *kv.read_pool(0))
+        # gather: KvCache::rows collected (kv.rs:133-150), one sequence at a
+        # time on one thread as the reference's iterator runs
+        g_sec, g_n = _cpu_time(lambda i: o.rows(0, i % B, ctx), B, min(args.cpu_seconds, 10.0), at_least=2)
+        q_h, tables_h, lens_h = q.cpu().numpy(), tables.cpu().numpy(), lens.cpu().numpy()
+        a_sec, a_n = _cpu_time(lambda _: o.attention_tables(0, tables_h, lens_h, q_h, n_heads, hd, threads=threads),
+                               3, min(args.cpu_seconds, 10.0))
+        line["cpu_baseline"] = _cpu_record(
+            args, a_sec * 1e6, "µs/step", f"{a_n} decode-attention passes over all 32 x 32768 tokens; gather: "
+            f"{g_n} sequences' rows collected on one thread, scaled to 32", threads,
+            tokens_per_s=round(B / a_sec, 1), gather_us=round(g_sec * B * 1e6, 1), gather_cores=1,
+            gather_GBps=round(g_bytes / (g_sec * B) / 1e9, 2))
+    print(json.dumps(line), flush=True)
 
 
-def _fill_pool_random(kv, kvd, n_blocks, seed):
-    """Write N(0,1) rows into every cell of a pool (device-only, outside timing),
-    so blocks that arrivals inherit hold finite data."""
+def _fill_pool_random(kv, kvd, n_blocks, seed, layer=0):
+    """Write N(0,1) rows into every cell of a layer's pool (device-only,
+    outside timing), so blocks that arrivals inherit hold finite data."""
     import torch
 
     gen = torch.Generator(device="cuda")
@@ -342,7 +491,7 @@ def _fill_pool_random(kv, kvd, n_blocks, seed):
         sm = torch.from_numpy(cells[i:i + chunk]).cuda()
         k = torch.randn((sm.numel(), kvd), generator=gen, device="cuda")
         v = torch.randn((sm.numel(), kvd), generator=gen, device="cuda")
-        kv.write_batch(0, sm, k, v)
+        kv.write_batch(layer, sm, k, v)
     torch.cuda.synchronize()
 
 
@@ -358,10 +507,12 @@ def bench_tinyllama(args):
     n_heads, n_kv, hd, B = 32, 4, 64, 4
     kvd = n_kv * hd
     kv = KvCache(1, kvd, 1024 * BLOCK, dtype="f32", device=0, stream=torch.cuda.current_stream())
-    kv.init_free_order(rng.permutation(1024))
+    order = rng.permutation(1024)
+    kv.init_free_order(order)
     ctx = rng.integers(128, 513, B)
-    sm = kv.append_batch(np.repeat(np.arange(B, dtype=np.uint32), ctx),
-                         np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx]))
+    pre_seqs = np.repeat(np.arange(B, dtype=np.uint32), ctx)
+    pre_pos = np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx])
+    sm = kv.append_batch(pre_seqs, pre_pos)
     k = torch.randn((sm.size, kvd), device="cuda")
     kv.write_batch(0, torch.from_numpy(sm).cuda(), k, k)
     seqs = np.arange(B, dtype=np.uint32)
@@ -380,10 +531,31 @@ def bench_tinyllama(args):
     a_us = _time_op(lambda: kv.decode_attention(0, q, tables, lens, n_heads, hd, scale=0.125, out=out),
                     reps=max(args.steps, 10))
     a_bytes = int((ctx + 1).sum()) * 2 * kvd * 4 + 2 * q.numel() * 4
-    print(json.dumps({"workload": "tinyllama f32, 4 seqs ctx U[128,512]", "step_us": round(us, 2),
-                      "attention_us": round(a_us, 2), "attention_bytes": a_bytes,
-                      "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}),
-          flush=True)
+    line = {"workload": "tinyllama f32, 4 seqs ctx U[128,512]", "step_us": round(us, 2),
+            "tokens_per_s": round(B / (us * 1e-6), 1),
+            "attention_us": round(a_us, 2), "attention_bytes": a_bytes,
+            "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+    if not args.no_cpu:
+        # the oracle on the same state: same allocator order and claims, pool read back
+        from oracle import OracleKv
+
+        threads = _cpu_setup(args)["threads"]
+        o = OracleKv(1, kvd, 1024 * BLOCK, dtype="f32")
+        o.init_free_order(order)
+        o.append_batch(pre_seqs, pre_pos)
+        o.load_pool(0, *kv.read_pool(0))
+        sm_h, kn_h, q_h = o.append_batch(seqs, ctx.astype(np.uint64)), kn.cpu().numpy(), q.cpu().numpy()
+        tables_h, lens_h = tables.cpu().numpy(), lens.cpu().numpy()
+
+        def cpu_step(_):
+            o.write_batch(0, sm_h, kn_h, kn_h)
+            o.attention_tables(0, tables_h, lens_h, q_h, n_heads, hd, scale=0.125, threads=threads)
+
+        sec, n = _cpu_time(cpu_step, 1 << 20, min(args.cpu_seconds, 5.0), at_least=10)
+        line["cpu_baseline"] = _cpu_record(args, sec * 1e6, "µs/step",
+                                           f"{n} steps of the same work (append of 4 rows + decode attention)",
+                                           threads, tokens_per_s=round(B / sec, 1))
+    print(json.dumps(line), flush=True)
 
 
 def bench_prefill(args):
@@ -478,25 +650,46 @@ def bench_rope_append(args):
     print(json.dumps({"workload": "rope-append", "rows": rows}), flush=True)
 
 
+def _unique_tokens(tables: np.ndarray, lens: np.ndarray) -> int:
+    """Tokens of the distinct physical blocks a batch reads: every block once,
+    with the most tokens any query reads from it (shared prefix blocks count
+    once, as the unique-byte roofline of a prefix-sharing step does)."""
+    lens = lens.astype(np.int64)
+    nb = -(-lens // BLOCK)
+    qi = np.repeat(np.arange(lens.size), nb)
+    j = np.concatenate([np.arange(n) for n in nb])
+    blocks = tables[qi, j]
+    toks = np.minimum(BLOCK, lens[qi] - j * BLOCK)
+    best = np.zeros(int(blocks.max()) + 1, np.int64)
+    np.maximum.at(best, blocks, toks)
+    return int(best.sum())
+
+
 def bench_prefix_cow(args):
     """Prefix sharing at the Llama-3-8B layer shape: 256 sequences hold a
     4088-token prefix (256 blocks, the last holding 8 tokens, refcount 256);
     step 0 appends a 64-token private suffix to every sequence, which copies
-    the shared partial block 255 times (the last holder writes in place); then
-    32 decode steps. Attention bytes count shared blocks once (unique bytes)."""
+    the shared partial block 255 times in every layer (the last holder writes
+    in place); then 32 decode steps. The cache has 8 layers (1.2 GB of pools,
+    more than the 256 MB last-level cache) and each step's attention runs on
+    layers 0..7 back to back, as a decode step's layers do, so every layer's
+    K/V comes from HBM. Attention bytes per step count each physical block
+    once with the tokens read from it (unique bytes), from that step's lengths."""
     import torch
 
     from langtrain_studio_amd import KvCache
 
-    n_heads, n_kv, hd, S, prefix, suffix, steps = 32, 8, 128, 256, 4088, 64, 32
+    n_heads, n_kv, hd, S, prefix, suffix, steps, L = 32, 8, 128, 256, 4088, 64, 32, 8
     kvd = n_kv * hd
     rng = np.random.default_rng(args.seed)
     per_seq = -(-(prefix + suffix + steps) // BLOCK) - prefix // BLOCK + 1
     n_blocks = int((prefix // BLOCK + 1 + S * per_seq) * 1.1)
-    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype=args.kv_dtype, device=0, stream=torch.cuda.current_stream())
+    kv = KvCache(L, kvd, n_blocks * BLOCK, dtype=args.kv_dtype, device=0, stream=torch.cuda.current_stream())
     eb = 2 if args.kv_dtype == "f16" else 1 + 2 / 32  # bytes per cached element (q8_0: quant + scale share)
-    kv.init_free_order(rng.permutation(n_blocks))
-    _fill_pool_random(kv, kvd, n_blocks, args.seed)
+    order = rng.permutation(n_blocks)
+    kv.init_free_order(order)
+    for layer in range(L):
+        _fill_pool_random(kv, kvd, n_blocks, args.seed + layer, layer)
     kv.append_batch(np.zeros(prefix, np.uint32), np.arange(prefix, dtype=np.uint64))
     for d in range(1, S):
         kv.share(0, d, prefix)
@@ -505,12 +698,14 @@ def bench_prefix_cow(args):
     pos0 = np.tile(np.arange(prefix, prefix + suffix, dtype=np.uint64), S)
     shared_last = int(kv.block_table(0)[-1])
     kn = torch.randn((seqs0.size, kvd), device="cuda")
-    sm0 = kv.append_batch(seqs0, pos0)  # launches the 255 copies itself
+    sm0 = kv.append_batch(seqs0, pos0)  # launches the 255 copies (every layer) itself
     d_sm0 = torch.from_numpy(sm0).cuda()
     torch.cuda.synchronize()
     assert kv.cow_copies() == S - 1, kv.cow_copies()
     app_us = _time_op(lambda: kv.write_batch(0, d_sm0, kn, kn), reps=10)
-    cow_bytes = int((S - 1) * 2 * 2 * BLOCK * kvd * eb)
+    for layer in range(1, L):
+        kv.write_batch(layer, d_sm0, kn, kn)
+    cow_bytes = int((S - 1) * 2 * 2 * BLOCK * kvd * eb * L)
     seqs = np.arange(S, dtype=np.uint32)
     sms, lens = [], []
     for s in range(steps):
@@ -525,20 +720,23 @@ def bench_prefix_cow(args):
     kd = torch.randn((steps, S, kvd), device="cuda")
     out = torch.empty((S, n_heads * hd), device="cuda")
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
-    # Each step's attention runs `layers` times back to back (as every layer
-    # of a decode step would), after one untimed call: the timed region holds
-    # device time, not the launch latency of an idle queue.
-    layers = 4
-    # Per-query decode attention (every sequence reads its whole table).
+
+    def write_step(s):
+        for layer in range(L):
+            kv.write_batch(layer, d_sm[s], kd[s], kd[s])
+
+    # Per-query decode attention (every sequence reads its whole table). One
+    # untimed call on the last layer first keeps the queue busy, so the timed
+    # region holds device time; layer 0 was last read 8 layers (~1 GB) ago.
     for s in range(steps):
-        kv.write_batch(0, d_sm[s], kd[s], kd[s])
-        kv.decode_attention(0, q[s], tables, d_lens[s], n_heads, hd, out=out)
+        write_step(s)
+        kv.decode_attention(L - 1, q[s], tables, d_lens[s], n_heads, hd, out=out)
         ev[s][0].record()
-        for _ in range(layers):
-            kv.decode_attention(0, q[s], tables, d_lens[s], n_heads, hd, out=out)
+        for layer in range(L):
+            kv.decode_attention(layer, q[s], tables, d_lens[s], n_heads, hd, out=out)
         ev[s][1].record()
     torch.cuda.synchronize()
-    flat_us = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]) * 1e3) / layers
+    flat_t = np.array([e[0].elapsed_time(e[1]) for e in ev]) * 1e3 / L
     # Planned attention: the step's tables are planned once on the host (the
     # shared prefix becomes one group) and uploaded before the timed region.
     plan_s = []
@@ -546,35 +744,70 @@ def bench_prefix_cow(args):
         t0 = time.perf_counter()
         stats = kv.plan_attention(seqs, lens[s], n_heads, hd, shared_prefix=True)
         plan_s.append(time.perf_counter() - t0)
-        kv.write_batch(0, d_sm[s], kd[s], kd[s])
-        kv.planned_attention(0, q[s], out=out)
+        write_step(s)
+        kv.planned_attention(L - 1, q[s], out=out)
         ev[s][0].record()
-        for _ in range(layers):
-            kv.planned_attention(0, q[s], out=out)
+        for layer in range(L):
+            kv.planned_attention(layer, q[s], out=out)
         ev[s][1].record()
     torch.cuda.synchronize()
-    att_us = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]) * 1e3) / layers
-    # The copy-on-write copies of step 0 again, timed alone (same pairs).
+    att_t = np.array([e[0].elapsed_time(e[1]) for e in ev]) * 1e3 / L
+    # The copy-on-write copies of step 0 again, timed alone (same pairs, all layers).
     dst = tables_h[:, prefix // BLOCK]
     pairs = np.stack([np.full(S, shared_last), dst], 1)[dst != shared_last].astype(np.int32)
     assert len(pairs) == S - 1
     d_pairs = torch.from_numpy(pairs).cuda()
     cow_us = _time_op(lambda: kv.copy_blocks(d_pairs), reps=100, warmup=10)
-    uniq_blocks = len(np.unique(tables_h[tables_h >= 0]))
-    uniq = int(uniq_blocks * BLOCK * kvd * eb * 2) + 2 * S * n_heads * hd * 4
-    logical = int(np.mean([l.astype(np.int64).sum() for l in lens]) * 2 * kvd * eb)
-    print(json.dumps({
-        "workload": f"prefix-cow llama3-8b {args.kv_dtype}: 256 seqs x 4088 shared + 64 private, 32 decode steps",
-        "cow_copies": S - 1, "cow_us": round(cow_us, 2), "cow_GBps": round(cow_bytes / (cow_us * 1e-6) / 1e9, 1),
+    row = 2 * kvd * eb  # K and V bytes of one token row
+    qo = 2 * S * n_heads * hd * 4
+    uniq = np.array([_unique_tokens(tables_h, l) * row + qo + (-(-l.astype(np.int64) // BLOCK)).sum() * 4 + S * 4
+                     for l in lens])
+    logical = np.array([l.astype(np.int64).sum() * row for l in lens])
+    att_us, flat_us = float(att_t.mean()), float(flat_t.mean())
+    frac = float(np.mean(uniq / (att_t * 1e-6) / 1e9 / PEAK_HBM_GBPS))
+    line = {
+        "workload": f"prefix-cow llama3-8b {args.kv_dtype}: 256 seqs x 4088 shared + 64 private, 32 decode steps, "
+                    f"{L} layers",
+        "cow_copies": S - 1, "cow_layers": L, "cow_us": round(cow_us, 2), "cow_bytes": cow_bytes,
+        "cow_GBps": round(cow_bytes / (cow_us * 1e-6) / 1e9, 1),
+        "cow_frac": round(cow_bytes / (cow_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
         "suffix_append_us": round(app_us, 2), "attention_us": round(att_us, 2),
-        "attention_unique_bytes": uniq, "attention_logical_bytes": logical,
-        "attention_frac_unique": round(uniq / (att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
-        "attention_logical_GBps": round(logical / (att_us * 1e-6) / 1e9, 1),
+        "attention_unique_bytes": round(float(uniq.mean())),
+        "attention_logical_bytes": round(float(logical.mean())),
+        "attention_frac_unique": round(frac, 4),
+        "attention_logical_GBps": round(float(logical.mean()) / (att_us * 1e-6) / 1e9, 1),
+        "tokens_per_s": round(S / (att_us * 1e-6), 1),
         "plan": {k: stats[k] for k in ("groups", "grouped", "shared_blocks", "prefix_workgroups")},
         "plan_host_us": round(float(np.mean(plan_s)) * 1e6, 1),
         "attention_per_query_us": round(flat_us, 2),
-        "attention_per_query_frac_unique": round(uniq / (flat_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}),
-        flush=True)
+        "attention_per_query_frac_unique": round(float(np.mean(uniq / (flat_t * 1e-6) / 1e9 / PEAK_HBM_GBPS)), 4)}
+    if not args.no_cpu:
+        # the oracle on the same history: copy-on-write as the reference does
+        # it (a memmove per layer inside append, kv.rs:99-110), then each
+        # step's attention per (query, kv head) over the whole table
+        from oracle import OracleKv
+
+        threads = _cpu_setup(args)["threads"]
+        o = OracleKv(L, kvd, n_blocks * BLOCK, dtype=args.kv_dtype)
+        o.init_free_order(order)
+        o.append_batch(np.zeros(prefix, np.uint32), np.arange(prefix, dtype=np.uint64))
+        for d in range(1, S):
+            o.share(0, d, prefix)
+        o.load_pool(0, *kv.read_pool(0))
+        if args.kv_dtype == "q8_0":
+            o.load_scales(0, *(x.transpose(0, 2, 1) for x in kv.read_scales(0)))
+        t0 = time.perf_counter()
+        o.append_batch(seqs, np.full(S, prefix, np.uint64))  # 255 copies x 8 layers
+        cow_cpu = (time.perf_counter() - t0) * 1e6
+        assert o.cow_copies() == S - 1
+        q_h = q.cpu().numpy()
+        sec, n = _cpu_time(lambda s: o.attention_tables(0, tables_h, lens[s], q_h[s], n_heads, hd, threads=threads),
+                           steps, min(args.cpu_seconds, 10.0), at_least=1)
+        line["cpu_baseline"] = _cpu_record(
+            args, sec * 1e6, "µs/step", f"{n} decode steps' attention (256 queries, one layer) on the same pool "
+            "and tables; copy-on-write: the 256 first suffix appends (255 copies x 8 layers)", threads,
+            tokens_per_s=round(S / sec, 1), cow_us=round(cow_cpu, 1), cow_cores=1)
+    print(json.dumps(line), flush=True)
 
 
 def bench_mixed(args):
@@ -681,17 +914,39 @@ def bench_mixed(args):
     e1.record()
     torch.cuda.synchronize()
     all_us = e0.elapsed_time(e1) * 1e3 / 4
-    print(json.dumps({
+    line = {
         "workload": "mixed qwen2.5-7b f16: 8x512 prefill append + 120 decode, 2% churn, "
                     f"{steps} steps", "append_us": round(app_us, 2),
         "append_GBps": round(app_bytes / (app_us * 1e-6) / 1e9, 1),
         "attention_us": round(att_us, 2), "attention_bytes": round(att_bytes),
         "attention_frac": round(att_bytes / (att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
         "step_us": round(app_us + att_us, 2),
+        "decode_tokens_per_s": round(n_dec / ((app_us + att_us) * 1e-6), 1),
         "full_step": {"rope_append_us": round(rope_us, 2),
                       "attention_all_tokens_us": round(all_us, 2),
-                      "plan": {k: stats[k] for k in ("groups", "grouped", "prefix_workgroups")}}}),
-        flush=True)
+                      "plan": {k: stats[k] for k in ("groups", "grouped", "prefix_workgroups")}}}
+    if not args.no_cpu:
+        # the oracle doing each timed step's work: the append of every batch
+        # row (f32 -> f16 writes) and the 120 decode queries' attention, on
+        # the pool read back from the device
+        from oracle import OracleKv
+
+        threads = _cpu_setup(args)["threads"]
+        o = OracleKv(1, kvd, n_blocks * BLOCK, dtype="f16")
+        o.load_pool(0, *kv.read_pool(0))
+        kn_h, q_h = kn.cpu().numpy(), q.cpu().numpy()
+        sm_h, tables_h, lens_h = np.stack(plan_sm), np.stack(plan_tables), np.stack(plan_lens)
+
+        def cpu_step(s):
+            o.write_batch(0, sm_h[s], kn_h, kn_h)
+            o.attention_tables(0, tables_h[s], lens_h[s], q_h, n_heads, hd, threads=threads)
+
+        sec, n = _cpu_time(cpu_step, steps, min(args.cpu_seconds, 10.0), at_least=2)
+        line["cpu_baseline"] = _cpu_record(
+            args, sec * 1e6, "µs/step", f"{n} steps of the same work (append of the step's "
+            f"{rows} rows + decode attention of the 120 decode queries)", threads,
+            decode_tokens_per_s=round(n_dec / sec, 1))
+    print(json.dumps(line), flush=True)
 
 
 def bench_descriptor(args):
@@ -918,10 +1173,11 @@ def bench_decode_q8(args):
         "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4), "wall_s": round(wall, 3),
     }
     if not args.no_cpu:
-        threads = _cpu_threads(args.cpu_threads)
+        threads = _cpu_setup(args)["threads"]
         cpu_us, n = cpu_baseline(w, threads, min(args.cpu_seconds, 10.0))
-        line["cpu_baseline"] = {"value": round(cpu_us, 1), "unit": "µs/step", "cores": threads, "kind": "port",
-                                "sample": f"{n} decode steps of the same workload on the oracle's q8_0 mode"}
+        line["cpu_baseline"] = _cpu_record(
+            args, cpu_us, "µs/step", f"{n} decode steps of the same workload on the oracle's q8_0 mode", threads,
+            tokens_per_s=round(w.batch / (cpu_us * 1e-6), 1))
     print(json.dumps(line), flush=True)
 
 
@@ -936,7 +1192,7 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
-    extra = {"copy": bench_copy, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
+    extra = {"copy": bench_copy, "copy-bulk": bench_copy_bulk, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
              "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
              "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8,
              "descriptor": bench_descriptor}
@@ -955,15 +1211,16 @@ def main():
 
     cpu = cpu1 = None
     if not args.no_cpu:
-        threads = _cpu_threads(args.cpu_threads)
-        host = _host_cpus()
+        threads = _cpu_setup(args)["threads"]
         cpu_us, n = cpu_baseline(w, threads, args.cpu_seconds)
-        cpu = {"value": round(cpu_us, 1), "unit": "µs/step", "cores": threads, "kind": "port",
-               "sample": f"{n} decode steps of the same workload (64 seqs, append+write+attention, "
-                         f"same cache state), oracle C++ restatement, {threads} threads; host: {host}"}
+        cpu = _cpu_record(args, cpu_us, "µs/step",
+                          f"{n} decode steps of the same workload (64 seqs, append+write+attention, same cache "
+                          f"state), oracle C++ restatement, {threads} threads", threads,
+                          tokens_per_s=round(w.batch / (cpu_us * 1e-6), 1))
         cpu1_us, n1 = cpu_baseline(w, 1, min(args.cpu_seconds, 5.0))
         cpu1 = {"value": round(cpu1_us, 1), "unit": "µs/step", "cores": 1, "kind": "port",
-                "sample": f"{n1} decode steps, same work, one thread"}
+                "sample": f"{n1} decode steps, same work, one thread",
+                "tokens_per_s": round(w.batch / (cpu1_us * 1e-6), 1)}
 
     out = {
         "metric": METRIC,
@@ -982,6 +1239,7 @@ def main():
                                "64 seqs ctx U[2048,4096], 1 append + 1 decode attention per step, "
                                "fused into one launch (ltkv_append_decode_attention)",
                    "global_batch": 64, "seq_len": "2048-4096", "parallelism": "none (1 GPU)"},
+        "tokens_per_s": round(w.batch / (fused_us * 1e-6), 1),
         "attention_us": round(att_us, 2),
         "attention_roofline_us": round(roofline_us, 2),
         "append_us": round(app_us, 2),

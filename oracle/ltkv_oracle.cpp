@@ -315,6 +315,22 @@ struct OracleKv {
   }
 
   // kv.rs:85-121. Returns 0, 1 (full) or 2 (non-contiguous).
+  // The copy-on-write body of kv.rs:99-110: every layer's K and V rows of
+  // block src copied into block dst (copy_within).
+  void copy_block(size_t src_b, size_t dst_b) {
+    const size_t n = kBlock * kv_dim * elem;
+    for (size_t l = 0; l < n_layers; ++l) {
+      const size_t src = offset(l, src_b, 0) * elem, dst = offset(l, dst_b, 0) * elem;
+      std::memmove(&k[dst], &k[src], n);
+      std::memmove(&v[dst], &v[src], n);
+      if (elem == 1) {  // the block's scales travel with its quants
+        const size_t ns = kBlock * kv_dim / 32, s0 = offset(l, src_b, 0) / 32, d0 = offset(l, dst_b, 0) / 32;
+        std::memmove(&ks[d0], &ks[s0], ns * 2);
+        std::memmove(&vs[d0], &vs[s0], ns * 2);
+      }
+    }
+  }
+
   int append(uint32_t seq, size_t pos, size_t *block_out, size_t *slot_out) {
     Seq &s = seqs[seq];  // entry().or_default()
     if (pos != s.len) {
@@ -332,17 +348,7 @@ struct OracleKv {
       if (refs[last] > 1) {
         size_t nb;
         if (!alloc(&nb)) return 1;
-        const size_t n = kBlock * kv_dim * elem;
-        for (size_t l = 0; l < n_layers; ++l) {
-          const size_t src = offset(l, last, 0) * elem, dst = offset(l, nb, 0) * elem;
-          std::memmove(&k[dst], &k[src], n);
-          std::memmove(&v[dst], &v[src], n);
-          if (elem == 1) {  // the block's scales travel with its quants
-            const size_t ns = kBlock * kv_dim / 32, s0 = offset(l, last, 0) / 32, d0 = offset(l, nb, 0) / 32;
-            std::memmove(&ks[d0], &ks[s0], ns * 2);
-            std::memmove(&vs[d0], &vs[s0], ns * 2);
-          }
-        }
+        copy_block(last, nb);
         release(last);
         s.blocks.back() = nb;
         ++cow_copies;
@@ -682,6 +688,20 @@ int ora_block_table(void *h, uint32_t seq, int32_t *out, size_t cap, size_t *n_b
 }
 
 void ora_truncate(void *h, uint32_t seq, size_t from) { ((OracleKv *)h)->truncate(seq, from); }
+
+// The copy-on-write body (kv.rs:99-110) for n (src, dst) block pairs, in
+// order; pairs with a block out of range are skipped. Returns pairs copied.
+size_t ora_copy_blocks(void *h, size_t n, const int32_t *pairs) {
+  auto *kv = (OracleKv *)h;
+  size_t done = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const int32_t a = pairs[2 * i], b = pairs[2 * i + 1];
+    if (a < 0 || b < 0 || (size_t)a >= kv->n_blocks || (size_t)b >= kv->n_blocks) continue;
+    kv->copy_block((size_t)a, (size_t)b);
+    ++done;
+  }
+  return done;
+}
 void ora_share(void *h, uint32_t src, uint32_t dst, size_t len) {
   ((OracleKv *)h)->share(src, dst, len);
 }

@@ -16,6 +16,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libltkv_oracle.so")
+_lib_path = _LIB_PATH
 _lib = None
 
 F16, F32, Q8_0 = 0, 1, 2
@@ -36,13 +37,31 @@ def build() -> str:
     return _LIB_PATH
 
 
+def build_native(out_dir: str) -> str:
+    """Compile the oracle with -march=native for the host this runs on (the
+    CPU baseline's build; every other flag as the Makefile's) into out_dir."""
+    out = os.path.join(out_dir, "libltkv_oracle_native.so")
+    subprocess.run(["make", "-s", "-C", _HERE, "MARCH=native", f"OUT={out}"], check=True,
+                   capture_output=True, text=True, timeout=300)
+    return out
+
+
+def use_library(path: str) -> None:
+    """Load the oracle from `path` for OracleKv objects created from now on
+    (the CPU baseline switches to its -march=native build this way)."""
+    global _lib, _lib_path
+    _lib = None
+    _lib_path = path
+    load()
+
+
 def load():
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(_LIB_PATH):
+    if _lib_path == _LIB_PATH and not os.path.exists(_LIB_PATH):
         build()
-    lib = C.CDLL(_LIB_PATH)
+    lib = C.CDLL(_lib_path)
     sz, u32, i32, u64, vp = C.c_size_t, C.c_uint32, C.c_int32, C.c_uint64, C.c_void_p
     P = C.POINTER
     sig = {
@@ -71,6 +90,7 @@ def load():
         "ora_rows": (C.c_int, [vp, sz, u32, sz, vp, vp]),
         "ora_block_table": (C.c_int, [vp, u32, vp, sz, P(sz)]),
         "ora_truncate": (None, [vp, u32, sz]),
+        "ora_copy_blocks": (sz, [vp, sz, vp]),
         "ora_share": (None, [vp, u32, u32, sz]),
         "ora_pool": (None, [vp, sz, vp, vp]),
         "ora_load_pool": (None, [vp, sz, vp, vp]),
@@ -252,6 +272,11 @@ class OracleKv:
         return out
 
     # -- kv.rs:153-183
+    def copy_blocks(self, pairs) -> int:
+        """The copy-on-write body (kv.rs:99-110) for (src, dst) block pairs."""
+        pairs = np.ascontiguousarray(pairs, dtype=np.int32).reshape(-1, 2)
+        return int(self._lib.ora_copy_blocks(self._h, pairs.shape[0], _ptr(pairs)))
+
     def truncate(self, seq: int, from_: int) -> None:
         self._lib.ora_truncate(self._h, seq, from_)
 

@@ -94,6 +94,41 @@ def test_share_then_diverge_copies_on_write():
     assert kv.len(0) == 20
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32", "q8_0"])
+def test_copy_blocks_is_the_cow_body(dtype):
+    """ora_copy_blocks (the copy-on-write body of kv.rs:99-110, in bulk) against
+    numpy copies of the pools: every layer's K and V rows (and Q8_0 scales) of
+    each source block land in its destination, in pair order (a chain a->b,
+    b->c moves a's rows to c), nothing else changes, out-of-range pairs are
+    skipped."""
+    rng = np.random.default_rng(5)
+    L, kvd, nb = 3, 64, 12
+    kv = OracleKv(L, kvd, nb * BLOCK, dtype=dtype)
+    for layer in range(L):
+        cells = np.arange(nb * BLOCK, dtype=np.int32)
+        k = rng.standard_normal((cells.size, kvd), dtype=np.float32)
+        kv.write_batch(layer, cells, k, -k)
+    before = [kv.pool(layer) for layer in range(L)]
+    sc_before = [kv.scales(layer) for layer in range(L)] if dtype == "q8_0" else None
+    pairs = np.array([[1, 4], [4, 7], [9, 2], [-1, 3], [0, nb], [11, 0]], np.int32)
+    assert kv.copy_blocks(pairs) == 4
+    for layer in range(L):
+        k, v = kv.pool(layer)
+        want_k, want_v = before[layer][0].copy(), before[layer][1].copy()
+        for a, b in pairs[:3].tolist() + [[11, 0]]:
+            want_k[b], want_v[b] = want_k[a], want_v[a]
+        np.testing.assert_array_equal(k, want_k)
+        np.testing.assert_array_equal(v, want_v)
+        np.testing.assert_array_equal(k[7], before[layer][0][1])  # the chain carried block 1's rows
+        if dtype == "q8_0":
+            ks, vs = kv.scales(layer)
+            wk, wv = sc_before[layer][0].copy(), sc_before[layer][1].copy()
+            for a, b in pairs[:3].tolist() + [[11, 0]]:
+                wk[b], wv[b] = wk[a], wv[a]
+            np.testing.assert_array_equal(ks, wk)
+            np.testing.assert_array_equal(vs, wv)
+
+
 def test_truncate_frees_blocks():
     """kv.rs:219-229."""
     kv = OracleKv(1, 4, 64)
