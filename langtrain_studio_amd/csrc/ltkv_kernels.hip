@@ -76,51 +76,78 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 // ----------------------------------------------------------------------------
 // Kernel 1: slot-mapped append. One thread moves 8 consecutive elements of
-// one token row of K and of V: two 32-byte f32 reads each, one 16-byte f16
-// write each (or two 16-byte f32 writes).
+// ROWS token rows of K and of V: all f32 reads (16 bytes each) are issued
+// before the conversions, then one 16-byte f16 write per row and tensor (or
+// two 16-byte f32 writes).
+//  * sources that fit the caches (the projection that produced K and V just
+//    wrote them): one row a thread, plain loads;
+//  * STREAM, sources larger than the 256 MB last-level cache: two rows a
+//    thread, non-temporal loads (1-2% faster at 64k-262k tokens of kv_dim
+//    1024; the same form on a 4216-token step whose sources sat in the
+//    caches was 37% slower, the loads missing them).
 // ----------------------------------------------------------------------------
-template <int ELEM>
+template <int ELEM, bool STREAM>
 __global__ void __launch_bounds__(256)
 write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
              const int32_t *__restrict__ slots, const float *__restrict__ k,
              const float *__restrict__ v, int64_t n, int64_t src_stride, int kv_dim,
              int64_t n_slots) {
+  constexpr int kWriteRows = STREAM ? 2 : 1;
   const int chunks = kv_dim >> 3;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / chunks;
-  if (row >= n) return;
-  const int c = (int)(gid - row * chunks);
-  const int32_t s = slots[row];
-  if (s < 0 || (int64_t)s >= n_slots) return;
+  const int64_t pair = gid / chunks;
+  const int64_t row0 = pair * kWriteRows;
+  if (row0 >= n) return;
+  const int c = (int)(gid - pair * chunks);
   const int col = c << 3;
-  const int64_t dst = (int64_t)s * kv_dim + col;  // cell block*16+slot, token-major row
-
-  const f32x4 *ks = reinterpret_cast<const f32x4 *>(k + row * src_stride + col);
-  const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
-  const f32x4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
-  if constexpr (ELEM == 2) {
-    u32x4 ko, vo;
-    ko.x = pack_f16x2(k0.x, k0.y);
-    ko.y = pack_f16x2(k0.z, k0.w);
-    ko.z = pack_f16x2(k1.x, k1.y);
-    ko.w = pack_f16x2(k1.z, k1.w);
-    vo.x = pack_f16x2(v0.x, v0.y);
-    vo.y = pack_f16x2(v0.z, v0.w);
-    vo.z = pack_f16x2(v1.x, v1.y);
-    vo.w = pack_f16x2(v1.z, v1.w);
-    // non-temporal: the cells are not read again before they leave the
-    // caches, and the attention after the append keeps its cache lines
-    // (continuous-batching step of 4216 tokens: append 4%, attention 2%
-    // faster; bulk appends unchanged)
-    __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kpool + dst * 2));
-    __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vpool + dst * 2));
-  } else {
-    f32x4 *kd = reinterpret_cast<f32x4 *>(kpool + dst * 4);
-    f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
-    kd[0] = k0;
-    kd[1] = k1;
-    vd[0] = v0;
-    vd[1] = v1;
+  f32x4 a[kWriteRows][4];
+  int32_t s[kWriteRows];
+#pragma unroll
+  for (int j = 0; j < kWriteRows; ++j) {
+    const int64_t row = row0 + j < n ? row0 + j : row0;  // a missing second row reloads the first
+    s[j] = row0 + j < n ? slots[row] : -1;
+    const f32x4 *ks = reinterpret_cast<const f32x4 *>(k + row * src_stride + col);
+    const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
+    if constexpr (STREAM) {
+      a[j][0] = __builtin_nontemporal_load(ks);
+      a[j][1] = __builtin_nontemporal_load(ks + 1);
+      a[j][2] = __builtin_nontemporal_load(vs);
+      a[j][3] = __builtin_nontemporal_load(vs + 1);
+    } else {
+      a[j][0] = ks[0];
+      a[j][1] = ks[1];
+      a[j][2] = vs[0];
+      a[j][3] = vs[1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kWriteRows; ++j) {
+    if (s[j] < 0 || (int64_t)s[j] >= n_slots) continue;  // skipped cell
+    const int64_t dst = (int64_t)s[j] * kv_dim + col;  // cell block*16+slot, token-major row
+    if constexpr (ELEM == 2) {
+      u32x4 ko, vo;
+      ko.x = pack_f16x2(a[j][0].x, a[j][0].y);
+      ko.y = pack_f16x2(a[j][0].z, a[j][0].w);
+      ko.z = pack_f16x2(a[j][1].x, a[j][1].y);
+      ko.w = pack_f16x2(a[j][1].z, a[j][1].w);
+      vo.x = pack_f16x2(a[j][2].x, a[j][2].y);
+      vo.y = pack_f16x2(a[j][2].z, a[j][2].w);
+      vo.z = pack_f16x2(a[j][3].x, a[j][3].y);
+      vo.w = pack_f16x2(a[j][3].z, a[j][3].w);
+      // non-temporal: the cells are not read again before they leave the
+      // caches, and the attention after the append keeps its cache lines
+      // (continuous-batching step of 4216 tokens: append 4%, attention 2%
+      // faster; bulk appends unchanged)
+      __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kpool + dst * 2));
+      __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vpool + dst * 2));
+    } else {
+      f32x4 *kd = reinterpret_cast<f32x4 *>(kpool + dst * 4);
+      f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
+      kd[0] = a[j][0];
+      kd[1] = a[j][1];
+      vd[0] = a[j][2];
+      vd[1] = a[j][3];
+    }
   }
 }
 
@@ -407,43 +434,116 @@ write_rope_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uin
                   (is_v ? vscale : kscale) + scale_index(s, e >> 5, kv_dim >> 5));
 }
 // ----------------------------------------------------------------------------
-// Kernel 2: block copy. Work item = (pair, layer, tensor, 8 KiB chunk); 256
-// threads each move 2 x 16 bytes, all loads issued before the stores. (At the
-// 255-copy step of 256 forks, 8 KiB chunks ran 5.2-5.4 us against 5.6-5.8 us
-// for 16 KiB, 6.4-6.5 for 4 KiB and 7.2-7.3 for 32 KiB.)
+// Kernel 2: block copy. Work item = one chunk of THREADS x VEC 16-byte
+// vectors of one (pair, layer, tensor); every thread issues its VEC
+// non-temporal loads before its stores. Two forms:
+//  * claim batches (copy-on-write, typically up to a few hundred pairs):
+//    256 threads x 2 vectors (8 KiB chunks), the layers of a pair adjacent,
+//    plain stores.
+//    At the 255-copy step of 256 forks (one shared source block) 8 KiB
+//    chunks ran 5.2-5.4 us against 5.6-5.8 us for 16 KiB, 6.4-6.5 for 4 KiB
+//    and 7.2-7.3 for 32 KiB; 1024-thread work-groups 20% slower.
+//  * bulk batches (4096 pairs and more): 1024 threads x 1 vector (16 KiB
+//    chunks), layer the slowest index, so the work-groups in flight copy
+//    consecutive pairs of one layer, in the destination order set up by
+//    copy_order_* below; non-temporal stores.
+// The order in which work-groups write matters on this part: 131 072 copies
+// of 32 KiB blocks between random places ran at 64% of 8 TB/s issued in a
+// random destination order and at 74% issued in ascending destination order
+// (the same with the destinations only bucketed by 64 blocks), so the
+// claim's copy-on-write pairs are sorted by destination on the host and bulk
+// caller batches are bucketed by destination on the device first.
 // ----------------------------------------------------------------------------
-constexpr int kCopyUnroll = 2;
-constexpr int64_t kCopyChunk = 256 * 16 * kCopyUnroll;  // bytes per work-group
+constexpr int kCopyBulkThreads = 1024;
 
-__global__ void __launch_bounds__(256)
+template <int THREADS, int VEC, bool LAYER_MAJOR>
+__global__ void __launch_bounds__(THREADS)
 copy_blocks_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
-                   const int32_t *__restrict__ pairs, int64_t n_blocks, int n_layers,
+                   const int32_t *__restrict__ pairs, int64_t n_pairs, int n_layers, int64_t n_blocks,
                    int64_t block_bytes, int64_t layer_bytes, int chunks_per_block) {
   int64_t wg = blockIdx.x;
   const int chunk = (int)(wg % chunks_per_block);
   wg /= chunks_per_block;
   const int tensor = (int)(wg & 1);
   wg >>= 1;
-  const int layer = (int)(wg % n_layers);
-  const int64_t pair = wg / n_layers;
+  const int64_t pair = LAYER_MAJOR ? wg % n_pairs : wg / n_layers;
+  const int64_t layer = LAYER_MAJOR ? wg / n_pairs : wg % n_layers;
   const int32_t src = pairs[2 * pair], dst = pairs[2 * pair + 1];
   if (src < 0 || dst < 0 || src >= n_blocks || dst >= n_blocks || src == dst) return;
-  uint8_t *base = (tensor ? vpool : kpool) + (int64_t)layer * layer_bytes;
+  uint8_t *base = (tensor ? vpool : kpool) + layer * layer_bytes;
   const u32x4 *s = reinterpret_cast<const u32x4 *>(base + (int64_t)src * block_bytes);
   u32x4 *d = reinterpret_cast<u32x4 *>(base + (int64_t)dst * block_bytes);
   const int64_t n16 = block_bytes >> 4;
-  const int64_t i0 = chunk * (kCopyChunk >> 4) + threadIdx.x;
-  u32x4 r[kCopyUnroll];
+  const int64_t i0 = (int64_t)chunk * THREADS * VEC + threadIdx.x;
+  u32x4 r[VEC];
 #pragma unroll
-  for (int u = 0; u < kCopyUnroll; ++u) {
-    const int64_t i = i0 + u * 256;
+  for (int u = 0; u < VEC; ++u) {
+    const int64_t i = i0 + u * THREADS;
     if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
   }
 #pragma unroll
-  for (int u = 0; u < kCopyUnroll; ++u) {
-    const int64_t i = i0 + u * 256;
-    if (i < n16) d[i] = r[u];
+  for (int u = 0; u < VEC; ++u) {
+    const int64_t i = i0 + u * THREADS;
+    if (i >= n16) continue;
+    if constexpr (LAYER_MAJOR) __builtin_nontemporal_store(r[u], d + i);
+    else d[i] = r[u];
   }
+}
+
+// Destination buckets of 2^kCopyOrderShift blocks: a counting sort of the
+// pairs by bucket (count, exclusive scan, scatter). The order within a
+// bucket is whatever the atomics give; it changes no result, since every
+// destination of a batch is written by one pair only. `counts` is all zero
+// on entry and is left all zero by copy_order_scan.
+constexpr int kCopyOrderShift = 6;
+
+__device__ __forceinline__ int32_t copy_bucket(int32_t dst, int64_t n_blocks) {
+  return (dst < 0 || dst >= n_blocks) ? 0 : (dst >> kCopyOrderShift);
+}
+
+__global__ void __launch_bounds__(256)
+copy_order_count(const int32_t *__restrict__ pairs, int64_t n, int64_t n_blocks,
+                 int32_t *__restrict__ counts) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  atomicAdd(counts + copy_bucket(pairs[2 * i + 1], n_blocks), 1);
+}
+
+// One work-group: cursors = exclusive prefix sums of counts; counts cleared.
+__global__ void __launch_bounds__(1024)
+copy_order_scan(int32_t *__restrict__ counts, int32_t *__restrict__ cursors, int n_buckets) {
+  __shared__ int32_t sh[1024];
+  int32_t carry = 0;
+  for (int base = 0; base < n_buckets; base += 1024) {
+    const int i = base + (int)threadIdx.x;
+    const int32_t c = i < n_buckets ? counts[i] : 0;
+    sh[threadIdx.x] = c;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int32_t t = threadIdx.x >= (unsigned)off ? sh[threadIdx.x - off] : 0;
+      __syncthreads();
+      sh[threadIdx.x] += t;
+      __syncthreads();
+    }
+    if (i < n_buckets) {
+      cursors[i] = carry + sh[threadIdx.x] - c;
+      counts[i] = 0;
+    }
+    carry += sh[1023];
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(256)
+copy_order_scatter(const int32_t *__restrict__ pairs, int64_t n, int64_t n_blocks,
+                   int32_t *__restrict__ cursors, int32_t *__restrict__ sorted) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t src = pairs[2 * i], dst = pairs[2 * i + 1];
+  const int32_t pos = atomicAdd(cursors + copy_bucket(dst, n_blocks), 1);
+  if (pos < 0 || pos >= n) return;  // only if counts were not zero on entry
+  sorted[2 * (int64_t)pos] = src;
+  sorted[2 * (int64_t)pos + 1] = dst;
 }
 
 // ----------------------------------------------------------------------------
@@ -2394,21 +2494,29 @@ hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void
   return hipGetLastError();
 }
 
+template <int ELEM, bool STREAM>
+hipError_t launch_write_form(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
+                             const float *k, const float *v, int64_t n, int64_t src_stride, hipStream_t s) {
+  constexpr int rows = STREAM ? 2 : 1;
+  const int64_t threads = (n + rows - 1) / rows * (g.kv_dim >> 3);
+  const int64_t blocks = (threads + 255) / 256;
+  write_kernel<ELEM, STREAM><<<(unsigned)blocks, 256, 0, s>>>(
+      static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n, src_stride, g.kv_dim,
+      g.n_blocks * 16);
+  return hipGetLastError();
+}
+
 hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
                         const float *k, const float *v, int64_t n, int64_t src_stride,
                         hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  const int64_t threads = n * (g.kv_dim >> 3);
-  const int64_t blocks = (threads + 255) / 256;
+  constexpr int64_t kLastLevelCache = 256ll << 20;  // MALL bytes
+  const bool stream = n * (int64_t)g.kv_dim * 8 > kLastLevelCache;
   if (g.elem == 2)
-    write_kernel<2><<<(unsigned)blocks, 256, 0, s>>>(
-        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n,
-        src_stride, g.kv_dim, g.n_blocks * 16);
-  else
-    write_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(
-        static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n,
-        src_stride, g.kv_dim, g.n_blocks * 16);
-  return hipGetLastError();
+    return stream ? launch_write_form<2, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s)
+                  : launch_write_form<2, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s);
+  return stream ? launch_write_form<4, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s)
+                : launch_write_form<4, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s);
 }
 
 hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
@@ -2447,17 +2555,36 @@ hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer,
   return hipGetLastError();
 }
 
-hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
-                              const int32_t *pairs, int64_t n_pairs, hipStream_t s) {
-  if (n_pairs <= 0) return hipSuccess;
+template <int THREADS, int VEC, bool LAYER_MAJOR>
+hipError_t launch_copy_form(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool, const int32_t *pairs,
+                            int64_t n_pairs, hipStream_t s) {
   const int64_t block_bytes = g.block_stride * g.elem;
   const int64_t layer_bytes = g.n_blocks * block_bytes;
-  const int chunks = (int)((block_bytes + kCopyChunk - 1) / kCopyChunk);
-  const int64_t wgs = n_pairs * n_layers * 2 * chunks;
-  copy_blocks_kernel<<<(unsigned)wgs, 256, 0, s>>>(static_cast<uint8_t *>(k_pool),
-                                                   static_cast<uint8_t *>(v_pool), pairs,
-                                                   g.n_blocks, n_layers, block_bytes,
-                                                   layer_bytes, chunks);
+  constexpr int64_t chunk = (int64_t)THREADS * VEC * 16;
+  const int chunks = (int)((block_bytes + chunk - 1) / chunk);
+  const int64_t wgs = (int64_t)n_layers * n_pairs * 2 * chunks;
+  copy_blocks_kernel<THREADS, VEC, LAYER_MAJOR><<<(unsigned)wgs, THREADS, 0, s>>>(
+      static_cast<uint8_t *>(k_pool), static_cast<uint8_t *>(v_pool), pairs, n_pairs, n_layers, g.n_blocks,
+      block_bytes, layer_bytes, chunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
+                              const int32_t *pairs, int64_t n_pairs, bool bulk, hipStream_t s) {
+  if (n_pairs <= 0) return hipSuccess;
+  if (bulk) return launch_copy_form<kCopyBulkThreads, 1, true>(g, n_layers, k_pool, v_pool, pairs, n_pairs, s);
+  return launch_copy_form<256, 2, false>(g, n_layers, k_pool, v_pool, pairs, n_pairs, s);
+}
+
+int64_t copy_order_buckets(int64_t n_blocks) { return (n_blocks >> kCopyOrderShift) + 1; }
+
+hipError_t launch_copy_order(const int32_t *pairs, int64_t n_pairs, int64_t n_blocks, int32_t *counts,
+                             int32_t *cursors, int32_t *sorted, hipStream_t s) {
+  if (n_pairs <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((n_pairs + 255) / 256);
+  copy_order_count<<<grid, 256, 0, s>>>(pairs, n_pairs, n_blocks, counts);
+  copy_order_scan<<<1, 1024, 0, s>>>(counts, cursors, (int)copy_order_buckets(n_blocks));
+  copy_order_scatter<<<grid, 256, 0, s>>>(pairs, n_pairs, n_blocks, cursors, sorted);
   return hipGetLastError();
 }
 

@@ -198,6 +198,36 @@ def test_copy_blocks_bulk(gpu):
         np.testing.assert_array_equal(v, wv)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+def test_copy_blocks_destination_ordered(gpu, dtype):
+    """Batches of 4096 pairs and more are bucketed by destination on the
+    device before the copy: the pools (and q8_0 scales) equal the oracle's
+    block copies bit for bit, invalid pairs are skipped, and the bucket
+    counts start from zero again on the next call (three calls in a row:
+    above, at and below the ordering threshold)."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    kv_dim, n_blocks = 64, 12000
+    g, o = _caches(2, kv_dim, n_blocks * BLOCK, dtype, rng.permutation(n_blocks))
+    fill_sequences([("gpu", g), ("oracle", o)], {s: 16 * BLOCK for s in range(n_blocks // 16)}, rng, kv_dim,
+                   layers=(0, 1))
+    for n_pairs in (5000, 4096, 100):
+        perm = rng.permutation(n_blocks).astype(np.int32)
+        pairs = np.stack([perm[:n_pairs], perm[n_pairs:2 * n_pairs]], 1)
+        bad = np.array([[-1, 5], [7, n_blocks], [3, 3], [n_blocks + 9, 2]], dtype=np.int32)
+        pairs = np.concatenate([pairs, bad])[rng.permutation(n_pairs + len(bad))]
+        g.copy_blocks(torch.from_numpy(np.ascontiguousarray(pairs)).to(gpu))
+        o.copy_blocks(pairs)
+        _assert_pools_equal(g, o, (0, 1))
+        if dtype == "q8_0":
+            for layer in (0, 1):
+                gks, gvs = g.read_scales(layer)
+                oks, ovs = o.scales(layer)
+                np.testing.assert_array_equal(gks, oks.transpose(0, 2, 1))  # [block][group][slot]
+                np.testing.assert_array_equal(gvs, ovs.transpose(0, 2, 1))
+
+
 # ---------------------------------------------------------------------------- gather (kernel 3)
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_gather_ragged_matches_rows(gpu, dtype):
