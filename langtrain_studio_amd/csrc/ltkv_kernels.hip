@@ -1513,6 +1513,86 @@ __device__ __forceinline__ h8 i8x8_to_h8(const u32x2 &w) {
 
 constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
 
+// ----------------------------------------------------------------------------
+// Work order of the decode grid. The grid's items are (query, partition)
+// pairs (times the kv-head groups, fastest). Taken in query order, a batch of
+// mixed lengths leaves the SIMDs whose waves drew short partitions idle while
+// the longest ones finish, and the chip stops being bandwidth-bound well
+// before the end. So the items are taken by descending partition size class
+// (64-token classes), then query index, then partition: the hardware hands
+// work-groups to freed SIMDs in grid order, which makes this longest-first
+// list scheduling. Each wave finds its item from the lengths alone (one
+// histogram in LDS, one prefix scan per 64 queries), so nothing is computed
+// or uploaded per step on the host; a query's partitions and result bits do
+// not depend on where its items land.
+// ----------------------------------------------------------------------------
+constexpr int kOrderClasses = 16;
+constexpr int kOrderMaxQueries = 256;  // beyond this, query order (the scans would cost more)
+
+__device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
+                                                  int part_tokens, int split, int &key, int &items) {
+  int64_t len = lens[q];
+  if (len < 0) len = 0;
+  if (len > max_len) len = max_len;
+  const int pt = partition_tokens(len, part_tokens) / split;
+  items = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+  key = pt >> 6 < kOrderClasses - 1 ? pt >> 6 : kOrderClasses - 1;
+}
+
+// Item t of the ordered grid: its query qx and partition part, or false
+// when t is past the last item. One wave; `hist` is kOrderClasses ints of LDS.
+__device__ __forceinline__ bool decode_order_item(int64_t t, const int32_t *__restrict__ lens, int64_t n,
+                                                  int64_t max_len, int part_tokens, int split, int lane,
+                                                  int32_t *hist, int64_t &qx, int &part) {
+  if (lane < kOrderClasses) hist[lane] = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n; c0 += 64) {
+    if (c0 + lane < n) {
+      int key, items;
+      decode_item_shape(lens, c0 + lane, max_len, part_tokens, split, key, items);
+      atomicAdd(hist + key, items);  // LDS
+    }
+  }
+  __syncthreads();
+  int cls = -1;
+  int64_t base = 0;
+  for (int k = kOrderClasses - 1; k >= 0; --k) {
+    const int c = hist[k];
+    if (t < base + c) {
+      cls = k;
+      break;
+    }
+    base += c;
+  }
+  if (cls < 0) return false;
+  t -= base;
+  for (int64_t c0 = 0; c0 < n; c0 += 64) {
+    int v = 0;
+    if (c0 + lane < n) {
+      int key, items;
+      decode_item_shape(lens, c0 + lane, max_len, part_tokens, split, key, items);
+      v = key == cls ? items : 0;
+    }
+    int incl = v;  // inclusive prefix sum over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    if (t < tot) {
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > t);
+      const int j = __builtin_ctzll(hit);
+      const int end = __shfl(incl, j, 64), cnt = __shfl(v, j, 64);
+      qx = c0 + j;
+      part = (int)(t - (end - cnt));
+      return true;
+    }
+    t -= tot;
+  }
+  return false;
+}
+
 // The weight operand's part for this lane: the lo part on lo lanes, else
 // the hi part (columns past the group are discarded, any finite value does).
 __device__ __forceinline__ _Float16 weight_part(float x, bool lo_lane) {
@@ -1545,7 +1625,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
                  int max_pre_parts, const int32_t *__restrict__ new_slots,
                  const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
-                 T *kdst, T *vdst) {
+                 T *kdst, T *vdst, int64_t n_queries, int order) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -1569,13 +1649,28 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   __shared__ __attribute__((aligned(16))) char sv[NH][16 * VPITCH];
   __shared__ __attribute__((aligned(16))) uint16_t ssc[2][Q8 ? NSC : 1];  // q8_0: K, V scales of a tile
 
-  // 1-D grid: (query, NH-head group, partition), the head group fastest.
+  __shared__ int32_t shist[kOrderClasses];
+
+  // 1-D grid: (query, NH-head group, partition), the head group fastest; with
+  // `order`, the (query, partition) items longest first (decode_order_item).
   const int n_groups = n_kv_heads / NH;
   const int kvh0 = (int)(blockIdx.x % n_groups) * NH;
-  const int part = (int)((blockIdx.x / n_groups) % max_parts);
-  const int64_t qx = blockIdx.x / ((unsigned)n_groups * max_parts);
-  const int64_t qi = qmap ? qmap[qx] : qx;
   const int lane = threadIdx.x & 63;
+  int part;
+  int64_t qx;
+  if (order) {
+    if (!decode_order_item(blockIdx.x / n_groups, lens, n_queries, max_len, part_tokens, split, lane, shist, qx,
+                           part))
+      return;
+    // uniform over the wave: keep them (and the table and buffer addresses
+    // derived from them) in scalar registers
+    qx = __builtin_amdgcn_readfirstlane((int)qx);
+    part = __builtin_amdgcn_readfirstlane(part);
+  } else {
+    part = (int)((blockIdx.x / n_groups) % max_parts);
+    qx = blockIdx.x / ((unsigned)n_groups * max_parts);
+  }
+  const int64_t qi = qmap ? qmap[qx] : qx;
   const int lr = lane & 15, lq = lane >> 4;
   const int n_heads = n_kv_heads * G;
 
@@ -1957,6 +2052,12 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   }
 }
 
+// Plain decode attention of up to kOrderMaxQueries queries takes its items
+// longest first; planned launches (query maps, group partials) keep query order.
+inline bool decode_ordered(const AttnArgs &a) {
+  return !a.qmap && !a.pre_parts && a.n > 1 && a.n <= kOrderMaxQueries;
+}
+
 // One wave per work-group: each wave streams a whole partition of NH kv heads.
 template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
@@ -1967,7 +2068,8 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
       a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts, a.new_slots, a.new_k, a.new_v, a.new_stride,
-      static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)));
+      static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)), a.n,
+      decode_ordered(a) ? 1 : 0);
   return launch_merge<HD>(a, s, true);
 }
 

@@ -460,11 +460,13 @@ def test_attention_physical_placement_invariance(gpu):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "q8_0", "f32"])
-@pytest.mark.parametrize("n_batch", [5, 300])
+@pytest.mark.parametrize("n_batch", [5, 200, 300])
 def test_attention_batch_independence(gpu, dtype, n_batch):
     """A query's output is bit-identical alone and inside a batch (the
     reference's batching property, engine/README.md:102), for small batches
-    and for ones that fill every SIMD."""
+    and for ones that fill every SIMD: batches of up to 256 queries take
+    their work items longest first (200: four 64-query rounds of the order
+    scan), larger ones in query order, a query alone in query order."""
     import torch
 
     rng = np.random.default_rng(15 + n_batch)
