@@ -178,7 +178,9 @@ LTKV_API int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs);
 /* Kernel 3, gather: KvCache::rows(layer, seq, len) collected (kv.rs:133-150)
  * for n sequences. Sequence i has table d_tables[i*table_stride ...] and
  * length d_lens[i] <= table_stride*16; its rows go to row d_out_offsets[i]
- * onward of d_k_out / d_v_out ([rows][kv_dim], cache dtype), bit-exact. */
+ * onward of d_k_out / d_v_out ([rows][kv_dim], cache dtype), bit-exact. A
+ * table entry outside the pool copies nothing and is reported by
+ * ltkv_synchronize (the reference panics, kv.rs:147). */
 LTKV_API int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
                 size_t table_stride, const int32_t *d_lens, const int64_t *d_out_offsets,
                 void *d_k_out, void *d_v_out);
@@ -189,7 +191,8 @@ LTKV_API int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d
  * d_tables[i*table_stride]; query head h uses kv head h/(n_heads/n_kv_heads).
  * Softmax of q.k*scale over the positions, times V; d_out is
  * [n][n_heads*head_dim] f32. head_dim in {64,128}; group size <= 8.
- * d_lens[i] == 0 yields zeros. */
+ * d_lens[i] == 0 yields zeros. A table entry outside the pool is read as
+ * block 0 and reported by ltkv_synchronize (the reference panics, kv.rs:147). */
 LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                           float scale, const float *d_q, const int32_t *d_tables,
                           size_t table_stride, const int32_t *d_lens, float *d_out);
@@ -225,8 +228,10 @@ LTKV_API int ltkv_decode_attention_noalloc(ltkv_cache *c, size_t layer, size_t n
  * d_lens[i] - 1 of query i's table (the cell the step's claim returned for
  * that query) and no two queries may read one sequence's new cells (one new
  * token per sequence, as in a decode step); then results and pools are
- * bit-identical to ltkv_write followed by ltkv_decode_attention. A negative
- * or out-of-range cell is skipped, as by ltkv_write. On f16 pools the
+ * bit-identical to ltkv_write followed by ltkv_decode_attention (a cell that
+ * is not position d_lens[i] - 1 is reported by ltkv_synchronize as
+ * LTKV_ERR_ARG). A negative or out-of-range cell is skipped, as by
+ * ltkv_write. On f16 pools the
  * attention kernel writes and uses each new row itself; on f32 and Q8_0
  * pools this is ltkv_write followed by ltkv_decode_attention. No reference
  * counterpart: the reference writes then attends per layer. */
@@ -351,7 +356,18 @@ LTKV_API int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void
 LTKV_API int ltkv_write_row(ltkv_cache *c, size_t layer, uint32_t block, uint32_t slot, const float *h_k,
                    const float *h_v);
 
-/* Wait for all work enqueued on the cache's stream. */
+/* Wait for all work enqueued on the cache's stream, then report (and clear)
+ * the faults the device ops met since the last call, which they cannot return
+ * themselves (they are asynchronous). Where the reference panics — an index
+ * past a sequence's blocks in rows() (kv.rs:147) — a device op instead
+ * continues safely and this call returns:
+ *   LTKV_ERR_RANGE  a block-table entry outside the pool was read by attention
+ *                   (which used block 0 in its place) or by gather (which copied
+ *                   nothing for it), or a resident-table row outside the tables
+ *                   came with a nonzero length;
+ *   LTKV_ERR_ARG    a fused append + attention cell (ltkv_append_decode_attention)
+ *                   was not position lens[i] - 1 of query i's table.
+ * ltkv_last_error() names the query (or gathered sequence). */
 LTKV_API int ltkv_synchronize(ltkv_cache *c);
 
 #ifdef __cplusplus

@@ -132,6 +132,12 @@ struct ltkv_cache {
   int32_t *d_order_counts = nullptr, *d_order_pairs = nullptr;
   size_t order_cap = 0;  // pairs
 
+  // Fault word of the device ops (int32[2], zeroed at creation): kernels OR
+  // in fault bits (a block-table entry outside the pool, a fused append's
+  // cell that is not the query's position len - 1); ltkv_synchronize reports
+  // and clears them.
+  int32_t *d_status = nullptr;
+
   // Attention workspace (partition partials), grown on demand.
   uint8_t *ws = nullptr;
   size_t ws_bytes = 0;
@@ -510,6 +516,7 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   a.part_tokens = part;
   a.max_parts = max_parts;
   a.split = 1;
+  a.status = c->d_status;
   return a;
 }
 
@@ -926,6 +933,10 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
     else if ((e = hipMemset(c->k, c->q8() ? 0x80 : 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(K pool)");
     else if ((e = hipMemset(c->v, c->q8() ? 0x80 : 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
   }
+  if (rc == LTKV_OK) {
+    if ((e = hipMalloc((void **)&c->d_status, 2 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMalloc(status)");
+    else if ((e = hipMemset(c->d_status, 0, 2 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMemset(status)");
+  }
   const size_t sbytes = c->q8() ? n_layers * c->layer_scales() * 2 : 0;
   if (rc == LTKV_OK && sbytes > 0) {
     if ((e = hipMalloc(&c->ks, sbytes)) != hipSuccess) rc = hip_fail(e, "hipMalloc(K scales)");
@@ -957,6 +968,7 @@ void ltkv_destroy(ltkv_cache *c) {
     if (c->d_order_counts) (void)hipFree(c->d_order_counts);
     if (c->d_order_pairs) (void)hipFree(c->d_order_pairs);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->d_status) (void)hipFree(c->d_status);
     if (c->rope) (void)hipFree(c->rope);
     if (c->plan.done) (void)hipEventDestroy(c->plan.done);
     if (c->plan.h) (void)hipHostFree(c->plan.h);
@@ -1250,7 +1262,7 @@ int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   HIP_TRY(ltkv::launch_gather(c->geom, c->k_layer(layer), c->v_layer(layer), d_tables,
                               (int64_t)table_stride, d_lens, d_out_offsets, (int64_t)n, d_k_out,
-                              d_v_out, c->stream),
+                              d_v_out, c->d_status, c->stream),
           "gather launch");
   return LTKV_OK;
 }
@@ -1470,7 +1482,18 @@ int ltkv_read_resident_tables(ltkv_cache *c, int32_t *h_tables, int32_t *h_lengt
                          c->stream),
           "hipMemcpyAsync(resident table lengths)");
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  return LTKV_OK;
+  int32_t st[2] = {0, 0};
+  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
+  if (st[0] == 0) return LTKV_OK;
+  const int32_t zero[2] = {0, 0};
+  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
+  if (st[0] & 1)  // kv.rs:147 panics on such an index
+    return fail(LTKV_ERR_RANGE,
+                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
+                "block 0 in its place (attention) or copied nothing (gather)",
+                st[1]);
+  return fail(LTKV_ERR_ARG,
+              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
 }
 
 int ltkv_table_uploads(const ltkv_cache *c, uint64_t *entries) {
@@ -1596,7 +1619,18 @@ int ltkv_synchronize(ltkv_cache *c) {
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  return LTKV_OK;
+  int32_t st[2] = {0, 0};
+  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
+  if (st[0] == 0) return LTKV_OK;
+  const int32_t zero[2] = {0, 0};
+  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
+  if (st[0] & 1)  // kv.rs:147 panics on such an index
+    return fail(LTKV_ERR_RANGE,
+                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
+                "block 0 in its place (attention) or copied nothing (gather)",
+                st[1]);
+  return fail(LTKV_ERR_ARG,
+              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
 }
 
 int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v) {
@@ -1629,7 +1663,18 @@ int ltkv_read_scales(ltkv_cache *c, size_t layer, uint16_t *h_k, uint16_t *h_v) 
   HIP_TRY(hipMemcpyAsync(h_k, c->k_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read K scales");
   HIP_TRY(hipMemcpyAsync(h_v, c->v_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read V scales");
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  return LTKV_OK;
+  int32_t st[2] = {0, 0};
+  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
+  if (st[0] == 0) return LTKV_OK;
+  const int32_t zero[2] = {0, 0};
+  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
+  if (st[0] & 1)  // kv.rs:147 panics on such an index
+    return fail(LTKV_ERR_RANGE,
+                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
+                "block 0 in its place (attention) or copied nothing (gather)",
+                st[1]);
+  return fail(LTKV_ERR_ARG,
+              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
 }
 
 int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v) {
@@ -1663,7 +1708,7 @@ int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, vo
   if (e == hipSuccess)
     e = ltkv::launch_gather(c->geom, c->k_layer(layer), c->v_layer(layer), (const int32_t *)d,
                             (int64_t)tb, (const int32_t *)(d + tb * 4), (const int64_t *)(d + off_pos),
-                            1, d + meta, d + meta + n * row_bytes, c->stream);
+                            1, d + meta, d + meta + n * row_bytes, c->d_status, c->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(h_k, d + meta, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(h_v, d + meta + n * row_bytes, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();

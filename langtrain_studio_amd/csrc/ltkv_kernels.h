@@ -63,10 +63,12 @@ int64_t copy_order_buckets(int64_t n_blocks);
 hipError_t launch_copy_order(const int32_t *pairs, int64_t n_pairs, int64_t n_blocks, int32_t *counts,
                              int32_t *cursors, int32_t *sorted, hipStream_t s);
 
+// Table entries outside the pool are not copied and set kFaultTable in
+// status[0] (see AttnArgs::status).
 hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_layer,
                          const int32_t *tables, int64_t table_stride, const int32_t *lens,
                          const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
-                         hipStream_t s);
+                         int32_t *status, hipStream_t s);
 
 // Resident block tables: updates (row, col, value) triples (col -1: the
 // row's length in blocks), and the slot mapping of (row, position) tokens.
@@ -121,6 +123,11 @@ struct AttnArgs {
   int max_pre_parts;
   // Queries the launch covers: qmap[0..n) (query indices), or all n when null.
   const int32_t *qmap;
+  // Fault word (int32[2], or nullptr): a table entry outside the pool that a
+  // query's context covers (read as block 0) ORs 1 into status[0], a fused
+  // append whose cell is not position lens[i] - 1 of the query's table ORs
+  // 2; status[1] gets the query. Kernels only ever set bits.
+  int32_t *status;
 };
 
 // Context tokens per attention partition when none is fixed: four

@@ -51,6 +51,10 @@ typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) hf4 lds_hf4;
 typedef __attribute__((address_space(3))) char lds_char;
 
+// Fault bits of a cache's status word (reported by ltkv_synchronize).
+constexpr int kFaultTable = 1;      // a block-table entry outside the pool
+constexpr int kFaultFusedCell = 2;  // a fused append's cell is not position len - 1 of its table
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
 // i % 4 of the 8 bytes addressed by lane 4 j + i / 4 as its element j.
 __device__ __forceinline__ hf4 lds_read_tr(const char *p) {
@@ -562,7 +566,7 @@ gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpo
               const int32_t *__restrict__ tables, int64_t table_stride,
               const int32_t *__restrict__ lens, const int64_t *__restrict__ out_offsets,
               uint8_t *__restrict__ kout, uint8_t *__restrict__ vout, int64_t n_blocks,
-              int64_t row_bytes, int chunks) {
+              int64_t row_bytes, int chunks, int32_t *__restrict__ status) {
   const int64_t per_entry = 2 * (int64_t)chunks;
   const int64_t entry = blockIdx.x / per_entry;
   const int part = (int)(blockIdx.x - entry * per_entry);
@@ -576,7 +580,13 @@ gather_kernel(const uint8_t *__restrict__ kpool, const uint8_t *__restrict__ vpo
   if (start >= len) return;
   const int64_t rows = len - start < 16 ? len - start : 16;
   const int32_t blk = tables[seq * table_stride + j];
-  if (blk < 0 || blk >= n_blocks) return;
+  if (blk < 0 || blk >= n_blocks) {  // kv.rs:147 panics here; nothing is copied
+    if (threadIdx.x == 0 && status) {
+      __hip_atomic_fetch_or(status, kFaultTable, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      status[1] = (int32_t)seq;
+    }
+    return;
+  }
   const int64_t i = (int64_t)chunk * kGatherChunk + threadIdx.x;
   if (i >= (rows * row_bytes) >> 4) return;
   const u32x4 *src = reinterpret_cast<const u32x4 *>((is_v ? vpool : kpool) +
@@ -645,6 +655,34 @@ __device__ __forceinline__ const int32_t *table_of(const int32_t *tables, int64_
   return tables + r * stride;
 }
 
+// Faults a device op met, for ltkv_synchronize to report (the reference
+// panics at the same places): status[0] ORs the fault bits, status[1] holds
+// the query of one of them. The op goes on safely (a bad entry reads block
+// 0), so nothing faults on the GPU.
+__device__ __forceinline__ void report_fault(int32_t *status, int code, int64_t qi) {
+  if (!status || (threadIdx.x & 63) != 0) return;
+  __hip_atomic_fetch_or(status, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  status[1] = (int32_t)qi;
+}
+
+// Checks the table entries of blocks [b0, b1) (the positions a work-group
+// reads: kv.rs:147 indexes the sequence's blocks with them) and the query's
+// row in the resident tables; run once before the tile loop, one wave.
+__device__ __forceinline__ void check_table(const int32_t *tab, int b0, int b1, int64_t n_blocks,
+                                            const int32_t *rows, int64_t n_rows, int64_t qi, int32_t *status) {
+  if (!status || b1 <= b0) return;
+  bool bad = false;
+  if (rows) {
+    const int32_t r = rows[qi];
+    bad = r < 0 || r >= n_rows;  // such a query must have length 0
+  }
+  for (int b = b0 + (int)(threadIdx.x & 63); b < b1 && !bad; b += 64) {
+    const int32_t blk = tab[b];
+    bad = blk < 0 || blk >= n_blocks;
+  }
+  if (__builtin_amdgcn_ballot_w64(bad)) report_fault(status, kFaultTable, qi);
+}
+
 template <typename T, int HD, int G>
 __global__ void __launch_bounds__(256)
 attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
@@ -654,7 +692,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
             int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
             int max_parts, const int32_t *__restrict__ pre_parts,
             const int32_t *__restrict__ qmap, const int32_t *__restrict__ rows, int64_t n_rows,
-            int64_t max_len) {
+            int64_t max_len, int32_t *__restrict__ status) {
   constexpr int E = Tile<T>::E;
   constexpr int L = HD / E;        // lanes per row
   constexpr int RPL = 64 / L;      // rows per wave load
@@ -710,6 +748,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
   }
 
   const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
+  check_table(tab, b0, b1, n_blocks, rows, n_rows, qi, status);
   const int64_t lane_off = (int64_t)rg * slot_stride + c * E;
   const int64_t head_off = (int64_t)kvh * head_stride;
 
@@ -1099,7 +1138,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
               int64_t slot_stride, int64_t head_stride, float qscale, int part_tokens,
               int max_parts, const int32_t *__restrict__ pre_parts,
               const int32_t *__restrict__ qmap, const int32_t *__restrict__ rows, int64_t n_rows,
-            int64_t max_len) {
+            int64_t max_len, int32_t *__restrict__ status) {
   constexpr int E = Tile<T>::E;
   static_assert(HD / E == 16, "16 lanes per row");
   constexpr int RPL = 4, LOADS = 4;                             // rows per wave load, loads per tile
@@ -1209,6 +1248,7 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
     for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
 
   const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
+  check_table(tab, b0, b1, n_blocks, rows, n_rows, qi, status);
 
   // A tile is read through buffer descriptors whose extent ends at the last
   // row inside the context: rows past it (and every row of a prefetch past
@@ -1625,7 +1665,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
                  int max_pre_parts, const int32_t *__restrict__ new_slots,
                  const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
-                 T *kdst, T *vdst, int64_t n_queries, int order) {
+                 T *kdst, T *vdst, int64_t n_queries, int order, int32_t *__restrict__ status) {
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -1752,6 +1792,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
+  check_table(tab, b0, b1, n_blocks, rows, n_rows, qi, status);
 
   // Fused append (f16, decode steps): the wave of the query's last partition
   // writes the query's new K/V row (position len - 1, cell new_slots[qi]) of
@@ -1763,6 +1804,10 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   if constexpr (!Q8) {
     if (new_slots && part == np - 1 && len > 0) {  // uniform
       const int32_t cell = new_slots[qi];
+      // The cell must be position len - 1 of the query's table (what the
+      // claim returned for it); otherwise write-then-attend would differ.
+      if (cell >= 0 && (int64_t)tab[(len - 1) >> 4] * 16 + ((len - 1) & 15) != (int64_t)cell)
+        report_fault(status, kFaultFusedCell, qi);
       if (cell >= 0 && (int64_t)cell < n_blocks * 16) {
         b_new = (int)((len - 1) >> 4);
         r_new = (int)((len - 1) & 15);
@@ -2069,7 +2114,7 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
       a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts, a.new_slots, a.new_k, a.new_v, a.new_stride,
       static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)), a.n,
-      decode_ordered(a) ? 1 : 0);
+      decode_ordered(a) ? 1 : 0, a.status);
   return launch_merge<HD>(a, s, true);
 }
 
@@ -2080,7 +2125,7 @@ hipError_t launch_attn16_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) 
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
+      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len, a.status);
   return launch_merge<HD>(a, s, false);
 }
 
@@ -2091,7 +2136,7 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables,
       a.table_stride, a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks,
       g.block_stride, g.slot_stride, g.head_stride, a.scale * kLog2e, a.part_tokens, a.max_parts,
-      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len);
+      a.pre_parts, a.qmap, a.rows, a.n_rows, a.max_len, a.status);
   return launch_merge<HD>(a, s, false);
 }
 
@@ -2693,7 +2738,7 @@ hipError_t launch_copy_order(const int32_t *pairs, int64_t n_pairs, int64_t n_bl
 hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_layer,
                          const int32_t *tables, int64_t table_stride, const int32_t *lens,
                          const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
-                         hipStream_t s) {
+                         int32_t *status, hipStream_t s) {
   if (n <= 0 || table_stride <= 0) return hipSuccess;
   const int64_t row_bytes = (int64_t)g.kv_dim * g.elem;
   // A block's K (or V) is 16 rows = row_bytes 16-byte vectors.
@@ -2703,7 +2748,7 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
   gather_kernel<<<(unsigned)wgs, kGatherThreads, 0, s>>>(
       static_cast<const uint8_t *>(k_layer), static_cast<const uint8_t *>(v_layer), tables,
       table_stride, lens, out_offsets, static_cast<uint8_t *>(k_out),
-      static_cast<uint8_t *>(v_out), g.n_blocks, row_bytes, chunks);
+      static_cast<uint8_t *>(v_out), g.n_blocks, row_bytes, chunks, status);
   return hipGetLastError();
 }
 

@@ -86,6 +86,36 @@ def test_write_row_strided_source(gpu):
     _assert_pools_equal(g, o, (0,))
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_write_bulk_streaming(gpu, dtype):
+    """An append whose sources exceed the 256 MB last-level cache (40 000 rows
+    of kv_dim 1024, 328 MB of f32 K and V) takes the streaming form (two rows
+    a thread, non-temporal loads): the pools equal the oracle's bit for bit,
+    skipped and out-of-range slots are left alone (including a missing
+    second row of an odd count), then a second streaming append and a
+    cached-size one follow."""
+    import torch
+
+    rng = np.random.default_rng(43)
+    kv_dim, n = 1024, 40000
+    n_blocks = n // BLOCK + 64
+    g, o = _caches(1, kv_dim, n_blocks * BLOCK, dtype, rng.permutation(n_blocks))
+    seqs = np.repeat(np.arange(n // 500, dtype=np.uint32), 500)
+    pos = np.tile(np.arange(500, dtype=np.uint64), n // 500)
+    sm = g.append_batch(seqs, pos)
+    np.testing.assert_array_equal(sm, o.append_batch(seqs, pos))
+    sm = sm.copy()
+    sm[rng.choice(n, 50, replace=False)] = -1
+    sm[rng.choice(n, 5, replace=False)] = n_blocks * BLOCK + 3
+    for rows in (n, 33001, 4000):
+        k = rng.standard_normal((rows, kv_dim), dtype=np.float32)
+        v = rng.standard_normal((rows, kv_dim), dtype=np.float32)
+        g.write_batch(0, torch.from_numpy(sm[:rows]).to(gpu), torch.from_numpy(k).to(gpu),
+                      torch.from_numpy(v).to(gpu))
+        o.write_batch(0, np.where(sm[:rows] >= n_blocks * BLOCK, -1, sm[:rows]), k, v)  # skipped on the GPU
+        _assert_pools_equal(g, o, (0,))
+
+
 # ---------------------------------------------------------------------------- kv.rs tests, on the GPU cache
 def test_share_then_diverge_copies_on_write(gpu):
     """kv.rs:202-217 with the K/V data living in HBM (kv_dim 8: the ABI needs a multiple of 8)."""
