@@ -81,8 +81,9 @@ LTKV_API const char *ltkv_last_error(void);
 
 /* KvCache::new(n_layers, kv_dim, n_tokens) (kv.rs:35-48): ceil(n_tokens/16)
  * blocks, zero-filled K and V pools on HIP device `device` (or none for
- * LTKV_NO_DEVICE), free stack (0..n_blocks).rev(). kv_dim must be a
- * multiple of 8. */
+ * LTKV_NO_DEVICE), free stack (0..n_blocks).rev(). Any kv_dim >= 1 (Q8_0:
+ * a multiple of 32); rows whose byte length is a multiple of 16 take the
+ * vectorised kernels, others element-wise ones. */
 LTKV_API int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int device,
                 ltkv_cache **out);
 LTKV_API void ltkv_destroy(ltkv_cache *c);
@@ -190,7 +191,9 @@ LTKV_API int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d
  * attends over positions 0..d_lens[i]-1 of the table at
  * d_tables[i*table_stride]; query head h uses kv head h/(n_heads/n_kv_heads).
  * Softmax of q.k*scale over the positions, times V; d_out is
- * [n][n_heads*head_dim] f32. head_dim in {64,128}; group size <= 8.
+ * [n][n_heads*head_dim] f32. Any group size and head_dim <= 1024: head_dim
+ * 64 or 128 with groups of 1..8 take the tuned kernels, other shapes a
+ * generic one (one work-group per query head, whole contexts).
  * d_lens[i] == 0 yields zeros. A table entry outside the pool is read as
  * block 0 and reported by ltkv_synchronize (the reference panics, kv.rs:147). */
 LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,

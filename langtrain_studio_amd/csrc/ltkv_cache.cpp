@@ -372,8 +372,7 @@ int check_attention_shape(const ltkv_cache *c, size_t n_heads, size_t head_dim, 
     return fail(LTKV_ERR_ARG, "n_heads %zu is not a multiple of n_kv_heads %zu", n_heads, n_kv_heads);
   *group = n_heads / n_kv_heads;
   if (!ltkv::attention_supported((int)c->elem, (int)head_dim, (int)*group))
-    return fail(LTKV_ERR_ARG, "unsupported shape: head_dim %zu (64 or 128), group %zu (1..8)", head_dim,
-                *group);
+    return fail(LTKV_ERR_ARG, "unsupported shape: head_dim %zu (at most 1024), group %zu", head_dim, *group);
   return LTKV_OK;
 }
 
@@ -608,7 +607,10 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   std::vector<Group> groups;
   std::vector<size_t> pre_tokens(n, 0);  // context of query i covered by its group
   const size_t n_kv_heads = c->kv_dim / head_dim;
-  if ((flags & LTKV_PLAN_SHARED_PREFIX) && ltkv::mq_supported((int)c->elem, (int)head_dim, (int)group)) {
+  // Groups need the shared-prefix kernel and a per-query pass that folds
+  // their partials (the tuned decode kernels); other shapes plan per query.
+  if ((flags & LTKV_PLAN_SHARED_PREFIX) && ltkv::mq_supported((int)c->elem, (int)head_dim, (int)group) &&
+      ltkv::attention_tuned((int)c->elem, (int)head_dim, (int)group)) {
     std::vector<char> taken(n, 0);
     {
       std::unordered_map<uint32_t, size_t> seq_of;
@@ -862,8 +864,7 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
                 ltkv_cache **out) {
   if (!out) return fail(LTKV_ERR_ARG, "out is null");
   *out = nullptr;
-  if (n_layers == 0 || kv_dim == 0 || kv_dim % 8 != 0)
-    return fail(LTKV_ERR_ARG, "n_layers must be > 0 and kv_dim a positive multiple of 8");
+  if (n_layers == 0 || kv_dim == 0) return fail(LTKV_ERR_ARG, "n_layers and kv_dim must be > 0");
   if (dtype != LTKV_F16 && dtype != LTKV_F32 && dtype != LTKV_Q8_0)
     return fail(LTKV_ERR_ARG, "dtype must be F16, F32 or Q8_0");
   if (dtype == LTKV_Q8_0 && kv_dim % 32 != 0)
@@ -1097,11 +1098,15 @@ int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapp
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
   if (n == 0) return LTKV_OK;
   if (!d_slot_mapping || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
-  if (src_stride < c->kv_dim || src_stride % 4 != 0)
-    return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
-  if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0) return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
-  if ((uint64_t)n * (c->kv_dim / 8) >= (1ull << 32) - 256)
-    return fail(LTKV_ERR_ARG, "too many rows for one launch");
+  if (src_stride < c->kv_dim) return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim");
+  if (c->kv_dim % 8 == 0) {  // 16-byte row pieces (other row lengths move element-wise)
+    if (src_stride % 4 != 0) return fail(LTKV_ERR_ARG, "src_stride must be a multiple of 4");
+    if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0)
+      return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
+  } else if (((uintptr_t)d_k | (uintptr_t)d_v) % 4 != 0) {
+    return fail(LTKV_ERR_ARG, "K/V must be 4-byte aligned");
+  }
+  if ((uint64_t)n * c->kv_dim >= (1ull << 40)) return fail(LTKV_ERR_ARG, "too many rows for one launch");
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   if (c->q8())
@@ -1390,7 +1395,8 @@ int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n
   if (src_stride < c->kv_dim || src_stride % 4 != 0)
     return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
   if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0) return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
-  if (c->elem != 2) {  // fused only on f16 pools: append, then attention, as two launches
+  if (c->elem != 2 || !ltkv::attention_tuned(2, (int)head_dim, (int)group)) {
+    // fused only on f16 pools of the tuned shapes: append, then attention, as two launches
     if (int rc = ltkv_write(c, layer, n, d_slot_mapping, d_k, d_v, src_stride)) return rc;
     return ltkv_decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride,
                                  d_lens, d_out);

@@ -157,6 +157,10 @@ struct AttnWorkspace {
 // path merges them with shared-prefix partials).
 AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_parts,
                                   bool always = false);
+// Shapes of the tuned decode kernels (head_dim 64 or 128, group 1..8) and of
+// every kernel (any group, head_dim up to 1024: the generic kernel, one
+// work-group per query head, no partitions, no group partials).
+bool attention_tuned(int elem, int head_dim, int group);
 bool attention_supported(int elem, int head_dim, int group);
 // Decode kernels on f16 and q8_0 pools read two adjacent kv heads per wave
 // when the group has at most 4 query heads and the kv heads pair up (the

@@ -2065,15 +2065,19 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
           float mx = mref;
 #pragma unroll
           for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pm[u]);  // clamped: a repeat, harmless
-          const float nref = mx == -INFINITY ? 0.f : mx;
-          const float a0 = __builtin_amdgcn_exp2f(mref - nref);
+          // While every reference seen is -inf (empty partials, empty own
+          // range) the running reference stays -inf and nothing is added; it
+          // never takes a finite placeholder that later rounds would use as a
+          // floor.
+          const bool any = mx != -INFINITY;
+          const float a0 = any ? __builtin_amdgcn_exp2f(mref - mx) : 1.f;
           l_run *= a0;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
-          mref = nref;
+          mref = any ? mx : mref;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const float a = p0 + u < npre ? __builtin_amdgcn_exp2f(pm[u] - mref) : 0.f;
+            const float a = p0 + u < npre && any ? __builtin_amdgcn_exp2f(pm[u] - mref) : 0.f;
             l_run += pl[u] * a;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a;
@@ -2588,6 +2592,178 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 }
 
 // ----------------------------------------------------------------------------
+// Generic forms for the shapes the kernels above do not cover. The reference
+// takes any shape (model.rs:401-402 reads head_dim and the group from the
+// model; its own cache test uses kv_dim 4, kv.rs:202-229): rows whose byte
+// length is not a multiple of 16 move element by element, and attention with
+// a head_dim other than 64 / 128 or a group above 8 runs on the vector ALU
+// with one work-group per (query, query head). They are correct for any
+// shape and serve the families the tuned kernels do not; the tuned kernels
+// stay the path for every shape they cover.
+// ----------------------------------------------------------------------------
+
+// Append of one element of K and of V per thread (any kv_dim).
+template <int ELEM>
+__global__ void __launch_bounds__(256)
+write_any_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool, const int32_t *__restrict__ slots,
+                 const float *__restrict__ k, const float *__restrict__ v, int64_t n, int64_t src_stride,
+                 int64_t kv_dim, int64_t n_slots) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / kv_dim;
+  if (row >= n) return;
+  const int64_t e = gid - row * kv_dim;
+  const int32_t s = slots[row];
+  if (s < 0 || (int64_t)s >= n_slots) return;
+  const int64_t dst = (int64_t)s * kv_dim + e;
+  const float kx = k[row * src_stride + e], vx = v[row * src_stride + e];
+  if constexpr (ELEM == 2) {
+    reinterpret_cast<uint16_t *>(kpool)[dst] = (uint16_t)f16_bits(kx);
+    reinterpret_cast<uint16_t *>(vpool)[dst] = (uint16_t)f16_bits(vx);
+  } else {
+    reinterpret_cast<float *>(kpool)[dst] = kx;
+    reinterpret_cast<float *>(vpool)[dst] = vx;
+  }
+}
+
+// Gather with element-wise moves: work-group = (sequence, table entry, K or V).
+template <typename E>
+__global__ void __launch_bounds__(256)
+gather_any_kernel(const E *__restrict__ kpool, const E *__restrict__ vpool, const int32_t *__restrict__ tables,
+                  int64_t table_stride, const int32_t *__restrict__ lens, const int64_t *__restrict__ out_offsets,
+                  E *__restrict__ kout, E *__restrict__ vout, int64_t n_blocks, int64_t kv_dim,
+                  int32_t *__restrict__ status) {
+  const int is_v = (int)(blockIdx.x & 1);
+  const int64_t entry = blockIdx.x >> 1;
+  const int64_t seq = entry / table_stride;
+  const int64_t j = entry - seq * table_stride;
+  int64_t len = lens[seq];
+  if (len > table_stride * 16) len = table_stride * 16;
+  const int64_t start = j * 16;
+  if (start >= len) return;
+  const int64_t rows = len - start < 16 ? len - start : 16;
+  const int32_t blk = tables[seq * table_stride + j];
+  if (blk < 0 || blk >= n_blocks) {  // kv.rs:147 panics here; nothing is copied
+    if (threadIdx.x == 0 && status) {
+      __hip_atomic_fetch_or(status, kFaultTable, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      status[1] = (int32_t)seq;
+    }
+    return;
+  }
+  const E *src = (is_v ? vpool : kpool) + (int64_t)blk * 16 * kv_dim;
+  E *dst = (is_v ? vout : kout) + (out_offsets[seq] + start) * kv_dim;
+  for (int64_t i = threadIdx.x; i < rows * kv_dim; i += 256) dst[i] = src[i];
+}
+
+constexpr int kAnyThreads = 256;
+constexpr int kAnyMaxHeadDim = 1024;  // four output elements per thread
+constexpr int kAnyD = kAnyMaxHeadDim / kAnyThreads;
+
+// Block-wide max / sum over the 256 threads (every thread gets it).
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float x, float *red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float y = __shfl_xor(x, off, 64);
+    x = MAX ? __builtin_fmaxf(x, y) : x + y;
+  }
+  __syncthreads();  // red may still be read by the previous reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  const float a = red[0], b = red[1], c = red[2], d = red[3];
+  return MAX ? __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d)) : (a + b) + (c + d);
+}
+
+// Element e of a pool row of cell `cell` (block * 16 + slot) as f32: f16 and
+// f32 as stored, q8_0 as d * q (quant byte q + 128, scale d of the element's
+// 32-element group, [block][kv_dim / 32][16 slots]).
+template <typename T>
+__device__ __forceinline__ float pool_elem(const T *pool, const uint16_t *scales, int64_t cell, int64_t kv_dim,
+                                           int64_t e) {
+  if constexpr (std::is_same_v<T, int8_t>) {
+    const int q = (int)(uint8_t)pool[cell * kv_dim + e] - 128;
+    const uint16_t d = scales[((cell >> 4) * (kv_dim >> 5) + (e >> 5)) * 16 + (cell & 15)];
+    return (float)q * (float)__builtin_bit_cast(_Float16, d);
+  } else {
+    return (float)pool[cell * kv_dim + e];
+  }
+}
+
+// Work-group = (query, query head): 256 tokens per round, one score per
+// thread (a dot product over head_dim), softmax of the round against the
+// running reference (exp2 domain), then each thread accumulates up to four
+// output elements d = t + 256 k over the round's tokens.
+template <typename T>
+__global__ void __launch_bounds__(kAnyThreads)
+attn_any_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const uint16_t *__restrict__ kscale,
+                const uint16_t *__restrict__ vscale, const float *__restrict__ q, const int32_t *__restrict__ tables,
+                int64_t table_stride, const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
+                int group, int head_dim, int64_t n_blocks, int64_t kv_dim, float qscale,
+                const int32_t *__restrict__ rows, int64_t n_rows, int64_t max_len, const int32_t *__restrict__ qmap,
+                int32_t *__restrict__ status) {
+  __shared__ float sq[kAnyMaxHeadDim];
+  __shared__ float sp[kAnyThreads];
+  __shared__ int32_t sblk[kAnyThreads / 16];
+  __shared__ float red[4];
+  const int t = (int)threadIdx.x;
+  const int h = (int)(blockIdx.x % n_heads);
+  const int64_t qx = blockIdx.x / n_heads;
+  const int64_t qi = qmap ? qmap[qx] : qx;
+  const int64_t head_off = (int64_t)(h / group) * head_dim;
+  int64_t len = lens[qi];
+  if (len < 0) len = 0;
+  if (len > max_len) len = max_len;
+  const int64_t qh = qi * n_heads + h;
+  for (int d = t; d < head_dim; d += kAnyThreads) sq[d] = q[qh * head_dim + d] * qscale;
+  const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
+  if (t < 64) check_table(tab, 0, (int)((len + 15) >> 4), n_blocks, rows, n_rows, qi, status);
+  float m = -INFINITY, l = 0.f, o[kAnyD];
+#pragma unroll
+  for (int k = 0; k < kAnyD; ++k) o[k] = 0.f;
+  for (int64_t t0 = 0; t0 < len; t0 += kAnyThreads) {
+    const int n_tok = len - t0 < kAnyThreads ? (int)(len - t0) : kAnyThreads;
+    if (t < (n_tok + 15) / 16) {
+      int32_t blk = tab[(t0 >> 4) + t];
+      if (blk < 0 || blk >= n_blocks) blk = 0;  // reported by check_table
+      sblk[t] = blk;
+    }
+    __syncthreads();
+    float sc = -INFINITY;
+    if (t < n_tok) {
+      const int64_t cell = (int64_t)sblk[t >> 4] * 16 + ((t0 + t) & 15);
+      float acc = 0.f;
+      for (int d = 0; d < head_dim; ++d) acc += sq[d] * pool_elem(kpool, kscale, cell, kv_dim, head_off + d);
+      sc = acc;
+    }
+    const float mx = block_reduce<true>(sc, red);
+    const float mn = __builtin_fmaxf(m, mx);  // finite: the round has a token
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    const float p = t < n_tok ? __builtin_amdgcn_exp2f(sc - mn) : 0.f;
+    sp[t] = p;
+    l = l * alpha + block_reduce<false>(p, red);
+    m = mn;
+#pragma unroll
+    for (int k = 0; k < kAnyD; ++k) o[k] *= alpha;
+    __syncthreads();
+    for (int j = 0; j < n_tok; ++j) {
+      const int64_t cell = (int64_t)sblk[j >> 4] * 16 + ((t0 + j) & 15);
+      const float pj = sp[j];
+#pragma unroll
+      for (int k = 0; k < kAnyD; ++k) {
+        const int d = t + kAnyThreads * k;
+        if (d < head_dim) o[k] += pj * pool_elem(vpool, vscale, cell, kv_dim, head_off + d);
+      }
+    }
+    __syncthreads();  // sblk and sp are rewritten next round
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int k = 0; k < kAnyD; ++k) {
+    const int d = t + kAnyThreads * k;
+    if (d < head_dim) out[qh * head_dim + d] = o[k] * inv;
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Resident block tables (step descriptor): in-place updates and the slot
 // mapping of a batch's tokens.
 
@@ -2657,6 +2833,19 @@ hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const i
                         const float *k, const float *v, int64_t n, int64_t src_stride,
                         hipStream_t s) {
   if (n <= 0) return hipSuccess;
+  if (g.kv_dim % 8 != 0) {  // rows of any length: element-wise
+    const int64_t blocks = (n * g.kv_dim + 255) / 256;
+    if (blocks >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+    if (g.elem == 2)
+      write_any_kernel<2><<<(unsigned)blocks, 256, 0, s>>>(static_cast<uint8_t *>(k_layer),
+                                                           static_cast<uint8_t *>(v_layer), slots, k, v, n,
+                                                           src_stride, g.kv_dim, g.n_blocks * 16);
+    else
+      write_any_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(static_cast<uint8_t *>(k_layer),
+                                                           static_cast<uint8_t *>(v_layer), slots, k, v, n,
+                                                           src_stride, g.kv_dim, g.n_blocks * 16);
+    return hipGetLastError();
+  }
   constexpr int64_t kLastLevelCache = 256ll << 20;  // MALL bytes
   const bool stream = n * (int64_t)g.kv_dim * 8 > kLastLevelCache;
   if (g.elem == 2)
@@ -2741,6 +2930,21 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
                          int32_t *status, hipStream_t s) {
   if (n <= 0 || table_stride <= 0) return hipSuccess;
   const int64_t row_bytes = (int64_t)g.kv_dim * g.elem;
+  if (row_bytes % 16 != 0) {  // rows of any length: element-wise
+    const int64_t wgs = n * table_stride * 2;
+    if (wgs >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+    if (g.elem == 2)
+      gather_any_kernel<uint16_t><<<(unsigned)wgs, 256, 0, s>>>(
+          static_cast<const uint16_t *>(k_layer), static_cast<const uint16_t *>(v_layer), tables, table_stride,
+          lens, out_offsets, static_cast<uint16_t *>(k_out), static_cast<uint16_t *>(v_out), g.n_blocks,
+          g.kv_dim, status);
+    else
+      gather_any_kernel<uint32_t><<<(unsigned)wgs, 256, 0, s>>>(
+          static_cast<const uint32_t *>(k_layer), static_cast<const uint32_t *>(v_layer), tables, table_stride,
+          lens, out_offsets, static_cast<uint32_t *>(k_out), static_cast<uint32_t *>(v_out), g.n_blocks,
+          g.kv_dim, status);
+    return hipGetLastError();
+  }
   // A block's K (or V) is 16 rows = row_bytes 16-byte vectors.
   const int chunks = (int)((row_bytes + kGatherChunk - 1) / kGatherChunk);
   const int64_t wgs = n * table_stride * 2 * chunks;
@@ -2781,13 +2985,37 @@ AttnWorkspace attention_workspace(int64_t n, int n_heads, int head_dim, int max_
   return w;
 }
 
-bool attention_supported(int elem, int head_dim, int group) {
+bool attention_tuned(int elem, int head_dim, int group) {
   return (elem == 1 || elem == 2 || elem == 4) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
          group <= 8;
 }
 
+bool attention_supported(int elem, int head_dim, int group) {
+  return (elem == 1 || elem == 2 || elem == 4) && head_dim >= 1 && head_dim <= kAnyMaxHeadDim && group >= 1;
+}
+
+template <typename T>
+hipError_t launch_attn_any_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  const int64_t grid = a.n * a.n_heads;
+  if (grid >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  attn_any_kernel<T><<<(unsigned)grid, kAnyThreads, 0, s>>>(
+      static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer),
+      static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.q, a.tables,
+      a.table_stride, a.lens, a.out, a.n_heads, a.n_heads / a.n_kv_heads, a.head_dim, g.n_blocks, g.kv_dim,
+      a.scale * kLog2e, a.rows, a.n_rows, a.max_len, a.qmap, a.status);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
+  if (!attention_tuned(g.elem, a.head_dim, a.n_heads / a.n_kv_heads)) {
+    // the generic kernel takes whole contexts: no partials, no group partials
+    if (a.pre_parts || !attention_supported(g.elem, a.head_dim, a.n_heads / a.n_kv_heads))
+      return hipErrorInvalidValue;
+    if (g.elem == 1) return launch_attn_any_t<int8_t>(g, a, s);
+    if (g.elem == 2) return launch_attn_any_t<_Float16>(g, a, s);
+    return launch_attn_any_t<float>(g, a, s);
+  }
   if (g.elem == 1) {
     if (a.head_dim == 64) return launch_attn_hd<int8_t, 64>(g, a, s);
     if (a.head_dim == 128) return launch_attn_hd<int8_t, 128>(g, a, s);

@@ -61,24 +61,27 @@ def test_metadata_only_cache_rejects_device_ops():
 def test_create_argument_errors():
     from langtrain_studio_amd import KvCache, KvError
 
-    with pytest.raises(KvError, match="multiple of 8"):
-        KvCache(1, 12, 256, device=None)
-    with pytest.raises(KvError, match="multiple of 8"):
+    with pytest.raises(KvError, match="must be > 0"):
+        KvCache(1, 0, 256, device=None)
+    with pytest.raises(KvError, match="must be > 0"):
         KvCache(0, 64, 256, device=None)
+    with pytest.raises(KvError, match="multiple of 32"):
+        KvCache(1, 48, 256, dtype="q8_0", device=None)
+    KvCache(1, 4, 256, device=None)  # any kv_dim, as kv.rs:202-229 use 4
 
 
 def test_reference_known_answers_on_product_host_logic():
     """kv.rs:202-229 bookkeeping through the product's C ABI (no data)."""
     from langtrain_studio_amd import KvCache, NonContiguous
 
-    kv = KvCache(1, 8, 256, device=None)
+    kv = KvCache(1, 4, 256, device=None)
     for p in range(20):
         kv.append(0, p)
     kv.share(0, 1, 20)
     before = kv.free_blocks()
     assert kv.append(1, 20) == (2, 4)
     assert kv.free_blocks() == before - 1 and kv.len(0) == 20 and kv.cow_copies() == 1
-    kv = KvCache(1, 8, 64, device=None)
+    kv = KvCache(1, 4, 64, device=None)
     for p in range(40):
         kv.append(3, p)
     assert kv.free_blocks() == 1

@@ -118,11 +118,11 @@ def test_write_bulk_streaming(gpu, dtype):
 
 # ---------------------------------------------------------------------------- kv.rs tests, on the GPU cache
 def test_share_then_diverge_copies_on_write(gpu):
-    """kv.rs:202-217 with the K/V data living in HBM (kv_dim 8: the ABI needs a multiple of 8)."""
+    """kv.rs:202-217 with the K/V data living in HBM, at the test's own kv_dim 4."""
     from langtrain_studio_amd import KvCache
     from oracle import f16_to_f32
 
-    kv = KvCache(1, 8, 256, device=0)
+    kv = KvCache(1, 4, 256, device=0)
 
     def fill(seq, n, base):
         for p in range(kv.len(seq), n):
@@ -134,7 +134,7 @@ def test_share_then_diverge_copies_on_write(gpu):
     kv.share(0, 1, 20)
     free_before = kv.free_blocks()
     b, s = kv.append(1, 20)
-    kv.write(0, b, s, np.full(8, 1000.0, np.float32), np.full(8, 1000.0, np.float32))
+    kv.write(0, b, s, np.full(4, 1000.0, np.float32), np.full(4, 1000.0, np.float32))
     assert kv.free_blocks() == free_before - 1
     a = f16_to_f32(kv.rows(0, 0, 20)[0][:, 0])
     c = f16_to_f32(kv.rows(0, 1, 21)[0][:, 0])
@@ -144,13 +144,13 @@ def test_share_then_diverge_copies_on_write(gpu):
 
 
 def test_truncate_frees_blocks(gpu):
-    """kv.rs:219-229 on the GPU cache."""
+    """kv.rs:219-229 on the GPU cache, at the test's own kv_dim 4."""
     from langtrain_studio_amd import KvCache, NonContiguous
 
-    kv = KvCache(1, 8, 64, device=0)
+    kv = KvCache(1, 4, 64, device=0)
     for p in range(40):
         b, s = kv.append(3, p)
-        x = np.full(8, float(p), np.float32)
+        x = np.full(4, float(p), np.float32)
         kv.write(0, b, s, x, x)
     assert kv.free_blocks() == 1
     kv.truncate(3, 10)
