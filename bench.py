@@ -593,6 +593,8 @@ def bench_prefill(args):
     plan_us = (time.perf_counter() - t0) * 1e6
     reps = max(args.steps, 10)
     p_us = _time_op(lambda: kv.planned_attention(0, q, out=out), reps=reps)
+    kv.plan_attention(seqs, lens, n_heads, hd, shared_prefix=True, f16_products=True)
+    p16_us = _time_op(lambda: kv.planned_attention(0, q, out=out), reps=reps)
     tables = torch.from_numpy(kv.block_tables(seqs)).cuda()
     d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
     d_us = _time_op(lambda: kv.decode_attention(0, q, tables, d_lens, n_heads, hd, out=out), reps=reps)
@@ -604,6 +606,7 @@ def bench_prefill(args):
         "attention_us": round(p_us, 2), "TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 1),
         "mfma_frac": round(flops / (p_us * 1e-6) / 1e12 / PEAK_F16_MFMA_TFLOPS, 4),
         "kv_bytes": kv_bytes, "flops": flops,
+        "f16_products_us": round(p16_us, 2), "f16_products_TFLOPs": round(flops / (p16_us * 1e-6) / 1e12, 1),
         "plan": {k: stats[k] for k in ("groups", "grouped", "shared_blocks", "prefix_workgroups")},
         "plan_host_us": round(plan_us, 1),
         "attention_per_query_us": round(d_us, 2),
@@ -752,6 +755,18 @@ def bench_prefix_cow(args):
         ev[s][1].record()
     torch.cuda.synchronize()
     att_t = np.array([e[0].elapsed_time(e[1]) for e in ev]) * 1e3 / L
+    # The same plans with the grouped products on f16-rounded Q and weights
+    # (LTKV_PLAN_F16_PRODUCTS: ~3e-4 relative error instead of f32 accuracy).
+    for s in range(steps):
+        kv.plan_attention(seqs, lens[s], n_heads, hd, shared_prefix=True, f16_products=True)
+        write_step(s)
+        kv.planned_attention(L - 1, q[s], out=out)
+        ev[s][0].record()
+        for layer in range(L):
+            kv.planned_attention(layer, q[s], out=out)
+        ev[s][1].record()
+    torch.cuda.synchronize()
+    att16_t = np.array([e[0].elapsed_time(e[1]) for e in ev]) * 1e3 / L
     # The copy-on-write copies of step 0 again, timed alone (same pairs, all layers).
     dst = tables_h[:, prefix // BLOCK]
     pairs = np.stack([np.full(S, shared_last), dst], 1)[dst != shared_last].astype(np.int32)
@@ -779,6 +794,8 @@ def bench_prefix_cow(args):
         "tokens_per_s": round(S / (att_us * 1e-6), 1),
         "plan": {k: stats[k] for k in ("groups", "grouped", "shared_blocks", "prefix_workgroups")},
         "plan_host_us": round(float(np.mean(plan_s)) * 1e6, 1),
+        "attention_f16_products_us": round(float(att16_t.mean()), 2),
+        "attention_f16_products_frac_unique": round(float(np.mean(uniq / (att16_t * 1e-6) / 1e9 / PEAK_HBM_GBPS)), 4),
         "attention_per_query_us": round(flat_us, 2),
         "attention_per_query_frac_unique": round(float(np.mean(uniq / (flat_t * 1e-6) / 1e9 / PEAK_HBM_GBPS)), 4)}
     if not args.no_cpu:

@@ -32,6 +32,7 @@ pub mod ffi {
     pub const LTKV_F32: c_int = 1;
     pub const LTKV_Q8_0: c_int = 2;
     pub const LTKV_PLAN_SHARED_PREFIX: c_uint = 1;
+    pub const LTKV_PLAN_F16_PRODUCTS: c_uint = 2;
     pub const LTKV_NOALLOC_SCRATCH_BYTES: usize = 32 << 20;
 
     #[link(name = "ltkv")]
@@ -306,10 +307,13 @@ impl KvCache {
     }
 
     /// Plans one batch's attention (every layer of the step reuses it).
+    /// `f16_products`: grouped products on f16-rounded Q and weights (faster,
+    /// ~3e-4 relative error instead of f32 accuracy).
     pub fn plan_attention(&mut self, seqs: &[u32], lens: &[u32], n_heads: usize, head_dim: usize,
-                          shared_prefix: bool) -> anyhow::Result<()> {
+                          shared_prefix: bool, f16_products: bool) -> anyhow::Result<()> {
         anyhow::ensure!(seqs.len() == lens.len(), "seqs and lens differ in length");
-        let flags = if shared_prefix { LTKV_PLAN_SHARED_PREFIX } else { 0 };
+        let flags = (if shared_prefix { LTKV_PLAN_SHARED_PREFIX } else { 0 })
+            | (if f16_products { LTKV_PLAN_F16_PRODUCTS } else { 0 });
         check(unsafe { ltkv_plan_attention(self.raw, seqs.len(), seqs.as_ptr(), lens.as_ptr(), n_heads, head_dim, flags) })
     }
 

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libltkv.so"
 
 OK, ERR_FULL, ERR_NONCONTIG, ERR_RANGE, ERR_HIP, ERR_ARG = 0, 1, 2, 3, 4, 5
 F16, F32, Q8_0 = 0, 1, 2
+PLAN_SHARED_PREFIX, PLAN_F16_PRODUCTS = 1, 2
 NO_DEVICE = -1
 BLOCK = 16
 NOALLOC_SCRATCH_BYTES = 32 << 20  # LTKV_NOALLOC_SCRATCH_BYTES

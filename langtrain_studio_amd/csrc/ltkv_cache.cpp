@@ -79,6 +79,7 @@ struct AttnPlan {
   size_t n_pass = 0;         // queries of the per-query pass (the rest are completed by groups)
   size_t max_suffix = 0;     // longest remainder (tokens) of a per-query-pass query
   bool empty_with_groups = false;  // a query with group partials and no remainder
+  bool f16_products = false;       // LTKV_PLAN_F16_PRODUCTS
   size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0, off_qmap = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
   std::vector<int32_t> host;  // the arrays above, in device layout
@@ -1516,7 +1517,10 @@ int ltkv_plan_attention(ltkv_cache *c, size_t n, const uint32_t *seqs, const uin
   if (int rc = check_attention_shape(c, n_heads, head_dim, &group)) return rc;
   if (n && (!seqs || !lens)) return fail(LTKV_ERR_ARG, "null argument");
   if (n > (size_t)INT32_MAX / 64) return fail(LTKV_ERR_ARG, "batch of %zu queries is too large", n);
+  if (flags & ~(unsigned)(LTKV_PLAN_SHARED_PREFIX | LTKV_PLAN_F16_PRODUCTS))
+    return fail(LTKV_ERR_ARG, "unknown plan flags 0x%x", flags);
   if (int rc = build_plan(c, n, seqs, lens, n_heads, head_dim, group, flags)) return rc;
+  c->plan.f16_products = (flags & LTKV_PLAN_F16_PRODUCTS) != 0;
   if (c->device != LTKV_NO_DEVICE) {
     if (int rc = upload_plan(c)) return rc;
   }
@@ -1597,6 +1601,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
     m.head_dim = (int)P.head_dim;
     m.scale = scale;
     m.max_pre_parts = P.max_pre_parts;
+    m.f16_products = P.f16_products;
     // The two passes run one after the other: the shared-prefix kernel's
     // footprint (two waves per SIMD) leaves no room to overlap them.
     HIP_TRY(ltkv::launch_mq_attention(g, m, c->stream), "shared-prefix attention launch");

@@ -196,6 +196,9 @@ struct MqArgs {
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int max_pre_parts;
+  // Products with Q and P rounded to f16 (LTKV_PLAN_F16_PRODUCTS), else
+  // with f16 hi + lo pairs (f32 accuracy).
+  bool f16_products;
 };
 bool mq_supported(int elem, int head_dim, int group);
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s);

@@ -2226,7 +2226,10 @@ constexpr int kMqWaves = 4;  // waves per work-group
 template <int X>
 constexpr int kMqMinWaves = X >= 128 ? 1 : 2;
 
-template <typename T, int HD>
+// F16P: the products take Q and the softmax weights P rounded to f16, one
+// MFMA each (no lo parts): half the MFMA work and no split of P on the VALU,
+// at ~2^-12 relative error per operand (opt-in, LTKV_PLAN_F16_PRODUCTS).
+template <typename T, int HD, bool F16P>
 __global__ void __launch_bounds__(64 * kMqWaves, kMqMinWaves<HD / (int)sizeof(T)>)
 mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
                const float *__restrict__ q, const int32_t *__restrict__ tables,
@@ -2298,7 +2301,14 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) split_hl(x[ks], qh[rt][ks], ql[rt][ks]);
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (F16P) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qh[rt][ks][e] = (_Float16)x[ks][e];
+      } else {
+        split_hl(x[ks], qh[rt][ks], ql[rt][ks]);
+      }
+    }
   }
   // q8_0 K is staged as 1152 + k (exact in f16): 1152 times the row's sum of
   // each k step of Q (hi + lo) comes off every score of that step.
@@ -2310,7 +2320,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       for (int ks = 0; ks < KS; ++ks) {
         float t = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) t += (float)qh[rt][ks][e] + (float)ql[rt][ks][e];
+        for (int e = 0; e < 8; ++e) t += (float)qh[rt][ks][e] + (F16P ? 0.f : (float)ql[rt][ks][e]);
         t += __shfl_xor(t, 16);
         t += __shfl_xor(t, 32);
         qbias[rt][ks] = 1152.f * t;
@@ -2429,7 +2439,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
             f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], c, 0, 0, 0);
+            if constexpr (!F16P) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], c, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[tt][rt][i] = __builtin_fmaf((float)d[i], c[i] - qbias[rt][ks], sc[tt][rt][i]);
           }
@@ -2440,11 +2450,13 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt)
             sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], qh[rt][ks], sc[tt][rt], 0, 0, 0);
+        if constexpr (!F16P) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+          for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
-            sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
+            for (int rt = 0; rt < 2; ++rt)
+              sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
+        }
       }
     }
   };
@@ -2525,12 +2537,24 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
               x[j] = pf[rt][j] * (float)d0[j];
               x[4 + j] = pf[rt][4 + j] * (float)d1[j];
             }
-            split_hl(x, ph[rt], pl[rt]);
+            if constexpr (F16P) {
+#pragma unroll
+              for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)x[j];
+            } else {
+              split_hl(x, ph[rt], pl[rt]);
+            }
           }
         }
       } else if (dt == 0) {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) split_hl(pf[rt], ph[rt], pl[rt]);
+        for (int rt = 0; rt < 2; ++rt) {
+          if constexpr (F16P) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)pf[rt][j];
+          } else {
+            split_hl(pf[rt], ph[rt], pl[rt]);
+          }
+        }
       }
       // V^T operand: d = 16 dt + lr, tokens 4 lq + j (j < 4) and 16 + 4 lq + j - 4.
       const int col = (dt * 16 + 4 * (lr & 3)) * 2;
@@ -2540,9 +2564,11 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
         o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph[rt], o[dt][rt], 0, 0, 0);
+      if constexpr (!F16P) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl[rt], o[dt][rt], 0, 0, 0);
+        for (int rt = 0; rt < 2; ++rt)
+          o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl[rt], o[dt][rt], 0, 0, 0);
+      }
     }
   };
 
@@ -3057,10 +3083,16 @@ hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s
   auto run = [&](auto tag, auto hd) {
     using T = decltype(tag);
     constexpr int HD = decltype(hd)::value;
-    mq_attn_kernel<T, HD><<<grid, 64 * kMqWaves, 0, s>>>(
-        static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
-        a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
-        g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
+    if (a.f16_products)
+      mq_attn_kernel<T, HD, true><<<grid, 64 * kMqWaves, 0, s>>>(
+          static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
+          a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
+          g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
+    else
+      mq_attn_kernel<T, HD, false><<<grid, 64 * kMqWaves, 0, s>>>(
+          static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
+          a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
+          g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
     return hipGetLastError();
   };
   if (g.elem == 2 && a.head_dim == 128) return run(_Float16{}, std::integral_constant<int, 128>{});

@@ -48,11 +48,11 @@ def _forked(rng, kv_dim, dtype, spec, singles=(), n_layers=1):
     return g, o
 
 
-def _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, shared=True, layer=0, dtype="f16"):
+def _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, shared=True, layer=0, dtype="f16", f16p=False):
     import torch
 
     q = rng.standard_normal((len(seqs), n_heads * head_dim), dtype=np.float32)
-    stats = g.plan_attention(seqs, lens, n_heads, head_dim, shared_prefix=shared)
+    stats = g.plan_attention(seqs, lens, n_heads, head_dim, shared_prefix=shared, f16_products=f16p)
     out = g.planned_attention(layer, torch.from_numpy(q).to(gpu)).cpu().numpy()
     tables, la = tables_and_lens(g, seqs, lens)
     want = o.attention_tables(layer, tables, la, q, n_heads, head_dim, threads=8)
@@ -161,6 +161,41 @@ def test_f32_pools_plan_without_groups(gpu):
     ref = g.decode_attention(0, torch.from_numpy(q).to(gpu), torch.from_numpy(tables).to(gpu),
                              torch.from_numpy(la).to(gpu), 32, 64).cpu().numpy()
     np.testing.assert_array_equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+@pytest.mark.parametrize("head_dim,group", [(128, 4), (128, 7), (64, 8)])
+def test_prefix_groups_f16_products(gpu, dtype, head_dim, group):
+    """LTKV_PLAN_F16_PRODUCTS: the grouped products on f16-rounded Q and
+    weights stay within the attention tolerance of the oracle (f16 pools:
+    max abs 2e-2, relative L2 1e-3; q8_0: the f32 bar on max abs), and
+    really differ from the f32-accurate products (the flag takes effect)."""
+    import torch
+
+    rng = np.random.default_rng(head_dim + group + (7 if dtype == "q8_0" else 0))
+    n_kv = 2
+    kv_dim = n_kv * head_dim
+    spec = [(0, 1200, [(1 + i, int(rng.integers(0, 60))) for i in range(40)])]
+    g, o = _forked(rng, kv_dim, dtype, spec, singles=[(60, 300)])
+    seqs = [1 + i for i in range(40)] + [60]
+    lens = [g.len(s) for s in seqs]
+    n_heads = group * n_kv
+    stats, q, fast, tables, la = _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, dtype=dtype, f16p=True)
+    assert stats["groups"] == 1
+    g.plan_attention(seqs, lens, n_heads, head_dim, shared_prefix=True)
+    exact = g.planned_attention(0, torch.from_numpy(q).to(gpu)).cpu().numpy()
+    rel = np.linalg.norm(fast - exact) / np.linalg.norm(exact)
+    assert 1e-6 < rel < 1e-3, rel
+
+
+@pytest.mark.parametrize("n_heads,n_kv,head_dim,ctx,chunk", [(28, 4, 128, 1000, 512), (32, 4, 64, 700, 100)])
+def test_prefill_chunk_f16_products(gpu, n_heads, n_kv, head_dim, ctx, chunk):
+    """Causal groups of a prefill chunk with LTKV_PLAN_F16_PRODUCTS, within
+    the attention tolerance of the oracle."""
+    rng = np.random.default_rng(ctx + chunk + head_dim + 1)
+    g, o, seqs, lens = _prefill_state(rng, n_kv * head_dim, [(0, ctx, chunk)])
+    stats, *_ = _run(gpu, g, o, seqs, lens, n_heads, head_dim, rng, f16p=True)
+    assert stats["groups"] == 1 and stats["grouped"] == chunk
 
 
 # ---------------------------------------------------------------------------- chunked prefill

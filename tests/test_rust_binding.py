@@ -92,7 +92,8 @@ def test_constants_match_the_header():
         hvals[m.group(1)] = int(m.group(2))
     for m in re.finditer(r"#define\s+(LTKV_\w+)\s+\(?\s*(?:\(size_t\))?\s*\(?(-?\d+)\)?(?:\s*<<\s*(\d+))?", htext):
         hvals[m.group(1)] = int(m.group(2)) << int(m.group(3) or 0)
-    hvals["LTKV_PLAN_SHARED_PREFIX"] = 1  # '1u'
+    for m in re.finditer(r"#define\s+(LTKV_\w+)\s+(\d+)u\b", htext):  # unsigned flags
+        hvals[m.group(1)] = int(m.group(2))
     consts = dict((m.group(1), eval(m.group(2))) for m in
                   re.finditer(r"pub const (LTKV_\w+): \w+ = ([^;]+);", rtext))
     assert len(consts) >= 12
