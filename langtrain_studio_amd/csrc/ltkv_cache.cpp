@@ -294,8 +294,11 @@ struct ltkv_cache {
     if (n > pairs_cap) {
       size_t cap = std::max<size_t>(n, 2 * pairs_cap);
       cap = std::max<size_t>(cap, 256);
+      if (d_pairs) {  // the last copy kernel may still read the old device pairs
+        HIP_TRY(stream ? hipStreamSynchronize(stream) : hipDeviceSynchronize(), "synchronize");
+        (void)hipFree(d_pairs);
+      }
       if (h_pairs) (void)hipHostFree(h_pairs);
-      if (d_pairs) (void)hipFree(d_pairs);
       h_pairs = nullptr;
       d_pairs = nullptr;
       pairs_cap = 0;
@@ -1213,7 +1216,11 @@ int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
     // launches), so the copy writes in ascending destination order.
     const size_t buckets = (size_t)ltkv::copy_order_buckets((int64_t)c->n_blocks);
     if (n > c->order_cap) {
-      if (c->d_order_pairs) (void)hipFree(c->d_order_pairs);
+      if (c->d_order_pairs) {
+        // the old buffer may still be read by an enqueued copy
+        HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+        (void)hipFree(c->d_order_pairs);
+      }
       c->d_order_pairs = nullptr;
       c->order_cap = 0;
       HIP_TRY(hipMalloc((void **)&c->d_order_pairs, n * 2 * sizeof(int32_t)), "hipMalloc(copy order)");
@@ -1230,7 +1237,9 @@ int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
     const hipError_t e = ltkv::launch_copy_order(d_pairs, (int64_t)n, (int64_t)c->n_blocks, c->d_order_counts,
                                                  c->d_order_counts + buckets, c->d_order_pairs, c->stream);
     if (e != hipSuccess) {
-      // The counts may be left non-zero: start from fresh ones next time.
+      // The counts may be left non-zero: start from fresh ones next time
+      // (once whatever was enqueued has finished with them).
+      (void)(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize());
       (void)hipFree(c->d_order_counts);
       c->d_order_counts = nullptr;
       return fail(LTKV_ERR_HIP, "copy order launch: %s", hipGetErrorString(e));
@@ -1722,7 +1731,10 @@ int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, vo
                             1, d + meta, d + meta + n * row_bytes, c->d_status, c->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(h_k, d + meta, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(h_v, d + meta + n * row_bytes, n * row_bytes, hipMemcpyDeviceToHost, c->stream);
-  if (e == hipSuccess) e = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+  {  // whatever was enqueued must be done with the staging before it is freed
+    const hipError_t se = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+    if (e == hipSuccess) e = se;
+  }
   (void)hipFree(d);
   if (e != hipSuccess) return hip_fail(e, "rows");
   return LTKV_OK;
@@ -1757,7 +1769,10 @@ int ltkv_write_row(ltkv_cache *c, size_t layer, uint32_t block, uint32_t slot, c
     e = ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), (const int32_t *)d,
                            (const float *)(d + 16), (const float *)(d + 16 + row), 1,
                            (int64_t)c->kv_dim, c->stream);
-  if (e == hipSuccess) e = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+  {  // whatever was enqueued must be done with the staging before it is freed
+    const hipError_t se = c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize();
+    if (e == hipSuccess) e = se;
+  }
   (void)hipFree(d);
   if (e != hipSuccess) return hip_fail(e, "write_row");
   return LTKV_OK;
