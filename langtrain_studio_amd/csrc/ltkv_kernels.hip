@@ -659,8 +659,18 @@ __device__ __forceinline__ const int32_t *table_of(const int32_t *tables, int64_
 // panics at the same places): status[0] ORs the fault bits, status[1] holds
 // the query of one of them. The op goes on safely (a bad entry reads block
 // 0), so nothing faults on the GPU.
+// A wave-uniform read of memory no thread writes during the launch (block
+// tables, lengths), through the scalar cache: the constant address space
+// tells the compiler so, where stores elsewhere in the kernel would keep it
+// from proving it.
+__device__ __forceinline__ int32_t scalar_read(const int32_t *p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t *)p)[i];
+}
+
+// Every calling lane stores the same bits and query: no lane test, so values
+// the caller computes around a report stay uniform over the wave.
 __device__ __forceinline__ void report_fault(int32_t *status, int code, int64_t qi) {
-  if (!status || (threadIdx.x & 63) != 0) return;
+  if (!status) return;
   __hip_atomic_fetch_or(status, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   status[1] = (int32_t)qi;
 }
@@ -1568,6 +1578,7 @@ constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
 // ----------------------------------------------------------------------------
 constexpr int kOrderClasses = 16;
 constexpr int kOrderMaxQueries = 256;  // beyond this, query order (the scans would cost more)
+constexpr int kOrderChunks = kOrderMaxQueries / 64;
 
 __device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
                                                   int part_tokens, int split, int &key, int &items) {
@@ -1579,25 +1590,40 @@ __device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ le
   key = pt >> 6 < kOrderClasses - 1 ? pt >> 6 : kOrderClasses - 1;
 }
 
-// Item t of the ordered grid: its query qx and partition part, or false
-// when t is past the last item. One wave; `hist` is kOrderClasses ints of LDS.
-__device__ __forceinline__ bool decode_order_item(int64_t t, const int32_t *__restrict__ lens, int64_t n,
-                                                  int64_t max_len, int part_tokens, int split, int lane,
-                                                  int32_t *hist, int64_t &qx, int &part) {
+// Size class and item count of queries lane, 64 + lane, ... (n <=
+// kOrderMaxQueries; zero past n), and the items per class in `hist`
+// (kOrderClasses ints of LDS). One wave.
+struct OrderShapes {
+  int key[kOrderChunks], items[kOrderChunks];
+};
+
+__device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
+                                                   int part_tokens, int split, int lane, int32_t *hist,
+                                                   OrderShapes &sh) {
   if (lane < kOrderClasses) hist[lane] = 0;
   __syncthreads();
-  for (int64_t c0 = 0; c0 < n; c0 += 64) {
-    if (c0 + lane < n) {
-      int key, items;
-      decode_item_shape(lens, c0 + lane, max_len, part_tokens, split, key, items);
-      atomicAdd(hist + key, items);  // LDS
+#pragma unroll
+  for (int c = 0; c < kOrderChunks; ++c) {
+    sh.key[c] = 0;
+    sh.items[c] = 0;
+    if ((int64_t)c * 64 + lane < n) {
+      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.items[c]);
+      atomicAdd(hist + sh.key[c], sh.items[c]);  // LDS
     }
   }
   __syncthreads();
+}
+
+// Item t of the ordered list: its query qx and partition part, or false when
+// t is past the last item. Every decision and result is uniform over the
+// wave (read-first-lane of the exchanged values), so the item's addresses
+// stay in scalar registers.
+__device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane, const int32_t *hist,
+                                                  const OrderShapes &sh, int64_t &qx, int &part) {
   int cls = -1;
   int64_t base = 0;
   for (int k = kOrderClasses - 1; k >= 0; --k) {
-    const int c = hist[k];
+    const int c = __builtin_amdgcn_readfirstlane(hist[k]);
     if (t < base + c) {
       cls = k;
       break;
@@ -1606,24 +1632,23 @@ __device__ __forceinline__ bool decode_order_item(int64_t t, const int32_t *__re
   }
   if (cls < 0) return false;
   t -= base;
-  for (int64_t c0 = 0; c0 < n; c0 += 64) {
-    int v = 0;
-    if (c0 + lane < n) {
-      int key, items;
-      decode_item_shape(lens, c0 + lane, max_len, part_tokens, split, key, items);
-      v = key == cls ? items : 0;
-    }
+#pragma unroll
+  for (int c = 0; c < kOrderChunks; ++c) {
+    const int64_t c0 = (int64_t)c * 64;
+    if (c0 >= n) break;
+    const int v = sh.key[c] == cls ? sh.items[c] : 0;
     int incl = v;  // inclusive prefix sum over the wave
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int y = __shfl_up(incl, d, 64);
       if (lane >= d) incl += y;
     }
-    const int tot = __shfl(incl, 63, 64);
+    const int tot = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
     if (t < tot) {
       const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > t);
       const int j = __builtin_ctzll(hit);
-      const int end = __shfl(incl, j, 64), cnt = __shfl(v, j, 64);
+      const int end = __builtin_amdgcn_readfirstlane(__shfl(incl, j, 64));
+      const int cnt = __builtin_amdgcn_readfirstlane(__shfl(v, j, 64));
       qx = c0 + j;
       part = (int)(t - (end - cnt));
       return true;
@@ -1691,41 +1716,18 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   __shared__ int32_t shist[kOrderClasses];
 
-  // 1-D grid: (query, NH-head group, partition), the head group fastest; with
-  // `order`, the (query, partition) items longest first (decode_order_item).
+  // 1-D grid of (wave, NH-head group), the head group fastest. Wave w of a
+  // head group streams one item: without `order`, partition w % max_parts of
+  // query w / max_parts; with `order`, item w of the longest-first list
+  // (decode_order_find).
   const int n_groups = n_kv_heads / NH;
   const int kvh0 = (int)(blockIdx.x % n_groups) * NH;
   const int lane = threadIdx.x & 63;
-  int part;
-  int64_t qx;
-  if (order) {
-    if (!decode_order_item(blockIdx.x / n_groups, lens, n_queries, max_len, part_tokens, split, lane, shist, qx,
-                           part))
-      return;
-    // uniform over the wave: keep them (and the table and buffer addresses
-    // derived from them) in scalar registers
-    qx = __builtin_amdgcn_readfirstlane((int)qx);
-    part = __builtin_amdgcn_readfirstlane(part);
-  } else {
-    part = (int)((blockIdx.x / n_groups) % max_parts);
-    qx = blockIdx.x / ((unsigned)n_groups * max_parts);
-  }
-  const int64_t qi = qmap ? qmap[qx] : qx;
   const int lr = lane & 15, lq = lane >> 4;
   const int n_heads = n_kv_heads * G;
-
-  int64_t len = lens[qi];
-  if (len < 0) len = 0;
-  if (len > max_len) len = max_len;
-  // A query with group partials and nothing else to read (or whose group
-  // wrote its output) has no work here.
-  if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
-  const int pt = partition_tokens(len, part_tokens) / split;
-  const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
-  if (part >= np) return;
-  const int64_t tok0 = (int64_t)part * pt;
-  const int64_t tok1 = len < tok0 + pt ? len : tok0 + pt;
-  const int b0 = (int)(tok0 >> 4), b1 = (int)((tok1 + 15) >> 4);
+  const int64_t wave_idx = blockIdx.x / n_groups;
+  OrderShapes osh;
+  if (order) decode_order_setup(lens, n_queries, max_len, part_tokens, split, lane, shist, osh);
 
   // B operands Q'_a^T of the score product, one per kv head a of the wave:
   // column lr < NQ holds the hi part of query head lr of the wave, column
@@ -1734,39 +1736,45 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   const bool hi_lane = lr < NQ, lo_lane = lr >= 16 - NQ;
   const int qj = hi_lane ? lr : (lo_lane ? 15 - lr : 0);  // the column's query head in the wave
   const int my_head = qj / G;                             // its kv head in the wave
-  h8 qb[NH][KS];
-  {
+  // The query operand is fetched (fetch_q) and converted (convert_q) apart:
+  // the conversion waits for the fetch, and the first tiles' loads are issued
+  // in between, so the two latencies overlap. q8_0 K enters the score product
+  // as 1152 + k: 1152 times the column's sum of each k step of Q' comes off
+  // afterwards (qbias).
+  auto fetch_q = [&](int64_t qi, f32x4 (&qr)[2 * KS]) __attribute__((always_inline)) {
     const float *qp = q + qi * (int64_t)n_heads * HD + ((int64_t)kvh0 * G + qj) * HD + 8 * lq;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
-      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
+      qr[2 * ks] = *reinterpret_cast<const f32x4 *>(qp + 32 * ks);
+      qr[2 * ks + 1] = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
+    }
+  };
+  auto convert_q = [&](const f32x4 (&qr)[2 * KS], h8 (&qb)[NH][KS], float (&qbias)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = (e < 4 ? x0[e] : x1[e - 4]) * qscale;
+        const float x = (e < 4 ? qr[2 * ks][e] : qr[2 * ks + 1][e - 4]) * qscale;
         const _Float16 h = (_Float16)x;
         const _Float16 part_x = hi_lane ? h : (lo_lane ? (_Float16)(x - (float)h) : (_Float16)0.f);
 #pragma unroll
         for (int a = 0; a < NH; ++a) qb[a][ks][e] = a == my_head ? part_x : (_Float16)0.f;
       }
     }
-  }
-  // q8_0 K enters the score product as 1152 + k: 1152 times the column's
-  // sum of each k step of Q' comes off afterwards.
-  float qbias[KS];
-  if constexpr (Q8) {
+    if constexpr (Q8) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      float t = 0.f;
+      for (int ks = 0; ks < KS; ++ks) {
+        float t = 0.f;
 #pragma unroll
-      for (int a = 0; a < NH; ++a)
+        for (int a = 0; a < NH; ++a)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) t += (float)qb[a][ks][e];
-      t += __shfl_xor(t, 16);
-      t += __shfl_xor(t, 32);
-      qbias[ks] = 1152.f * t;
+          for (int e = 0; e < 8; ++e) t += (float)qb[a][ks][e];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        qbias[ks] = 1152.f * t;
+      }
     }
-  }
+  };
 
   // Loads: lane l takes 16-byte piece l % LPR of rows RPI i + l / LPR of the
   // wave's row segment (NH adjacent heads); piece p is head p / HP, bytes
@@ -1788,60 +1796,148 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 
   float m_ref = -INFINITY, l_run = 0.f;  // softmax reference and sum of this lane's column
   f32x4 o[DT];
+  auto reset = [&]() __attribute__((always_inline)) {
+    m_ref = -INFINITY;
+    l_run = 0.f;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
 
-  const int32_t *tab = table_of(tables, table_stride, rows, n_rows, qi);
-  check_table(tab, b0, b1, n_blocks, rows, n_rows, qi, status);
+  // One item: a partition [tok0, tok1) of query qi (tiles b0 .. b1 - 1).
+  // Every field is uniform over the wave (scalar registers).
+  struct Item {
+    int64_t qi, len, tok1;
+    int part, np, b0, b1;
+    const int32_t *tab;
+    int b_new, r_new;  // fused new row: its tile and row (b_new -1: none)
+    int32_t cell;      // ... and its pool cell
+    bool valid;
+  };
+  // The wave's item (valid false: none), with its query operand (qr) and
+  // fused new row (kr, vr) fetched, as f32.
+  auto make_item = [&](Item &it, f32x4 (&qr)[2 * KS], f32x4 (&kr)[2], f32x4 (&vr)[2]) __attribute__((always_inline)) {
+    it.valid = false;
+    int64_t qx;
+    int part;
+    if (order) {
+      if (!decode_order_find(wave_idx, n_queries, lane, shist, osh, qx, part)) return;
+      // uniform over the wave: keep them (and the table and buffer addresses
+      // derived from them) in scalar registers
+      qx = __builtin_amdgcn_readfirstlane((int)qx);
+      part = __builtin_amdgcn_readfirstlane(part);
+    } else {
+      part = (int)(wave_idx % max_parts);
+      qx = wave_idx / max_parts;
+    }
+    const int64_t qi = qmap ? qmap[qx] : qx;
+    int64_t len = lens[qi];
+    if (len < 0) len = 0;
+    if (len > max_len) len = max_len;
+    // A query with group partials and nothing else to read (or whose group
+    // wrote its output) has no work here.
+    if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
+    const int pt = partition_tokens(len, part_tokens) / split;
+    const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+    if (part >= np) return;
+    const int64_t tok0 = (int64_t)part * pt;
+    it.qi = qi;
+    it.len = len;
+    it.part = part;
+    it.np = np;
+    it.tok1 = len < tok0 + pt ? len : tok0 + pt;
+    it.b0 = (int)(tok0 >> 4);
+    it.b1 = (int)((it.tok1 + 15) >> 4);
+    it.tab = table_of(tables, table_stride, rows, n_rows, qi);
+    // A resident row outside the tables is a fault when the query has tokens
+    // (table entries are checked as their tiles load).
+    if (rows && it.b1 > it.b0) {
+      const int32_t r = rows[qi];
+      if (r < 0 || r >= n_rows) report_fault(status, kFaultTable, qi);
+    }
+    fetch_q(qi, qr);
 
-  // Fused append (f16, decode steps): the wave of the query's last partition
-  // writes the query's new K/V row (position len - 1, cell new_slots[qi]) of
-  // its heads, rounded to f16 as write_kernel does, and uses those registers
-  // for that row of the last tile instead of loading it. The lanes that hold
-  // row r_new of the tile (load index r_new / RPI) own the row's pieces.
-  int b_new = -1, r_new = 0;
-  u32x4 nk = {0u, 0u, 0u, 0u}, nv = {0u, 0u, 0u, 0u};
-  if constexpr (!Q8) {
-    if (new_slots && part == np - 1 && len > 0) {  // uniform
-      const int32_t cell = new_slots[qi];
-      // The cell must be position len - 1 of the query's table (what the
-      // claim returned for it); otherwise write-then-attend would differ.
-      if (cell >= 0 && (int64_t)tab[(len - 1) >> 4] * 16 + ((len - 1) & 15) != (int64_t)cell)
-        report_fault(status, kFaultFusedCell, qi);
-      if (cell >= 0 && (int64_t)cell < n_blocks * 16) {
-        b_new = (int)((len - 1) >> 4);
-        r_new = (int)((len - 1) & 15);
-        if (prow == r_new % RPI) {
+    // Fused append (f16, decode steps): the wave of the query's last partition
+    // writes the query's new K/V row (position len - 1, cell new_slots[qi]) of
+    // its heads, rounded to f16 as write_kernel does, and uses those registers
+    // for that row of the last tile instead of loading it (commit_new). Every
+    // lane takes the 16-byte piece it loads (lanes of different rows hold the
+    // same piece and store the same bytes): no lane test, so the item's
+    // fields stay uniform.
+    it.b_new = -1;
+    it.r_new = 0;
+    it.cell = -1;
+    kr[0] = kr[1] = vr[0] = vr[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!Q8) {
+      if (new_slots && part == np - 1 && len > 0) {  // uniform
+        const int32_t cell = scalar_read(new_slots, qi);
+        // The cell must be position len - 1 of the query's table (what the
+        // claim returned for it); otherwise write-then-attend would differ.
+        if (cell >= 0 && (int64_t)scalar_read(it.tab, (len - 1) >> 4) * 16 + ((len - 1) & 15) != (int64_t)cell)
+          report_fault(status, kFaultFusedCell, qi);
+        if (cell >= 0 && (int64_t)cell < n_blocks * 16) {
+          it.b_new = (int)((len - 1) >> 4);
+          it.r_new = (int)((len - 1) & 15);
+          it.cell = cell;
           const float *ksrc = new_k + qi * new_stride + (int64_t)kvh0 * head_stride + 8 * piece;
           const float *vsrc = new_v + qi * new_stride + (int64_t)kvh0 * head_stride + 8 * piece;
-          const f32x4 k0 = *reinterpret_cast<const f32x4 *>(ksrc), k1 = *reinterpret_cast<const f32x4 *>(ksrc + 4);
-          const f32x4 v0 = *reinterpret_cast<const f32x4 *>(vsrc), v1 = *reinterpret_cast<const f32x4 *>(vsrc + 4);
-          nk = u32x4{pack_f16x2(k0.x, k0.y), pack_f16x2(k0.z, k0.w), pack_f16x2(k1.x, k1.y), pack_f16x2(k1.z, k1.w)};
-          nv = u32x4{pack_f16x2(v0.x, v0.y), pack_f16x2(v0.z, v0.w), pack_f16x2(v1.x, v1.y), pack_f16x2(v1.z, v1.w)};
-          const int64_t dst = (int64_t)cell * slot_stride + (int64_t)kvh0 * head_stride + 8 * piece;
-          *reinterpret_cast<u32x4 *>(kdst + dst) = nk;
-          *reinterpret_cast<u32x4 *>(vdst + dst) = nv;
+          kr[0] = *reinterpret_cast<const f32x4 *>(ksrc);
+          kr[1] = *reinterpret_cast<const f32x4 *>(ksrc + 4);
+          vr[0] = *reinterpret_cast<const f32x4 *>(vsrc);
+          vr[1] = *reinterpret_cast<const f32x4 *>(vsrc + 4);
         }
       }
     }
-  }
+    it.valid = true;
+  };
+
+  // The item's fused row as f16 (nk, nv), written to its pool cell.
+  auto commit_new = [&](const Item &it, const f32x4 (&kr)[2], const f32x4 (&vr)[2], u32x4 &nk, u32x4 &nv) __attribute__((always_inline)) {
+    nk = u32x4{pack_f16x2(kr[0].x, kr[0].y), pack_f16x2(kr[0].z, kr[0].w), pack_f16x2(kr[1].x, kr[1].y),
+               pack_f16x2(kr[1].z, kr[1].w)};
+    nv = u32x4{pack_f16x2(vr[0].x, vr[0].y), pack_f16x2(vr[0].z, vr[0].w), pack_f16x2(vr[1].x, vr[1].y),
+               pack_f16x2(vr[1].z, vr[1].w)};
+    if constexpr (!Q8) {
+      if (it.cell >= 0) {  // uniform
+        const int64_t dst = (int64_t)it.cell * slot_stride + (int64_t)kvh0 * head_stride + 8 * piece;
+        *reinterpret_cast<u32x4 *>(kdst + dst) = nk;
+        *reinterpret_cast<u32x4 *>(vdst + dst) = nv;
+      }
+    }
+  };
 
   struct Stage {
     u32x4 k[NLD], v[NLD];
     SV ks, vs;  // q8_0: scale entries sidx (.. sidx + 1) of K and of V
   };
 
+  // The wave's item, its query operand (qb, qbias) and fused row (nk, nv).
+  Item cur;
+  h8 qb[NH][KS];
+  float qbias[KS];
+  u32x4 nk, nv;
+
   // Loads go through buffer descriptors whose extent ends at the last row
-  // inside the context: rows past it (and every row of a prefetch past the
-  // last tile, extent 0) read as zeros without touching memory.
-  auto load_tile = [&](int b, Stage &st) {
-    const int bb = b < b1 ? b : b1 - 1;
-    int32_t blk = tab[bb];
-    if (blk < 0 || blk >= n_blocks) blk = 0;  // out-of-range entries read block 0 (never faults)
-    const int valid = b < b1 ? (int)(tok1 - (int64_t)b * 16) : 0;
-    const int rows = valid < 16 ? valid : 16;
-    // the fused new row (the tile's last valid row) is not loaded
-    const int lrows = b == b_new ? r_new : rows;
+  // inside the context: rows past it, and every row of a load past the last
+  // tile (live false), read as zeros without touching memory.
+  // A table entry outside the pool reads block 0 instead (never faults); the
+  // query of the last one is reported when the wave ends (a store inside the
+  // tile loop would keep the compiler from reading the tables through the
+  // scalar cache).
+  int64_t fault_q = -1;
+  auto load_tile = [&](const int32_t *tab, int64_t qi, int64_t tok1, int b_new, int r_new, bool live, int b,
+                       Stage &st) __attribute__((always_inline)) {
+    int32_t blk = 0;
+    int rows = 0, lrows = 0;
+    if (live) {  // uniform; b is a tile of the item, in [b0, b1)
+      blk = scalar_read(tab, b);
+      const bool bad = blk < 0 || blk >= n_blocks;
+      fault_q = bad ? qi : fault_q;
+      blk = bad ? 0 : blk;
+      const int valid = (int)(tok1 - (int64_t)b * 16);
+      rows = valid < 16 ? valid : 16;
+      // the fused new row (the tile's last valid row) is not loaded
+      lrows = b == b_new ? r_new : rows;
+    }
     const int extent = lrows > 0 ? (lrows - 1) * (int)row_bytes + NH * RB : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(kbase + (int64_t)blk * block_bytes), (short)0, extent, kBufferWord3);
@@ -1874,7 +1970,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
   };
 
-  auto compute_tile = [&](int b, const Stage &st) {
+  auto compute_tile = [&](int b, const Stage &st) __attribute__((always_inline)) {
     // Stage K (as loaded) and V (as f16) in LDS, row order, one region per head.
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
@@ -1889,10 +1985,11 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
     if constexpr (!Q8) {
       // The fused new row (loaded as zeros: outside the tile's extent) is
-      // overwritten from registers by the lanes that own it.
-      if (b == b_new && prow == r_new % RPI) {
-        *reinterpret_cast<u32x4 *>(sk[ph] + r_new * KPITCH + pc * 16) = nk;
-        *reinterpret_cast<u32x4 *>(sv[ph] + r_new * VPITCH + pc * 16) = nv;
+      // overwritten from registers (every lane writes its piece; lanes of
+      // different rows write the same bytes).
+      if (b == cur.b_new) {
+        *reinterpret_cast<u32x4 *>(sk[ph] + cur.r_new * KPITCH + pc * 16) = nk;
+        *reinterpret_cast<u32x4 *>(sv[ph] + cur.r_new * VPITCH + pc * 16) = nv;
       }
     }
     if constexpr (Q8) {
@@ -1938,7 +2035,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     float sc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[i] = s[i] + dpp<0x140>(s[i]);  // hi + lo (row_mirror: lane ^ 15)
-    const int valid = (int)(tok1 - (int64_t)b * 16);  // rows of this tile inside the context
+    const int valid = (int)(cur.tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     if (valid < 16) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1994,53 +2091,19 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
   };
 
-  // Software pipeline: STAGES - 1 tiles in flight while one is computed.
-  // Loads past the last tile read nothing (extent 0).
-  {
-    int b = b0;
-    if (b < b1) {
-      if constexpr (STAGES == 3) {
-        Stage s0, s1, s2;
-        load_tile(b, s0);
-        load_tile(b + 1, s1);
-        for (;;) {
-          load_tile(b + 2, s2);
-          compute_tile(b, s0);
-          if (++b >= b1) break;
-          load_tile(b + 2, s0);
-          compute_tile(b, s1);
-          if (++b >= b1) break;
-          load_tile(b + 2, s1);
-          compute_tile(b, s2);
-          if (++b >= b1) break;
-        }
-      } else {
-        Stage s0, s1;
-        load_tile(b, s0);
-        for (;;) {
-          load_tile(b + 1, s1);
-          compute_tile(b, s0);
-          if (++b >= b1) break;
-          load_tile(b + 1, s0);
-          compute_tile(b, s1);
-          if (++b >= b1) break;
-        }
-      }
-    }
-  }
-
-  // Column sums over the four lane rows; hi + lo parts of the numerators.
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
+  // The item's result: the output (one partition) or its partial.
+  auto finish = [&](const Item &it) __attribute__((always_inline)) {
+    // Column sums over the four lane rows; hi + lo parts of the numerators.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[dt][i] += dpp<0x140>(o[dt][i]);
-
-  if (hi_lane) {  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
-    const int64_t qh = qi * n_heads + (int64_t)kvh0 * G + lr;
-    if (np == 1) {  // one partition: this wave writes the output
-      const int npre = pre_parts ? pre_parts[qi] : 0;
+      for (int i = 0; i < 4; ++i) o[dt][i] += dpp<0x140>(o[dt][i]);
+    if (!hi_lane) return;  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
+    const int64_t qh = it.qi * n_heads + (int64_t)kvh0 * G + lr;
+    if (it.np == 1) {  // one partition: this wave writes the output
+      const int npre = pre_parts ? pre_parts[it.qi] : 0;
       if (npre > 0) {
         // Fold the query's group partials (numerator, reference, sum) into
         // the wave's own, four partials per round (indices clamped to the
@@ -2090,7 +2153,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         *reinterpret_cast<f32x4 *>(out + qh * HD + 16 * dt + 4 * lq) =
             l_run > 0.f ? o[dt] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
-      const int64_t pi = qh * max_parts + part;
+      const int64_t pi = qh * max_parts + it.part;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(part_o + pi * HD + 16 * dt + 4 * lq) = o[dt];
       if (lq == 0) {
@@ -2098,16 +2161,64 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         part_ml[2 * pi + 1] = l_run;
       }
     }
+  };
+
+  // STAGES - 1 tiles in flight while one is computed; loads past the last
+  // tile read nothing (extent 0).
+  f32x4 qr[2 * KS], kr[2], vr[2];
+  make_item(cur, qr, kr, vr);
+  if (!cur.valid) return;
+  reset();
+  int b = cur.b0;
+  auto load_b = [&](int bb, Stage &st) __attribute__((always_inline)) {
+    load_tile(cur.tab, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
+  };
+  if (b < cur.b1) {
+    if constexpr (STAGES == 3) {
+      Stage s0, s1, s2;
+      load_b(b, s0);
+      load_b(b + 1, s1);
+      convert_q(qr, qb, qbias);
+      commit_new(cur, kr, vr, nk, nv);
+      for (;;) {
+        load_b(b + 2, s2);
+        compute_tile(b, s0);
+        if (++b >= cur.b1) break;
+        load_b(b + 2, s0);
+        compute_tile(b, s1);
+        if (++b >= cur.b1) break;
+        load_b(b + 2, s1);
+        compute_tile(b, s2);
+        if (++b >= cur.b1) break;
+      }
+    } else {
+      Stage s0, s1;
+      load_b(b, s0);
+      convert_q(qr, qb, qbias);
+      commit_new(cur, kr, vr, nk, nv);
+      for (;;) {
+        load_b(b + 1, s1);
+        compute_tile(b, s0);
+        if (++b >= cur.b1) break;
+        load_b(b + 1, s0);
+        compute_tile(b, s1);
+        if (++b >= cur.b1) break;
+      }
+    }
   }
+  finish(cur);
+  if (fault_q >= 0) report_fault(status, kFaultTable, fault_q);
 }
 
 // Plain decode attention of up to kOrderMaxQueries queries takes its items
-// longest first; planned launches (query maps, group partials) keep query order.
+// longest first; planned launches (query maps, group partials) keep query
+// order.
 inline bool decode_ordered(const AttnArgs &a) {
   return !a.qmap && !a.pre_parts && a.n > 1 && a.n <= kOrderMaxQueries;
 }
 
-// One wave per work-group: each wave streams a whole partition of NH kv heads.
+// One wave per work-group and item: each streams a whole partition of NH kv
+// heads.
 template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.n * (a.n_kv_heads / NH) * a.max_parts);
