@@ -690,10 +690,10 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   // a member has partials for the partitions that start below its limit.
   // With one partition, a tile whose members read nothing else writes their
   // outputs itself (pre_parts -1: no per-query pass, no merge).
-  const size_t per_job = (size_t)ltkv::mq_rows((int)head_dim) / group;  // members per work-group
+  const size_t per_job = (size_t)ltkv::mq_rows((int)c->elem, (int)head_dim) / group;  // members per work-group
   size_t units = 0;
   for (const auto &gr : groups) units += (gr.members.size() + per_job - 1) / per_job * n_kv_heads;
-  const size_t waves = (size_t)ltkv::mq_rows((int)head_dim) / 32;
+  const size_t waves = (size_t)ltkv::mq_rows((int)c->elem, (int)head_dim) / 32;
   const size_t target = 8 * (size_t)c->device_count_cu / waves;  // two waves per SIMD
   std::vector<ltkv::MqJob> jobs;
   std::vector<int32_t> members;
@@ -706,7 +706,8 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     const Group &gr = groups[gi];
     const size_t tokens = gr.tokens;
     const size_t max_split = std::max<size_t>(1, tokens / kMinPrefixPart);
-    const size_t split = std::min(max_split, std::max<size_t>(1, (target + units - 1) / units));
+    const size_t split = std::max(std::min(max_split, std::max<size_t>(1, (target + units - 1) / units)),
+                                  (tokens + ltkv::kMqMaxRange - 1) / ltkv::kMqMaxRange);
     const size_t pt = ((tokens + split - 1) / split + 31) / 32 * 32;
     const size_t parts = (tokens + pt - 1) / pt;
     const size_t m0 = members.size() / 2;

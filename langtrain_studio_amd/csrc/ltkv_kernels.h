@@ -181,7 +181,8 @@ struct MqJob {
   int32_t kvh;
   int32_t direct;              // 1: the rows' only contribution; write the output
 };
-int mq_rows(int head_dim);  // query rows per work-group
+int mq_rows(int elem, int head_dim);  // query rows per work-group
+constexpr int kMqMaxRange = 16384;  // longest token range of one group job (its block ids sit in LDS)
 
 struct MqArgs {
   const void *k_layer, *v_layer;

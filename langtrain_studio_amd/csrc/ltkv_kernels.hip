@@ -43,6 +43,7 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -935,6 +936,21 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   const int h = (int)(pair % n_heads);
   const int64_t qx = pair / n_heads;
   const int64_t qi = qmap ? qmap[qx] : qx;
+  const int64_t qh = qi * n_heads + h;
+  const float *ml = part_ml + qh * max_parts * 2;
+  // The first four partials are loaded before the length is known (slots
+  // clamped to max_parts - 1; slots past the query's np are never used, by
+  // selection, so stale values there cannot leak), so the common case costs
+  // one round trip.
+  float m4[4], l4[4];
+  f32x4 o4[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int pc = p < max_parts ? p : max_parts - 1;
+    m4[p] = ml[2 * pc];
+    l4[p] = ml[2 * pc + 1];
+    o4[p] = *reinterpret_cast<const f32x4 *>(part_o + (qh * max_parts + pc) * HD + d);
+  }
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
@@ -947,31 +963,21 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   const int np = (int)((len + pt - 1) / pt);
   if (np <= 1 && npre == 0) return;
   if (np == 1 && folded) return;
-  const int64_t qh = qi * n_heads + h;
-  const float *ml = part_ml + qh * max_parts * 2;
   if (npre == 0 && np <= 4) {
-    // The common case (a query of up to four partitions): every load is
-    // issued up front (indices clamped, weight 0 past np), one round trip.
-    float m4[4], l4[4];
-    f32x4 o4[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int pc = p < np ? p : np - 1;
-      m4[p] = ml[2 * pc];
-      l4[p] = ml[2 * pc + 1];
-      o4[p] = *reinterpret_cast<const f32x4 *>(part_o + (qh * max_parts + pc) * HD + d);
-    }
+    // The common case (a query of up to four partitions, np <= max_parts).
     float mx = m4[0];
 #pragma unroll
-    for (int p = 1; p < 4; ++p) mx = __builtin_fmaxf(mx, m4[p]);  // clamped copies change nothing
+    for (int p = 1; p < 4; ++p) mx = p < np ? __builtin_fmaxf(mx, m4[p]) : mx;
     const float mref = mx == -INFINITY ? 0.f : mx;
     float lsum = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const float a = p < np ? __builtin_amdgcn_exp2f(m4[p] - mref) : 0.f;
-      lsum += l4[p] * a;
-      o += o4[p] * a;
+      if (p < np) {
+        const float a = __builtin_amdgcn_exp2f(m4[p] - mref);
+        lsum += l4[p] * a;
+        o += o4[p] * a;
+      }
     }
     f32x4 r = {0.f, 0.f, 0.f, 0.f};
     if (lsum > 0.f) r = f32x4{o.x / lsum, o.y / lsum, o.z / lsum, o.w / lsum};
@@ -1581,10 +1587,11 @@ constexpr int kOrderMaxQueries = 256;  // beyond this, query order (the scans wo
 constexpr int kOrderChunks = kOrderMaxQueries / 64;
 
 __device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
-                                                  int part_tokens, int split, int &key, int &items) {
+                                                  int part_tokens, int split, int &key, int &items, int &clen) {
   int64_t len = lens[q];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
+  clen = (int)len;
   const int pt = partition_tokens(len, part_tokens) / split;
   items = len > 0 ? (int)((len + pt - 1) / pt) : 1;
   key = pt >> 6 < kOrderClasses - 1 ? pt >> 6 : kOrderClasses - 1;
@@ -1594,7 +1601,7 @@ __device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ le
 // kOrderMaxQueries; zero past n), and the items per class in `hist`
 // (kOrderClasses ints of LDS). One wave.
 struct OrderShapes {
-  int key[kOrderChunks], items[kOrderChunks];
+  int key[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
 };
 
 __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
@@ -1606,8 +1613,10 @@ __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ l
   for (int c = 0; c < kOrderChunks; ++c) {
     sh.key[c] = 0;
     sh.items[c] = 0;
+    sh.len[c] = 0;
     if ((int64_t)c * 64 + lane < n) {
-      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.items[c]);
+      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.items[c],
+                        sh.len[c]);
       atomicAdd(hist + sh.key[c], sh.items[c]);  // LDS
     }
   }
@@ -1619,7 +1628,7 @@ __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ l
 // wave (read-first-lane of the exchanged values), so the item's addresses
 // stay in scalar registers.
 __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane, const int32_t *hist,
-                                                  const OrderShapes &sh, int64_t &qx, int &part) {
+                                                  const OrderShapes &sh, int64_t &qx, int &part, int &qlen) {
   int cls = -1;
   int64_t base = 0;
   for (int k = kOrderClasses - 1; k >= 0; --k) {
@@ -1649,6 +1658,7 @@ __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane
       const int j = __builtin_ctzll(hit);
       const int end = __builtin_amdgcn_readfirstlane(__shfl(incl, j, 64));
       const int cnt = __builtin_amdgcn_readfirstlane(__shfl(v, j, 64));
+      qlen = __builtin_amdgcn_readfirstlane(__shfl(sh.len[c], j, 64));
       qx = c0 + j;
       part = (int)(t - (end - cnt));
       return true;
@@ -1818,9 +1828,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   auto make_item = [&](Item &it, f32x4 (&qr)[2 * KS], f32x4 (&kr)[2], f32x4 (&vr)[2]) __attribute__((always_inline)) {
     it.valid = false;
     int64_t qx;
-    int part;
+    int part, olen = 0;
     if (order) {
-      if (!decode_order_find(wave_idx, n_queries, lane, shist, osh, qx, part)) return;
+      if (!decode_order_find(wave_idx, n_queries, lane, shist, osh, qx, part, olen)) return;
       // uniform over the wave: keep them (and the table and buffer addresses
       // derived from them) in scalar registers
       qx = __builtin_amdgcn_readfirstlane((int)qx);
@@ -1830,9 +1840,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       qx = wave_idx / max_parts;
     }
     const int64_t qi = qmap ? qmap[qx] : qx;
-    int64_t len = lens[qi];
-    if (len < 0) len = 0;
-    if (len > max_len) len = max_len;
+    int64_t len;
+    if (order) {
+      len = olen;  // the order scan read and clamped it (ordered launches have no query map)
+    } else {
+      len = lens[qi];
+      if (len < 0) len = 0;
+      if (len > max_len) len = max_len;
+    }
     // A query with group partials and nothing else to read (or whose group
     // wrote its output) has no work here.
     if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
@@ -1924,12 +1939,12 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // tile loop would keep the compiler from reading the tables through the
   // scalar cache).
   int64_t fault_q = -1;
-  auto load_tile = [&](const int32_t *tab, int64_t qi, int64_t tok1, int b_new, int r_new, bool live, int b,
+  auto load_tile = [&](int32_t entry, int64_t qi, int64_t tok1, int b_new, int r_new, bool live, int b,
                        Stage &st) __attribute__((always_inline)) {
     int32_t blk = 0;
     int rows = 0, lrows = 0;
-    if (live) {  // uniform; b is a tile of the item, in [b0, b1)
-      blk = scalar_read(tab, b);
+    if (live) {  // uniform; b is a tile of the item, in [b0, b1); entry is its table entry
+      blk = entry;
       const bool bad = blk < 0 || blk >= n_blocks;
       fault_q = bad ? qi : fault_q;
       blk = bad ? 0 : blk;
@@ -2170,37 +2185,50 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   if (!cur.valid) return;
   reset();
   int b = cur.b0;
-  auto load_b = [&](int bb, Stage &st) __attribute__((always_inline)) {
-    load_tile(cur.tab, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
+  // Table entries are read one tile ahead of their loads (the first ones
+  // together), so no load waits on its own scalar read.
+  auto entry_of = [&](int bb) __attribute__((always_inline)) { return bb < cur.b1 ? scalar_read(cur.tab, bb) : 0; };
+  auto load_b = [&](int bb, int32_t entry, Stage &st) __attribute__((always_inline)) {
+    load_tile(entry, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
   };
   if (b < cur.b1) {
     if constexpr (STAGES == 3) {
       Stage s0, s1, s2;
-      load_b(b, s0);
-      load_b(b + 1, s1);
+      const int32_t e0 = entry_of(b), e1 = entry_of(b + 1);
+      int32_t en = entry_of(b + 2);
+      load_b(b, e0, s0);
+      load_b(b + 1, e1, s1);
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
-        load_b(b + 2, s2);
+        int32_t ea = entry_of(b + 3);
+        load_b(b + 2, en, s2);
         compute_tile(b, s0);
         if (++b >= cur.b1) break;
-        load_b(b + 2, s0);
+        en = entry_of(b + 3);
+        load_b(b + 2, ea, s0);
         compute_tile(b, s1);
         if (++b >= cur.b1) break;
-        load_b(b + 2, s1);
+        ea = entry_of(b + 3);
+        load_b(b + 2, en, s1);
         compute_tile(b, s2);
         if (++b >= cur.b1) break;
+        en = ea;
       }
     } else {
       Stage s0, s1;
-      load_b(b, s0);
+      const int32_t e0 = entry_of(b);
+      int32_t en = entry_of(b + 1);
+      load_b(b, e0, s0);
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
-        load_b(b + 1, s1);
+        int32_t ea = entry_of(b + 2);
+        load_b(b + 1, en, s1);
         compute_tile(b, s0);
         if (++b >= cur.b1) break;
-        load_b(b + 1, s0);
+        en = entry_of(b + 2);
+        load_b(b + 1, ea, s0);
         compute_tile(b, s1);
         if (++b >= cur.b1) break;
       }
@@ -2317,6 +2345,7 @@ hipError_t launch_attn_hd(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 // ----------------------------------------------------------------------------
 
 constexpr int kMqChunk = 32;       // tokens per staging step
+constexpr int kMqTabMax = kMqMaxRange / 16;  // table entries of one job's token range
 constexpr float kMqSlack = 8.f;    // log2 headroom of the softmax reference
 
 __device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
@@ -2324,24 +2353,20 @@ __device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
   for (int j = 0; j < 8; ++j) {
     const _Float16 h = (_Float16)x[j];
     hi[j] = h;
-    lo[j] = (_Float16)(x[j] - (float)h);
+    lo[j] = (_Float16)__builtin_fmaf((float)h, -1.f, x[j]);  // x - h, exact in f32 (v_fma_mix)
   }
 }
 
 
-constexpr int kMqWaves = 4;  // waves per work-group
-
-// Waves per SIMD the kernel is built for (register budget 512 / waves): two,
-// except q8_0 rows of 128 (X = HD / element bytes = 128), whose scale
-// handling does not fit 256 registers.
-template <int X>
-constexpr int kMqMinWaves = X >= 128 ? 1 : 2;
+// Work-group: eight waves of 32 query rows (256 rows), two waves per SIMD;
+// each staged K/V chunk serves all 256 rows.
+constexpr int kMqWaves = 8;
 
 // F16P: the products take Q and the softmax weights P rounded to f16, one
 // MFMA each (no lo parts): half the MFMA work and no split of P on the VALU,
 // at ~2^-12 relative error per operand (opt-in, LTKV_PLAN_F16_PRODUCTS).
 template <typename T, int HD, bool F16P>
-__global__ void __launch_bounds__(64 * kMqWaves, kMqMinWaves<HD / (int)sizeof(T)>)
+__global__ void __launch_bounds__(64 * kMqWaves, 2)
 mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
                const float *__restrict__ q, const int32_t *__restrict__ tables,
                const MqJob *__restrict__ jobs, int n_jobs, const int32_t *__restrict__ members,
@@ -2353,18 +2378,26 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;                // k steps of the score product (q8_0: scale groups)
   constexpr int DT = HD / 16;                // 16-wide d tiles of the output
-  constexpr int ROWB = HD * 2 + 16;          // LDS bytes per staged row, f16 (pad: no bank conflicts)
+  // LDS bytes per staged row, f16. The pads keep the score product's K
+  // reads (16 bytes a lane) and the transposing V reads (8 bytes a lane,
+  // four rows x four columns per 16 lanes) free of bank conflicts.
+  constexpr int ROWK = HD * 2 + 16;
+  constexpr int ROWV = HD * 2 + 32;
   constexpr int VPR = HD * (int)sizeof(T) / 16;  // 16-byte vectors per pool row
-  constexpr int NT = 64 * kMqWaves;     // threads
+  constexpr int NT = 64 * kMqWaves;  // threads
   constexpr int NV = kMqChunk * VPR;         // vectors per chunk, K and V each
   constexpr int NPT = (NV + NT - 1) / NT;    // vectors per thread per chunk, K and V each
   static_assert(NV % NT == 0 || NV < NT, "chunk must split over the threads");
   static_assert(64 / VPR <= 16, "a wave's rows of a chunk must lie in one block");
   constexpr int NSC = KS * kMqChunk;         // q8_0 scale entries of a chunk, K or V
   static_assert(!Q8 || 2 * NSC <= NT, "one scale entry per thread");
-  __shared__ __attribute__((aligned(16))) char sm[2][2][kMqChunk * ROWB];  // [stage][K, V] as f16
+  __shared__ __attribute__((aligned(16))) char smk[2][kMqChunk * ROWK];  // [stage] K rows as f16
+  __shared__ __attribute__((aligned(16))) char smv[2][kMqChunk * ROWV];  // [stage] V rows as f16
   // q8_0: [stage][K, V][group][token] scales of the staged chunk
   __shared__ __attribute__((aligned(16))) uint16_t ssm[2][2][Q8 ? NSC : 1];
+  // The job's blocks: {byte offset lo, hi, load extent, block id}; extent 0
+  // for blocks outside the pool.
+  __shared__ __attribute__((aligned(16))) i32x4 stab[kMqTabMax];
 
   // The job list is ordered by work-group id (XCD placement is the host's);
   // empty jobs pad it.
@@ -2441,25 +2474,63 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // Staging: token tok's row of this kv head is one contiguous HD-element
   // run; tokens at or past t1 stage as zeros. q8_0 rows are converted to f16
   // on the way into LDS (K biased as above, V exact), with their scales.
+  // The job's block-table entries are read once into LDS with each block's
+  // byte offset and load extent, so a chunk's buffer descriptors cost an LDS
+  // read and a 64-bit add, with no scalar-memory wait.
   const int32_t *tab = tables + jb.table;
+  const int tb0 = jb.t0 >> 4;                       // first table entry of the range
+  const int ntab = (jb.t1 - jb.t0 + 15) >> 4;       // entries of the range (<= kMqTabMax)
+  const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
+  for (int i = threadIdx.x; i < ntab && i < kMqTabMax; i += NT) {
+    const int32_t blk = tab[tb0 + i];
+    const int valid = jb.t1 - (tb0 + i) * 16;  // rows of the block inside the range (> 0)
+    const bool ok = blk >= 0 && blk < n_blocks;
+    const int64_t off = ok ? (int64_t)blk * block_stride * (int64_t)sizeof(T) : 0;
+    const int ext = ok ? ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * (int)sizeof(T) : 0;
+    stab[i] = i32x4{(int32_t)(uint32_t)off, (int32_t)(off >> 32), ext, ok ? blk : -1};
+  }
   const int64_t head_off = (int64_t)jb.kvh * HD;
   // Chunks start on block boundaries (t0 % 32 == 0) and a wave's share of a
-  // chunk lies in one block, so its table entry is one scalar load. K/V
-  // rows go through buffer descriptors whose extent ends at t1: rows past it
-  // load as zeros with no branch.
-  const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
+  // chunk lies in one block. K/V rows go through buffer descriptors whose
+  // extent ends at t1: rows past it (and chunks past the range) load as
+  // zeros with no branch and no traffic.
   const int64_t sgroups = slot_stride >> 5;         // q8_0 scale groups per pool row
   const int64_t shead = (int64_t)jb.kvh * (HD / 32);  // first scale group of this kv head
-  auto load_chunk = [&](int c0, u32x4 (&kr)[NPT], u32x4 (&vr)[NPT], uint32_t &sc) {
+  struct ChunkBlocks {
+    int64_t off0, off1;  // byte offsets of the chunk's two blocks (wave-uniform)
+    int ext0, ext1;      // their load extents (wave-uniform)
+    int blk0, blk1;      // their block ids, -1 outside the range or the pool
+  };
+  // The two blocks of chunk j: one LDS read each.
+  auto chunk_blocks = [&](int j) {
+    const int e0 = 2 * j < kMqTabMax ? 2 * j : kMqTabMax - 1;
+    const int e1 = 2 * j + 1 < kMqTabMax ? 2 * j + 1 : kMqTabMax - 1;
+    const i32x4 v0 = stab[e0], v1 = stab[e1];
+    const bool in0 = 2 * j < ntab && 2 * j < kMqTabMax, in1 = 2 * j + 1 < ntab && 2 * j + 1 < kMqTabMax;
+    ChunkBlocks cb;
+    cb.off0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(v0.y) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane(v0.x));
+    cb.off1 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(v1.y) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane(v1.x));
+    cb.ext0 = in0 ? __builtin_amdgcn_readfirstlane(v0.z) : 0;
+    cb.ext1 = in1 ? __builtin_amdgcn_readfirstlane(v1.z) : 0;
+    cb.blk0 = in0 ? v0.w : -1;
+    cb.blk1 = in1 ? v1.w : -1;
+    return cb;
+  };
+  // Chunk j of K (KIND 0) or V (KIND 1) into registers.
+  auto load_part = [&](auto kind, int j, const ChunkBlocks &cb, u32x4 (&r)[NPT], uint32_t &sc) {
+    constexpr int KIND = decltype(kind)::value;
+    const char *pool = reinterpret_cast<const char *>((KIND == 0 ? kpool : vpool) + head_off);
+    const int c0 = jb.t0 + j * kMqChunk;
     if constexpr (Q8) {
-      // thread t < 2 NSC: entry t % NSC (group e / 32, token e % 32) of K (t < NSC) or V
+      // thread t < NSC: entry t (group t / 32, token t % 32) of the chunk's scales
       sc = 0;
-      if ((int)threadIdx.x < 2 * NSC) {
-        const int e = (int)threadIdx.x % NSC, tok = c0 + e % kMqChunk;
-        const int bi = tok >> 4;
-        const int32_t blk = tok < jb.t1 ? tab[bi] : -1;
-        if (blk >= 0 && blk < n_blocks) {
-          const uint16_t *sp = (int)threadIdx.x < NSC ? kscale : vscale;
+      if ((int)threadIdx.x < NSC) {
+        const int e = (int)threadIdx.x, tok = c0 + e % kMqChunk;
+        const int32_t blk = (tok & 16) ? cb.blk1 : cb.blk0;
+        if (blk >= 0 && tok < jb.t1) {
+          const uint16_t *sp = KIND == 0 ? kscale : vscale;
           sc = sp[((int64_t)blk * sgroups + shead + e / kMqChunk) * 16 + (tok & 15)];
         }
       }
@@ -2469,43 +2540,40 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       const int idx = threadIdx.x + NT * u;
       if (NV < NT && idx >= NV) break;  // wave-uniform: NV is a multiple of 64
       const int row = idx / VPR, col = idx - row * VPR;
-      const int wrow = __builtin_amdgcn_readfirstlane(row);  // first row of this wave's share
-      const int bi = (c0 + wrow) >> 4;
-      const int valid = jb.t1 - bi * 16;  // rows of the block inside the range
-      int32_t blk = valid > 0 ? tab[bi] : -1;
-      if (blk >= n_blocks) blk = -1;
-      const int extent = blk < 0 ? 0 : ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * (int)sizeof(T);
-      const int64_t base = (int64_t)(blk < 0 ? 0 : blk) * block_stride + head_off;
-      const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc((void *)(kpool + base), (short)0, extent, kBufferWord3);
-      const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc((void *)(vpool + base), (short)0, extent, kBufferWord3);
+      const bool h1 = (__builtin_amdgcn_readfirstlane(row) & 16) != 0;  // this wave's share is in block 1
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(pool + (h1 ? cb.off1 : cb.off0)), (short)0, h1 ? cb.ext1 : cb.ext0, kBufferWord3);
       const uint32_t voff = (uint32_t)((c0 + row) & 15) * row_bytes + (uint32_t)col * 16;
-      kr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
-      vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
+      r[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0));
     }
   };
-  auto store_chunk = [&](int st, const u32x4 (&kr)[NPT], const u32x4 (&vr)[NPT], uint32_t sc) {
+  auto store_part = [&](auto kind, int st, const u32x4 (&r)[NPT], uint32_t sc) {
+    constexpr int KIND = decltype(kind)::value;
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       const int idx = threadIdx.x + NT * u;
       if (NV < NT && idx >= NV) break;
       const int row = idx / VPR, col = idx - row * VPR;
+      char *base = KIND == 0 ? smk[st] + row * ROWK : smv[st] + row * ROWV;
       if constexpr (Q8) {
-        char *kd = &sm[st][0][row * ROWB + col * 32], *vd = &sm[st][1][row * ROWB + col * 32];
-        *reinterpret_cast<h8 *>(kd) = i8x8_to_h8_biased(u32x2{kr[u].x, kr[u].y});
-        *reinterpret_cast<h8 *>(kd + 16) = i8x8_to_h8_biased(u32x2{kr[u].z, kr[u].w});
-        *reinterpret_cast<h8 *>(vd) = i8x8_to_h8(u32x2{vr[u].x, vr[u].y});
-        *reinterpret_cast<h8 *>(vd + 16) = i8x8_to_h8(u32x2{vr[u].z, vr[u].w});
+        char *d = base + col * 32;
+        if constexpr (KIND == 0) {
+          *reinterpret_cast<h8 *>(d) = i8x8_to_h8_biased(u32x2{r[u].x, r[u].y});
+          *reinterpret_cast<h8 *>(d + 16) = i8x8_to_h8_biased(u32x2{r[u].z, r[u].w});
+        } else {
+          *reinterpret_cast<h8 *>(d) = i8x8_to_h8(u32x2{r[u].x, r[u].y});
+          *reinterpret_cast<h8 *>(d + 16) = i8x8_to_h8(u32x2{r[u].z, r[u].w});
+        }
       } else {
-        *reinterpret_cast<u32x4 *>(&sm[st][0][row * ROWB + col * 16]) = kr[u];
-        *reinterpret_cast<u32x4 *>(&sm[st][1][row * ROWB + col * 16]) = vr[u];
+        *reinterpret_cast<u32x4 *>(base + col * 16) = r[u];
       }
     }
     if constexpr (Q8) {
-      if ((int)threadIdx.x < 2 * NSC) ssm[st][(int)threadIdx.x / NSC][(int)threadIdx.x % NSC] = (uint16_t)sc;
+      if ((int)threadIdx.x < NSC) ssm[st][KIND][threadIdx.x] = (uint16_t)sc;
     }
   };
+  using KPart = std::integral_constant<int, 0>;
+  using VPart = std::integral_constant<int, 1>;
 
   // Chunks wholly inside every valid row's visible range need no masking
   // (rows past n_members are never stored and need none).
@@ -2523,24 +2591,30 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // so p <= 2^kMqSlack (exact in the f16 hi/lo split). The reference is
   // raised (and the accumulators rescaled) only when a score exceeds it by
   // more than the slack, which after the first chunk is rare; the fast path
-  // needs no cross-lane exchange.
+  // needs no cross-lane exchange. The score product starts its accumulators
+  // at -m_ref (0 while the row has no reference), so they hold s - m_ref.
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   f32x4 o[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mref = [&](int rt) { return m_run[rt] == -INFINITY ? 0.f : m_run[rt]; };
 
   // Scores of 32 tokens (two 16-token tiles) x this wave's 32 rows, from the
-  // K rows of LDS stage st. Consecutive MFMAs go to different accumulators.
+  // K rows of LDS stage st, less the rows' references. Consecutive MFMAs go
+  // to different accumulators.
   auto score = [&](int st, f32x4 (&sc)[2][2]) {
-    const char *ks_base = sm[st][0];
+    const char *ks_base = smk[st];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) sc[tt][0] = sc[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < 2; ++rt) {
+      const float m = -mref(rt);
+      sc[0][rt] = sc[1][rt] = f32x4{m, m, m, m};
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       h8 a[2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
-        a[tt] = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWB + (32 * ks + 8 * lq) * 2);
+        a[tt] = *reinterpret_cast<const h8 *>(ks_base + (tt * 16 + lr) * ROWK + (32 * ks + 8 * lq) * 2);
       if constexpr (Q8) {
         // each k step is one scale group: its product is scaled by the
         // token's K scale d after the bias comes off, d (sum - bias)
@@ -2572,10 +2646,14 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
     }
   };
 
-  // Online softmax of one chunk's scores into the P^T operands. This lane
+  // Online softmax of one chunk's scores into the P^T operand. This lane
   // holds tokens 4 lq + i and 16 + 4 lq + i of its row; k slot j of P^T is
-  // token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4.
-  auto softmax = [&](f32x4 (&sc)[2][2], int c0, float (&pf)[2][8]) {
+  // token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4. f16 products of f16 pools
+  // take P rounded to f16 (ph), and the row sums add the same rounded
+  // values (v_dot2_f32_f16); otherwise P stays f32 (pf) for the split or
+  // the q8_0 scales.
+  constexpr bool PH = F16P && !Q8;
+  auto softmax = [&](f32x4 (&sc)[2][2], int c0, float (&pf)[2][8], h8 (&ph)[2]) {
     float lmax[2];
     if (c0 + kMqChunk > lim_min) {  // wave-uniform: the chunk crosses a row's limit
 #pragma unroll
@@ -2596,42 +2674,56 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
         for (int i = 0; i < 4; ++i) lmax[rt] = __builtin_fmaxf(lmax[rt], sc[tt][rt][i]);
     }
-    const bool over = lmax[0] > m_run[0] + kMqSlack || lmax[1] > m_run[1] + kMqSlack;
+    // With a reference, the scores exceed it by more than the slack; without
+    // one (m_run = -inf), any score above -inf sets it.
+    const bool over = lmax[0] > (m_run[0] == -INFINITY ? -INFINITY : kMqSlack) ||
+                      lmax[1] > (m_run[1] == -INFINITY ? -INFINITY : kMqSlack);
     if (__builtin_amdgcn_ballot_w64(over)) {
       // Raise the reference of the rows some lane found above it; the row
       // max is exchanged over the row's four lanes, so the decision and the
       // new reference are the same in all of them.
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        float mx = lmax[rt];
+        const float m0 = mref(rt);
+        float mx = lmax[rt] + m0;
         mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
         mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
         const bool raise = mx > m_run[rt] + kMqSlack;
         const float alpha = raise ? __builtin_amdgcn_exp2f(m_run[rt] - mx) : 1.f;
+        const float shift = raise ? m0 - mx : 0.f;
         m_run[rt] = raise ? mx : m_run[rt];
         l_run[rt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) sc[tt][rt] += shift;
       }
     }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
-      float ps = 0.f;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pf[rt][tt * 4 + i] = __builtin_amdgcn_exp2f(sc[tt][rt][i] - mref);
-          ps += pf[rt][tt * 4 + i];
-        }
-      l_run[rt] += ps;
+        for (int i = 0; i < 4; ++i) pf[rt][tt * 4 + i] = __builtin_amdgcn_exp2f(sc[tt][rt][i]);
+      if constexpr (PH) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)pf[rt][j];
+        float ps = l_run[rt];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) ps = __builtin_amdgcn_fdot2(h2{ph[rt][j], ph[rt][j + 1]}, h2{1.f16, 1.f16}, ps, false);
+        l_run[rt] = ps;
+      } else {
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ps += pf[rt][j];
+        l_run[rt] += ps;
+      }
     }
   };
 
   // O^T += V^T P^T over the V rows of LDS stage st.
-  auto pv = [&](int st, const float (&pf)[2][8]) {
-    const char *vs_base = sm[st][1];
+  auto pv = [&](int st, const float (&pf)[2][8], const h8 (&php)[2]) {
+    const char *vs_base = smv[st];
     h8 ph[2], pl[2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -2660,8 +2752,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           if constexpr (F16P) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)pf[rt][j];
+            ph[rt] = php[rt];
           } else {
             split_hl(pf[rt], ph[rt], pl[rt]);
           }
@@ -2669,8 +2760,8 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       }
       // V^T operand: d = 16 dt + lr, tokens 4 lq + j (j < 4) and 16 + 4 lq + j - 4.
       const int col = (dt * 16 + 4 * (lr & 3)) * 2;
-      const u32x2 a0 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (4 * lq + (lr >> 2)) * ROWB + col));
-      const u32x2 a1 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (16 + 4 * lq + (lr >> 2)) * ROWB + col));
+      const u32x2 a0 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (4 * lq + (lr >> 2)) * ROWV + col));
+      const u32x2 a1 = __builtin_bit_cast(u32x2, lds_read_tr(vs_base + (16 + 4 * lq + (lr >> 2)) * ROWV + col));
       const h8 a = __builtin_bit_cast(h8, u32x4{a0.x, a0.y, a1.x, a1.y});
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
@@ -2683,26 +2774,53 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
     }
   };
 
-  // Double-buffered staging: the next chunk's global loads are in flight
-  // while the current one is computed.
+  // Chunk loop: K and V of 32 tokens are staged through double-buffered LDS;
+  // global loads run one or two iterations ahead of their LDS stores through
+  // register sets. (Staging K one chunk ahead of V, so that the next chunk's
+  // score product could overlap this chunk's softmax, measured 5-10% slower:
+  // the wave's own VALU and MFMA work already interleave across its tiles.)
+  // Chunks past the range load as zeros (empty extent), so every step is
+  // unconditional.
   const int nch = (jb.t1 - jb.t0 + kMqChunk - 1) / kMqChunk;
-  u32x4 kr[NPT], vr[NPT];
-  uint32_t scv = 0;
-  load_chunk(jb.t0, kr, vr, scv);
-  store_chunk(0, kr, vr, scv);
+  struct Staged {
+    u32x4 k[NPT], v[NPT];
+    uint32_t sk, sv;
+  };
+  // Two register sets in flight: loads run two iterations ahead of their
+  // LDS stores.
+  constexpr bool DEEP = true;
+  auto load_pair = [&](int j, Staged &r) {  // K(j) and V(j)
+    const ChunkBlocks cb = chunk_blocks(j);
+    load_part(KPart{}, j, cb, r.k, r.sk);
+    load_part(VPart{}, j, cb, r.v, r.sv);
+  };
+  auto store_pair = [&](int j, const Staged &r) {
+    store_part(KPart{}, j & 1, r.k, r.sk);
+    store_part(VPart{}, j & 1, r.v, r.sv);
+  };
+  Staged ra, rb;
+  __syncthreads();  // the table entries
+  load_pair(0, ra);
+  if constexpr (DEEP) load_pair(1, rb);
+  store_pair(0, ra);
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
-    const bool more = c + 1 < nch;
-    if (more) load_chunk(jb.t0 + (c + 1) * kMqChunk, kr, vr, scv);
+  auto iter = [&](int c, Staged &ld, Staged &stg) {
+    if constexpr (DEEP) load_pair(c + 2, ld);
+    else load_pair(c + 1, stg);
     if (active) {
       f32x4 sc[2][2];
-      score(c & 1, sc);
       float pf[2][8];
-      softmax(sc, jb.t0 + c * kMqChunk, pf);
-      pv(c & 1, pf);
+      h8 ph[2];
+      score(c & 1, sc);
+      softmax(sc, jb.t0 + c * kMqChunk, pf, ph);
+      pv(c & 1, pf, ph);
     }
-    if (more) store_chunk((c + 1) & 1, kr, vr, scv);
+    store_pair(c + 1, stg);
     __syncthreads();
+  };
+  for (int c = 0; c < nch; c += 2) {
+    iter(c, ra, rb);
+    if (c + 1 < nch) iter(c + 1, rb, ra);
   }
 
   // Partial per row: the row's sum is spread over its four lanes (lq).
@@ -3177,11 +3295,11 @@ int attention_split(int elem, int group, int n_kv_heads) {
   return elem == 1 ? 2 : 1;
 }
 
-int mq_rows(int) { return 32 * kMqWaves; }
+int mq_rows(int, int) { return 32 * kMqWaves; }
 
 bool mq_supported(int elem, int head_dim, int group) {
   return (elem == 2 || elem == 1) && (head_dim == 64 || head_dim == 128) && group >= 1 &&
-         group <= mq_rows(head_dim);
+         group <= mq_rows(elem, head_dim);
 }
 
 hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s) {
@@ -3194,16 +3312,14 @@ hipError_t launch_mq_attention(const PoolGeom &g, const MqArgs &a, hipStream_t s
   auto run = [&](auto tag, auto hd) {
     using T = decltype(tag);
     constexpr int HD = decltype(hd)::value;
-    if (a.f16_products)
-      mq_attn_kernel<T, HD, true><<<grid, 64 * kMqWaves, 0, s>>>(
+    auto go = [&](auto f16p) {
+      mq_attn_kernel<T, HD, decltype(f16p)::value><<<grid, 64 * kMqWaves, 0, s>>>(
           static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
           a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
           g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
-    else
-      mq_attn_kernel<T, HD, false><<<grid, 64 * kMqWaves, 0, s>>>(
-          static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.jobs,
-          a.n_jobs, a.members, a.pre_o, a.pre_ml, a.out, a.n_heads, group, g.n_blocks, g.block_stride,
-          g.slot_stride, qscale, a.max_pre_parts, ksc, vsc);
+    };
+    if (a.f16_products) go(std::true_type{});
+    else go(std::false_type{});
     return hipGetLastError();
   };
   if (g.elem == 2 && a.head_dim == 128) return run(_Float16{}, std::integral_constant<int, 128>{});
