@@ -920,7 +920,7 @@ attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const floa
 // threads with 4 output elements each (16-byte loads and stores), a
 // work-group 256 / (HD/4) pairs; the partition loop is unrolled so several
 // partials are in flight per thread.
-template <int HD>
+template <int HD, int NF>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                   const int32_t *__restrict__ lens, float *__restrict__ out, int n_heads,
@@ -938,14 +938,14 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   const int64_t qi = qmap ? qmap[qx] : qx;
   const int64_t qh = qi * n_heads + h;
   const float *ml = part_ml + qh * max_parts * 2;
-  // The first four partials are loaded before the length is known (slots
+  // The first NF partials are loaded before the length is known (slots
   // clamped to max_parts - 1; slots past the query's np are never used, by
   // selection, so stale values there cannot leak), so the common case costs
   // one round trip.
-  float m4[4], l4[4];
-  f32x4 o4[4];
+  float m4[NF], l4[NF];
+  f32x4 o4[NF];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
+  for (int p = 0; p < NF; ++p) {
     const int pc = p < max_parts ? p : max_parts - 1;
     m4[p] = ml[2 * pc];
     l4[p] = ml[2 * pc + 1];
@@ -963,16 +963,16 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   const int np = (int)((len + pt - 1) / pt);
   if (np <= 1 && npre == 0) return;
   if (np == 1 && folded) return;
-  if (npre == 0 && np <= 4) {
-    // The common case (a query of up to four partitions, np <= max_parts).
+  if (npre == 0 && np <= NF) {
+    // The common case (a query of up to NF partitions, np <= max_parts).
     float mx = m4[0];
 #pragma unroll
-    for (int p = 1; p < 4; ++p) mx = p < np ? __builtin_fmaxf(mx, m4[p]) : mx;
+    for (int p = 1; p < NF; ++p) mx = p < np ? __builtin_fmaxf(mx, m4[p]) : mx;
     const float mref = mx == -INFINITY ? 0.f : mx;
     float lsum = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int p = 0; p < NF; ++p) {
       if (p < np) {
         const float a = __builtin_amdgcn_exp2f(m4[p] - mref);
         lsum += l4[p] * a;
@@ -1017,10 +1017,11 @@ hipError_t launch_merge(const AttnArgs &a, hipStream_t s, bool folded) {
   const int64_t pairs = a.n * a.n_heads;
   constexpr int ppw = 256 / (HD / 4);
   const unsigned mgrid = (unsigned)((pairs + ppw - 1) / ppw);
-  attn_merge_kernel<HD><<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads,
-                                              a.part_tokens, a.split, a.max_parts, a.max_len,
-                                              a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts,
-                                              a.qmap, pairs, folded ? 1 : 0);
+  // One round of loads for queries of up to four (eight) partitions.
+  auto kern = a.max_parts <= 4 ? attn_merge_kernel<HD, 4> : attn_merge_kernel<HD, 8>;
+  kern<<<mgrid, 256, 0, s>>>(a.part_o, a.part_ml, a.lens, a.out, a.n_heads, a.part_tokens, a.split, a.max_parts,
+                             a.max_len, a.pre_parts, a.pre_o, a.pre_ml, a.max_pre_parts, a.qmap, pairs,
+                             folded ? 1 : 0);
   return hipGetLastError();
 }
 
