@@ -1556,10 +1556,15 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   // short (forks reading a few private blocks), their per-query pass takes
   // the plan's partition unless one is fixed; long remainders keep the
   // per-query policy.
+  // Such remainders are not cut further (the q8_0 decode cut): a remainder in
+  // one partition lets its wave fold the group partials itself, with no merge
+  // launch (q8_0 config-3 step: the merge took ~11 us of ~98).
   int part = (int)c->attn_part_tokens;
-  if (grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder) part = P.suffix_part;
+  const bool short_rem = grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder;
+  if (short_rem) part = P.suffix_part;
   const int parts = ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
-  const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim));
+  const int split =
+      short_rem ? 1 : ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim));
   const size_t max_parts = (size_t)parts * split;
   if ((uint64_t)P.n * (P.n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
