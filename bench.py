@@ -9,8 +9,10 @@ paged decode-attention pass over the contexts including it; contexts grow by
 one per step. `value` times the step as one launch (ltkv_append_decode_attention:
 the attention kernel writes and uses each new row); the same steps as two
 launches (write kernel, then attention) give `unfused_step_us` and the
-per-kernel `append_us` / `attention_us`. Inputs are synthetic (seeded N(0,1))
-and resident in HBM before the timed region.
+per-kernel `append_us` / `attention_us`; `attention_valu_us` times the same
+attention launches on the vector-ALU kernels (LTKV_ENGINE_VALU, no matrix
+cores). Inputs are synthetic (seeded N(0,1)) and resident in HBM before the
+timed region.
 
 Prints one JSON line: the metric, µs per step, the attention kernel's roofline
 (algorithmic bytes / HIP-event time of the unfused attention launch vs 8 TB/s),
@@ -1221,6 +1223,11 @@ def main():
     us_step, att_us, app_us, wall = _time_decode(w, steps, warmup)
     graph_us = _time_decode_graph(w, steps)
     fused_us = _time_decode_fused(w, steps, warmup)
+    # The same steps on the vector-ALU kernels (LTKV_ENGINE_VALU: no matrix
+    # cores), the design the matrix-core kernel is measured against.
+    w.kv.set_attention_engine("valu")
+    _, valu_att_us, _, _ = _time_decode(w, steps, warmup)
+    w.kv.set_attention_engine("auto")
     att_bytes = float(np.mean([w.attention_bytes(s) for s in range(steps)]))
     att_gbps = att_bytes / (att_us * 1e-6) / 1e9
     app_gbps = w.append_bytes() / (app_us * 1e-6) / 1e9
@@ -1264,6 +1271,8 @@ def main():
         "append_frac": round(app_gbps / PEAK_HBM_GBPS, 4),
         "unfused_step_us": round(us_step, 2),
         "graph_step_us": round(graph_us, 2),
+        "attention_valu_us": round(valu_att_us, 2),
+        "attention_valu_frac": round(att_bytes / (valu_att_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(att_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(att_gbps / PEAK_HBM_GBPS, 4), "traffic": _profiled_traffic(),
                      "traffic_source": TRAFFIC_PROFILE,

@@ -253,6 +253,24 @@ LTKV_API int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n,
  * Tuning knob. */
 LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);
 
+/* Engines of the decode attention kernels (ltkv_set_attention_engine). */
+#define LTKV_ENGINE_AUTO 0 /* f16 and Q8_0 pools on the matrix cores, f32 on the vector ALU */
+#define LTKV_ENGINE_VALU 1 /* f16 pools on the vector ALU as well */
+
+/* Which kernels run decode attention (ltkv_decode_attention, _rows, _noalloc,
+ * ltkv_append_decode_attention and the per-query pass of planned attention)
+ * on this cache. LTKV_ENGINE_AUTO (the default) takes the matrix-core kernel
+ * for f16 and Q8_0 pools. LTKV_ENGINE_VALU takes, for f16 pools, the
+ * vector-ALU kernels (wave-wide dot products and shuffle reductions, no
+ * MFMA: the bandwidth-bound design) that f32 pools always use; the fused
+ * append then runs as ltkv_write followed by attention, and group partials
+ * are folded by the merge. Results match the reference within the same
+ * tolerance either way, and a query's result stays independent of the rest
+ * of the batch. Refused (LTKV_ERR_ARG) on Q8_0 pools. No reference
+ * counterpart: it keeps the two kernel designs measurable against each
+ * other on one build. */
+LTKV_API int ltkv_set_attention_engine(ltkv_cache *c, int engine);
+
 /* ---- planned attention (one step descriptor, reused by every layer) ---- */
 
 /* Flags of ltkv_plan_attention. */

@@ -34,6 +34,8 @@ pub mod ffi {
     pub const LTKV_PLAN_SHARED_PREFIX: c_uint = 1;
     pub const LTKV_PLAN_F16_PRODUCTS: c_uint = 2;
     pub const LTKV_NOALLOC_SCRATCH_BYTES: usize = 32 << 20;
+    pub const LTKV_ENGINE_AUTO: c_int = 0;
+    pub const LTKV_ENGINE_VALU: c_int = 1;
 
     #[link(name = "ltkv")]
     extern "C" {
@@ -91,6 +93,7 @@ pub mod ffi {
                                             d_k: *const f32, d_v: *const f32, src_stride: usize,
                                             d_out: *mut f32) -> c_int;
         pub fn ltkv_set_attention_partition(c: *mut ltkv_cache, tokens: usize) -> c_int;
+        pub fn ltkv_set_attention_engine(c: *mut ltkv_cache, engine: c_int) -> c_int;
 
         // planned attention
         pub fn ltkv_plan_attention(c: *mut ltkv_cache, n: usize, seqs: *const u32, lens: *const u32,
@@ -299,6 +302,11 @@ impl KvCache {
 
     pub fn set_attention_partition(&mut self, tokens: usize) -> anyhow::Result<()> {
         check(unsafe { ltkv_set_attention_partition(self.raw, tokens) })
+    }
+
+    /// `LTKV_ENGINE_AUTO` or `LTKV_ENGINE_VALU` (f16 pools on the vector ALU).
+    pub fn set_attention_engine(&mut self, engine: c_int) -> anyhow::Result<()> {
+        check(unsafe { ltkv_set_attention_engine(self.raw, engine) })
     }
 
     pub fn rope_init(&mut self, base: f32, rope_dim: usize, head_dim: usize, neox: bool,

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libltkv.so"
 OK, ERR_FULL, ERR_NONCONTIG, ERR_RANGE, ERR_HIP, ERR_ARG = 0, 1, 2, 3, 4, 5
 F16, F32, Q8_0 = 0, 1, 2
 PLAN_SHARED_PREFIX, PLAN_F16_PRODUCTS = 1, 2
+ENGINE_AUTO, ENGINE_VALU = 0, 1
 NO_DEVICE = -1
 BLOCK = 16
 NOALLOC_SCRATCH_BYTES = 32 << 20  # LTKV_NOALLOC_SCRATCH_BYTES
@@ -53,6 +54,7 @@ SIGNATURES = {
     "ltkv_append_decode_attention": (_int, [_vp, _sz, _sz, _sz, _sz, _f32, _vp, _vp, _sz, _vp, _vp, _vp, _vp,
                                             _sz, _vp]),
     "ltkv_set_attention_partition": (_int, [_vp, _sz]),
+    "ltkv_set_attention_engine": (_int, [_vp, _int]),
     "ltkv_plan_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _u32]),
     "ltkv_planned_attention": (_int, [_vp, _sz, _f32, _vp, _vp]),
     "ltkv_plan_stats": (_int, [_vp, _vp]),

@@ -146,6 +146,7 @@ struct ltkv_cache {
   // creation; shared by every cache on the device.
   uint8_t *scratch = nullptr;
   size_t attn_part_tokens = 0;  // 0 = automatic
+  int attn_engine = LTKV_ENGINE_AUTO;
 
   // RoPE table (ltkv_rope_init): [max_pos][rope_dim / 2] of (cos, sin).
   float *rope = nullptr;
@@ -519,6 +520,7 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   a.part_tokens = part;
   a.max_parts = max_parts;
   a.split = 1;
+  a.valu = c->attn_engine == LTKV_ENGINE_VALU && c->elem == 2;
   a.status = c->d_status;
   return a;
 }
@@ -1283,6 +1285,16 @@ int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_tables,
   return LTKV_OK;
 }
 
+int ltkv_set_attention_engine(ltkv_cache *c, int engine) {
+  if (!c) return fail(LTKV_ERR_ARG, "cache is null");
+  if (engine != LTKV_ENGINE_AUTO && engine != LTKV_ENGINE_VALU)
+    return fail(LTKV_ERR_ARG, "unknown attention engine %d", engine);
+  if (engine == LTKV_ENGINE_VALU && c->elem == 1)
+    return fail(LTKV_ERR_ARG, "the vector-ALU engine serves f16 and f32 pools, not Q8_0");
+  c->attn_engine = engine;
+  return LTKV_OK;
+}
+
 int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens) {
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (tokens % 64 != 0 || tokens > (size_t{1} << 30))
@@ -1406,8 +1418,10 @@ int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n
   if (src_stride < c->kv_dim || src_stride % 4 != 0)
     return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim and a multiple of 4");
   if (((uintptr_t)d_k | (uintptr_t)d_v) % 16 != 0) return fail(LTKV_ERR_ARG, "K/V rows must be 16-byte aligned");
-  if (c->elem != 2 || !ltkv::attention_tuned(2, (int)head_dim, (int)group)) {
-    // fused only on f16 pools of the tuned shapes: append, then attention, as two launches
+  if (c->elem != 2 || !ltkv::attention_tuned(2, (int)head_dim, (int)group) ||
+      c->attn_engine == LTKV_ENGINE_VALU) {
+    // fused only on f16 pools of the tuned shapes with the matrix-core kernel:
+    // otherwise append, then attention, as two launches
     if (int rc = ltkv_write(c, layer, n, d_slot_mapping, d_k, d_v, src_stride)) return rc;
     return ltkv_decode_attention(c, layer, n, n_heads, head_dim, scale, d_q, d_tables, table_stride,
                                  d_lens, d_out);

@@ -123,6 +123,10 @@ struct AttnArgs {
   int max_pre_parts;
   // Queries the launch covers: qmap[0..n) (query indices), or all n when null.
   const int32_t *qmap;
+  // f16 pools: the vector-ALU kernels (attn16_kernel / attn_kernel) instead
+  // of the matrix-core one (LTKV_ENGINE_VALU); they write partials for every
+  // multi-partition query and leave group partials to the merge.
+  bool valu;
   // Fault word (int32[2], or nullptr): a table entry outside the pool that a
   // query's context covers (read as block 0) ORs 1 into status[0], a fused
   // append whose cell is not position lens[i] - 1 of the query's table ORs

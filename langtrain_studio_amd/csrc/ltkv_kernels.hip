@@ -629,6 +629,16 @@ template <typename T>
 struct Tile;
 
 template <>
+struct Tile<_Float16> {
+  static constexpr int E = 8;  // elements per 16-byte load
+  __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[8]) {
+    const h8 h = __builtin_bit_cast(h8, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
+  }
+};
+
+template <>
 struct Tile<float> {
   static constexpr int E = 4;
   __device__ static __forceinline__ void unpack(const u32x4 &u, float (&f)[4]) {
@@ -2286,12 +2296,21 @@ hipError_t launch_attn_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
 
 // f16 and q8_0 pools take the matrix-core kernel. f32 pools (no f32 MFMA
 // form keeps the products exact at this rate) stay on the VALU: 16 lanes per
-// row (f32 x 64) take attn16_kernel, 32 lanes per row (f32 x 128) attn_kernel.
+// row (f32 x 64, f16 x 128) take attn16_kernel, other rows attn_kernel. f16
+// pools take the VALU kernels too when the caller asks for them
+// (LTKV_ENGINE_VALU: the bandwidth-bound design without matrix cores, kept
+// to measure the two against each other).
 template <typename T, int HD>
 constexpr bool kRow16 = HD / Tile<T>::E == 16;
 
 template <typename T, int HD, int G>
 hipError_t launch_attn_g(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  if constexpr (std::is_same_v<T, _Float16>) {
+    if (a.valu) {
+      if constexpr (kRow16<T, HD>) return launch_attn16_t<T, HD, G>(g, a, s);
+      else return launch_attn_t<T, HD, G>(g, a, s);
+    }
+  }
   if constexpr (!std::is_same_v<T, float>) {
     if constexpr (G <= 4) {
       if (a.n_kv_heads % 2 == 0) return launch_attn_mfma_t<T, HD, G, 2>(g, a, s);

@@ -447,6 +447,14 @@ class KvCache:
     def set_attention_partition(self, tokens: int) -> None:
         _check(self._lib.ltkv_set_attention_partition(self._h, tokens))
 
+    def set_attention_engine(self, engine: str) -> None:
+        """'auto' (matrix cores for f16 and q8_0 pools) or 'valu' (f16 pools on
+        the vector-ALU kernels, as f32 pools always are)."""
+        codes = {"auto": _lib.ENGINE_AUTO, "valu": _lib.ENGINE_VALU}
+        if engine not in codes:
+            raise ValueError(f"engine must be one of {sorted(codes)}")
+        _check(self._lib.ltkv_set_attention_engine(self._h, codes[engine]))
+
     def read_pool(self, layer: int = 0) -> tuple[np.ndarray, np.ndarray]:
         """Raw K and V pools of one layer, [n_blocks][16][kv_dim] on the host
         (f16 bits as uint16, float32, or q8_0 quants as int8)."""
