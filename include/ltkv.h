@@ -236,8 +236,9 @@ LTKV_API int ltkv_decode_attention_noalloc(ltkv_cache *c, size_t layer, size_t n
  * LTKV_ERR_ARG). A negative or out-of-range cell is skipped, as by
  * ltkv_write. On f16 pools the
  * attention kernel writes and uses each new row itself; on f32 and Q8_0
- * pools this is ltkv_write followed by ltkv_decode_attention. No reference
- * counterpart: the reference writes then attends per layer. */
+ * pools, and on f16 pools set to LTKV_ENGINE_VALU, this is ltkv_write
+ * followed by ltkv_decode_attention. No reference counterpart: the reference
+ * writes then attends per layer. */
 LTKV_API int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads,
                                           size_t head_dim, float scale, const float *d_q,
                                           const int32_t *d_tables, size_t table_stride,
