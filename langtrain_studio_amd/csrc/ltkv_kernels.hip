@@ -47,6 +47,7 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef __fp16 hf4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) hf4 lds_hf4;
@@ -2368,13 +2369,27 @@ constexpr int kMqChunk = 32;       // tokens per staging step
 constexpr int kMqTabMax = kMqMaxRange / 16;  // table entries of one job's token range
 constexpr float kMqSlack = 8.f;    // log2 headroom of the softmax reference
 
-__device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo) {
+// x = hi + lo with hi = f16(x) and lo = f16(x - hi); x - hi is exact in f32.
+// m1 holds -1 in a register the compiler cannot see through, so x - hi stays
+// one v_fma_mix_f32 on the packed f16 hi (a literal -1 turns it into a
+// conversion back to f32 and a subtraction), and hi is converted once, two
+// elements per v_cvt_pk_f16_f32.
+__device__ __forceinline__ void split_hl(const float (&x)[8], h8 &hi, h8 &lo, float m1) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const _Float16 h = (_Float16)x[j];
-    hi[j] = h;
-    lo[j] = (_Float16)__builtin_fmaf((float)h, -1.f, x[j]);  // x - h, exact in f32 (v_fma_mix)
+  for (int j = 0; j < 8; j += 2) {
+    const h2 h = __builtin_convertvector(f32x2{x[j], x[j + 1]}, h2);
+    hi[j] = h[0];
+    hi[j + 1] = h[1];
+    lo[j] = (_Float16)__builtin_fmaf((float)h[0], m1, x[j]);
+    lo[j + 1] = (_Float16)__builtin_fmaf((float)h[1], m1, x[j + 1]);
   }
+}
+
+// -1.f in a register that the optimiser treats as unknown (for split_hl).
+__device__ __forceinline__ float opaque_minus_one() {
+  float m1 = -1.f;
+  asm volatile("" : "+v"(m1));
+  return m1;
 }
 
 
@@ -2471,7 +2486,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
         for (int e = 0; e < 8; ++e) qh[rt][ks][e] = (_Float16)x[ks][e];
       } else {
-        split_hl(x[ks], qh[rt][ks], ql[rt][ks]);
+        split_hl(x[ks], qh[rt][ks], ql[rt][ks], -1.f);
       }
     }
   }
@@ -2607,6 +2622,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
     const int other = __shfl_xor(lim_min, off);
     lim_min = other < lim_min ? other : lim_min;
   }
+  lim_min = __builtin_amdgcn_readfirstlane(lim_min);  // the same in every lane now
 
   // Softmax reference per row: p = 2^(s - m_ref) with s <= m_ref + kMqSlack,
   // so p <= 2^kMqSlack (exact in the f16 hi/lo split). The reference is
@@ -2619,6 +2635,10 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mref = [&](int rt) { return m_run[rt] == -INFINITY ? 0.f : m_run[rt]; };
+  // Start of the score accumulators, -reference, changed only where the
+  // reference is raised.
+  f32x4 sinit[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const float m1 = opaque_minus_one();
 
   // Scores of 32 tokens (two 16-token tiles) x this wave's 32 rows, from the
   // K rows of LDS stage st, less the rows' references. Consecutive MFMAs go
@@ -2634,10 +2654,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   };
   auto score = [&](int st, const h8 (&ka)[KS][2], f32x4 (&sc)[2][2]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const float m = -mref(rt);
-      sc[0][rt] = sc[1][rt] = f32x4{m, m, m, m};
-    }
+    for (int rt = 0; rt < 2; ++rt) sc[0][rt] = sc[1][rt] = sinit[rt];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const h8 a[2] = {ka[ks][0], ka[ks][1]};
@@ -2718,6 +2735,8 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
         const float alpha = raise ? __builtin_amdgcn_exp2f(m_run[rt] - mx) : 1.f;
         const float shift = raise ? m0 - mx : 0.f;
         m_run[rt] = raise ? mx : m_run[rt];
+        const float nm = -mref(rt);
+        sinit[rt] = f32x4{nm, nm, nm, nm};
         l_run[rt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
@@ -2739,9 +2758,9 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
         for (int j = 0; j < 8; j += 2) ps = __builtin_amdgcn_fdot2(h2{ph[rt][j], ph[rt][j + 1]}, h2{1.f16, 1.f16}, ps, false);
         l_run[rt] = ps;
       } else {
-        float ps = 0.f;
+        float ps = pf[rt][0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ps += pf[rt][j];
+        for (int j = 1; j < 8; ++j) ps += pf[rt][j];
         l_run[rt] += ps;
       }
     }
@@ -2770,7 +2789,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
 #pragma unroll
               for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)x[j];
             } else {
-              split_hl(x, ph[rt], pl[rt]);
+              split_hl(x, ph[rt], pl[rt], m1);
             }
           }
         }
@@ -2780,7 +2799,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
           if constexpr (F16P) {
             ph[rt] = php[rt];
           } else {
-            split_hl(pf[rt], ph[rt], pl[rt]);
+            split_hl(pf[rt], ph[rt], pl[rt], m1);
           }
         }
       }
@@ -2809,7 +2828,11 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // 406 -> 392 us against two stages; q8_0 pools ~3% slower). Measured and
   // dropped: reading chunk c + 1's K fragments during chunk c's value product
   // (f16 products 3% slower); staging K one chunk ahead of V so that the next
-  // chunk's score product overlaps this chunk's softmax (5-10% slower).
+  // chunk's score product overlaps this chunk's softmax (5-10% slower);
+  // skewing each wave by half a chunk (chunk c + 1's scores beside chunk c's
+  // weight split, chunk c's values beside chunk c + 1's exponentials, the
+  // issue order pinned with sched_group_barrier: prefill 8 x 512 375 -> 392
+  // us, 249 -> 285 us with f16 products).
   // Chunks past the range load as zeros (empty extent), so every step is
   // unconditional.
   const int nch = (jb.t1 - jb.t0 + kMqChunk - 1) / kMqChunk;
