@@ -2432,8 +2432,11 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // q8_0: [stage][K, V][group][token] scales of the staged chunk
   __shared__ __attribute__((aligned(16))) uint16_t ssm[kMqStages][2][Q8 ? NSC : 1];
   // The job's blocks: {byte offset lo, hi, load extent, block id}; extent 0
-  // for blocks outside the pool.
-  __shared__ __attribute__((aligned(16))) i32x4 stab[kMqTabMax];
+  // for blocks outside the pool. kMqTabPad entries past the range read as
+  // {0, 0, 0, -1} (no load, no block), enough for the ring's loads past the
+  // last chunk.
+  constexpr int kMqTabPad = 10;
+  __shared__ __attribute__((aligned(16))) i32x4 stab[kMqTabMax + kMqTabPad];
 
   // The job list is ordered by work-group id (XCD placement is the host's);
   // empty jobs pad it.
@@ -2515,15 +2518,20 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // read and a 64-bit add, with no scalar-memory wait.
   const int32_t *tab = tables + jb.table;
   const int tb0 = jb.t0 >> 4;                       // first table entry of the range
-  const int ntab = (jb.t1 - jb.t0 + 15) >> 4;       // entries of the range (<= kMqTabMax)
+  int ntab = (jb.t1 - jb.t0 + 15) >> 4;             // entries of the range
+  ntab = ntab < kMqTabMax ? ntab : kMqTabMax;        // (the planner keeps ranges within it)
   const uint32_t row_bytes = (uint32_t)(slot_stride * (int64_t)sizeof(T));
-  for (int i = threadIdx.x; i < ntab && i < kMqTabMax; i += NT) {
-    const int32_t blk = tab[tb0 + i];
-    const int valid = jb.t1 - (tb0 + i) * 16;  // rows of the block inside the range (> 0)
-    const bool ok = blk >= 0 && blk < n_blocks;
-    const int64_t off = ok ? (int64_t)blk * block_stride * (int64_t)sizeof(T) : 0;
-    const int ext = ok ? ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * (int)sizeof(T) : 0;
-    stab[i] = i32x4{(int32_t)(uint32_t)off, (int32_t)(off >> 32), ext, ok ? blk : -1};
+  for (int i = threadIdx.x; i < ntab + kMqTabPad; i += NT) {
+    i32x4 e = i32x4{0, 0, 0, -1};
+    if (i < ntab) {
+      const int32_t blk = tab[tb0 + i];
+      const int valid = jb.t1 - (tb0 + i) * 16;  // rows of the block inside the range (> 0)
+      const bool ok = blk >= 0 && blk < n_blocks;
+      const int64_t off = ok ? (int64_t)blk * block_stride * (int64_t)sizeof(T) : 0;
+      const int ext = ok ? ((valid < 16 ? valid : 16) - 1) * (int)row_bytes + HD * (int)sizeof(T) : 0;
+      e = i32x4{(int32_t)(uint32_t)off, (int32_t)(off >> 32), ext, ok ? blk : -1};
+    }
+    stab[i] = e;
   }
   const int64_t head_off = (int64_t)jb.kvh * HD;
   // Chunks start on block boundaries (t0 % 32 == 0) and a wave's share of a
@@ -2532,30 +2540,17 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // zeros with no branch and no traffic.
   const int64_t sgroups = slot_stride >> 5;         // q8_0 scale groups per pool row
   const int64_t shead = (int64_t)jb.kvh * (HD / 32);  // first scale group of this kv head
-  struct ChunkBlocks {
-    int64_t off0, off1;  // byte offsets of the chunk's two blocks (wave-uniform)
-    int ext0, ext1;      // their load extents (wave-uniform)
-    int blk0, blk1;      // their block ids, -1 outside the range or the pool
+  // Table entry e (wave-uniform) as a byte offset and a load extent.
+  auto block_desc = [&](int e, int64_t &off, int &ext) {
+    e = e < kMqTabMax + kMqTabPad ? e : kMqTabMax + kMqTabPad - 1;
+    const i32x4 v = stab[e];
+    off = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(v.y) << 32) |
+                    (uint32_t)__builtin_amdgcn_readfirstlane(v.x));
+    ext = __builtin_amdgcn_readfirstlane(v.z);
   };
-  // The two blocks of chunk j: one LDS read each.
-  auto chunk_blocks = [&](int j) {
-    const int e0 = 2 * j < kMqTabMax ? 2 * j : kMqTabMax - 1;
-    const int e1 = 2 * j + 1 < kMqTabMax ? 2 * j + 1 : kMqTabMax - 1;
-    const i32x4 v0 = stab[e0], v1 = stab[e1];
-    const bool in0 = 2 * j < ntab && 2 * j < kMqTabMax, in1 = 2 * j + 1 < ntab && 2 * j + 1 < kMqTabMax;
-    ChunkBlocks cb;
-    cb.off0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(v0.y) << 32) |
-                        (uint32_t)__builtin_amdgcn_readfirstlane(v0.x));
-    cb.off1 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(v1.y) << 32) |
-                        (uint32_t)__builtin_amdgcn_readfirstlane(v1.x));
-    cb.ext0 = in0 ? __builtin_amdgcn_readfirstlane(v0.z) : 0;
-    cb.ext1 = in1 ? __builtin_amdgcn_readfirstlane(v1.z) : 0;
-    cb.blk0 = in0 ? v0.w : -1;
-    cb.blk1 = in1 ? v1.w : -1;
-    return cb;
-  };
-  // Chunk j of K (KIND 0) or V (KIND 1) into registers.
-  auto load_part = [&](auto kind, int j, const ChunkBlocks &cb, u32x4 (&r)[NPT], uint32_t &sc) {
+  // Chunk j of K (KIND 0) or V (KIND 1) into registers: a wave's rows of the
+  // chunk lie in one of its two blocks, entry 2 j or 2 j + 1.
+  auto load_part = [&](auto kind, int j, u32x4 (&r)[NPT], uint32_t &sc) {
     constexpr int KIND = decltype(kind)::value;
     const char *pool = reinterpret_cast<const char *>((KIND == 0 ? kpool : vpool) + head_off);
     const int c0 = jb.t0 + j * kMqChunk;
@@ -2564,7 +2559,8 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       sc = 0;
       if ((int)threadIdx.x < NSC) {
         const int e = (int)threadIdx.x, tok = c0 + e % kMqChunk;
-        const int32_t blk = (tok & 16) ? cb.blk1 : cb.blk0;
+        const int te = 2 * j + ((tok >> 4) & 1);
+        const int32_t blk = stab[te < kMqTabMax + kMqTabPad ? te : kMqTabMax + kMqTabPad - 1].w;
         if (blk >= 0 && tok < jb.t1) {
           const uint16_t *sp = KIND == 0 ? kscale : vscale;
           sc = sp[((int64_t)blk * sgroups + shead + e / kMqChunk) * 16 + (tok & 15)];
@@ -2576,9 +2572,11 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       const int idx = threadIdx.x + NT * u;
       if (NV < NT && idx >= NV) break;  // wave-uniform: NV is a multiple of 64
       const int row = idx / VPR, col = idx - row * VPR;
-      const bool h1 = (__builtin_amdgcn_readfirstlane(row) & 16) != 0;  // this wave's share is in block 1
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(pool + (h1 ? cb.off1 : cb.off0)), (short)0, h1 ? cb.ext1 : cb.ext0, kBufferWord3);
+      int64_t off;
+      int ext;
+      block_desc(2 * j + ((__builtin_amdgcn_readfirstlane(row) >> 4) & 1), off, ext);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void *)(pool + off), (short)0, ext, kBufferWord3);
       const uint32_t voff = (uint32_t)((c0 + row) & 15) * row_bytes + (uint32_t)col * 16;
       r[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0));
     }
@@ -2631,6 +2629,15 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // needs no cross-lane exchange. The score product starts its accumulators
   // at -m_ref (0 while the row has no reference), so they hold s - m_ref.
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  // f16 products of f16 pools take the row sums on the matrix cores: one
+  // more value tile of ones (lsum, every element the row's sum of the same
+  // f16 weights the numerator takes; prefill 8 x 512 235 -> 231 us). The
+  // other forms add them on the vector ALU (l_run, spread over the row's
+  // four lanes): f32-accurate products would need two more products per
+  // row tile beside their doubled ones (359 -> 369 us), and q8_0 pools
+  // scale the weights per V group.
+  constexpr bool LM = F16P && !Q8;
+  f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   f32x4 o[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2638,6 +2645,9 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // Start of the score accumulators, -reference, changed only where the
   // reference is raised.
   f32x4 sinit[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  // A chunk's row maximum (less the reference) above this takes the raise
+  // path: the slack with a reference, -inf without one (any score sets it).
+  float thr[2] = {-INFINITY, -INFINITY};
   const float m1 = opaque_minus_one();
 
   // Scores of 32 tokens (two 16-token tiles) x this wave's 32 rows, from the
@@ -2692,13 +2702,13 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   // Online softmax of one chunk's scores into the P^T operand. This lane
   // holds tokens 4 lq + i and 16 + 4 lq + i of its row; k slot j of P^T is
   // token j < 4 ? 4 lq + j : 16 + 4 lq + j - 4. f16 products of f16 pools
-  // take P rounded to f16 (ph), and the row sums add the same rounded
-  // values (v_dot2_f32_f16); otherwise P stays f32 (pf) for the split or
-  // the q8_0 scales.
+  // take P rounded to f16 (ph, summed by the products); otherwise P stays
+  // f32 (pf) for the split or the q8_0 scales, and its row sums are added
+  // here.
   constexpr bool PH = F16P && !Q8;
   auto softmax = [&](f32x4 (&sc)[2][2], int c0, float (&pf)[2][8], h8 (&ph)[2]) {
     float lmax[2];
-    if (c0 + kMqChunk > lim_min) {  // wave-uniform: the chunk crosses a row's limit
+    if (c0 + kMqChunk > lim_min) {  // uniform: the chunk crosses a row's limit
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         const int lim = (jb.t1 < limit[rt] ? jb.t1 : limit[rt]) - c0;  // visible tokens of the chunk
@@ -2709,18 +2719,17 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
             if (tt * 16 + 4 * lq + i >= lim) sc[tt][rt][i] = -INFINITY;
       }
     }
+    // NaN-propagating maxima (v_maximum3_f32, no operand canonicalisation):
+    // a NaN score makes its row's output NaN either way.
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       lmax[rt] = sc[0][rt][0];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lmax[rt] = __builtin_fmaxf(lmax[rt], sc[tt][rt][i]);
+        for (int i = 0; i < 4; ++i) lmax[rt] = __builtin_elementwise_maximum(lmax[rt], sc[tt][rt][i]);
     }
-    // With a reference, the scores exceed it by more than the slack; without
-    // one (m_run = -inf), any score above -inf sets it.
-    const bool over = lmax[0] > (m_run[0] == -INFINITY ? -INFINITY : kMqSlack) ||
-                      lmax[1] > (m_run[1] == -INFINITY ? -INFINITY : kMqSlack);
+    const bool over = (lmax[0] > thr[0]) | (lmax[1] > thr[1]);
     if (__builtin_amdgcn_ballot_w64(over)) {
       // Raise the reference of the rows some lane found above it; the row
       // max is exchanged over the row's four lanes, so the decision and the
@@ -2737,7 +2746,9 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
         m_run[rt] = raise ? mx : m_run[rt];
         const float nm = -mref(rt);
         sinit[rt] = f32x4{nm, nm, nm, nm};
+        thr[rt] = m_run[rt] == -INFINITY ? -INFINITY : kMqSlack;
         l_run[rt] *= alpha;
+        lsum[rt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
 #pragma unroll
@@ -2753,11 +2764,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       if constexpr (PH) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) ph[rt][j] = (_Float16)pf[rt][j];
-        float ps = l_run[rt];
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) ps = __builtin_amdgcn_fdot2(h2{ph[rt][j], ph[rt][j + 1]}, h2{1.f16, 1.f16}, ps, false);
-        l_run[rt] = ps;
-      } else {
+      } else if constexpr (!LM) {
         float ps = pf[rt][0];
 #pragma unroll
         for (int j = 1; j < 8; ++j) ps += pf[rt][j];
@@ -2816,6 +2823,16 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
         for (int rt = 0; rt < 2; ++rt)
           o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl[rt], o[dt][rt], 0, 0, 0);
       }
+      if constexpr (LM) {
+        if (dt == 0) {  // the row sums: V^T rows of ones
+          const h8 ones = h8{1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16};
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[rt], lsum[rt], 0, 0, 0);
+            if constexpr (!F16P) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[rt], lsum[rt], 0, 0, 0);
+          }
+        }
+      }
     }
   };
 
@@ -2841,9 +2858,8 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
     uint32_t sk, sv;
   };
   auto load_pair = [&](int j, Staged &r) {  // K(j) and V(j)
-    const ChunkBlocks cb = chunk_blocks(j);
-    load_part(KPart{}, j, cb, r.k, r.sk);
-    load_part(VPart{}, j, cb, r.v, r.sv);
+    load_part(KPart{}, j, r.k, r.sk);
+    load_part(VPart{}, j, r.v, r.sv);
   };
   auto store_pair = [&](int st, const Staged &r) {
     store_part(KPart{}, st, r.k, r.sk);
@@ -2883,12 +2899,18 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
     if (c + 2 < nch) iter(S2{}, c + 2, r0, r1);
   }
 
-  // Partial per row: the row's sum is spread over its four lanes (lq).
+  // Partial per row: the row's sum (lsum, or l_run spread over its four
+  // lanes).
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    float l = l_run[rt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    float l;
+    if constexpr (LM) {
+      l = lsum[rt][0];
+    } else {
+      l = l_run[rt];
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+    }
     if (slot[rt] >= 0 && jb.direct) {  // the row's only contribution: normalised output
       const float inv = l > 0.f ? 1.f / l : 0.f;
       float *po = out + qrow[rt] * HD + 4 * lq;
