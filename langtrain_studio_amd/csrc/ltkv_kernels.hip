@@ -1594,26 +1594,36 @@ constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
 // or uploaded per step on the host; a query's partitions and result bits do
 // not depend on where its items land.
 // ----------------------------------------------------------------------------
-constexpr int kOrderClasses = 16;
+constexpr int kOrderClasses = 32;  // 32-token size classes of an item
 constexpr int kOrderMaxQueries = 256;  // beyond this, query order (the scans would cost more)
 constexpr int kOrderChunks = kOrderMaxQueries / 64;
 
+__device__ __forceinline__ int order_class(int tokens) {
+  return tokens >> 5 < kOrderClasses - 1 ? tokens >> 5 : kOrderClasses - 1;
+}
+
+// Query q's items: `items` partitions, all but the last of the partition's
+// size (class key), the last of the tokens left (class keyl; 0 tokens for an
+// empty query).
 __device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
-                                                  int part_tokens, int split, int &key, int &items, int &clen) {
+                                                  int part_tokens, int split, int &key, int &keyl, int &items,
+                                                  int &clen) {
   int64_t len = lens[q];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
   clen = (int)len;
   const int pt = partition_tokens(len, part_tokens) / split;
   items = len > 0 ? (int)((len + pt - 1) / pt) : 1;
-  key = pt >> 6 < kOrderClasses - 1 ? pt >> 6 : kOrderClasses - 1;
+  key = order_class(pt);
+  keyl = order_class(len > 0 ? (int)(len - (int64_t)(items - 1) * pt) : 0);
 }
 
-// Size class and item count of queries lane, 64 + lane, ... (n <=
+// Size classes and item counts of queries lane, 64 + lane, ... (n <=
 // kOrderMaxQueries; zero past n), and the items per class in `hist`
-// (kOrderClasses ints of LDS). One wave.
+// (kOrderClasses ints of LDS): a query's last partition counts in the class
+// of its own length, so the list is longest first item by item. One wave.
 struct OrderShapes {
-  int key[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
+  int key[kOrderChunks], keyl[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
 };
 
 __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
@@ -1624,12 +1634,14 @@ __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ l
 #pragma unroll
   for (int c = 0; c < kOrderChunks; ++c) {
     sh.key[c] = 0;
+    sh.keyl[c] = 0;
     sh.items[c] = 0;
     sh.len[c] = 0;
     if ((int64_t)c * 64 + lane < n) {
-      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.items[c],
-                        sh.len[c]);
-      atomicAdd(hist + sh.key[c], sh.items[c]);  // LDS
+      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.keyl[c],
+                        sh.items[c], sh.len[c]);
+      if (sh.items[c] > 1) atomicAdd(hist + sh.key[c], sh.items[c] - 1);  // LDS
+      atomicAdd(hist + sh.keyl[c], 1);
     }
   }
   __syncthreads();
@@ -1657,7 +1669,9 @@ __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane
   for (int c = 0; c < kOrderChunks; ++c) {
     const int64_t c0 = (int64_t)c * 64;
     if (c0 >= n) break;
-    const int v = sh.key[c] == cls ? sh.items[c] : 0;
+    // this class's items of the lane's query: its full partitions (parts
+    // 0 .. items - 2) and / or its last one (part items - 1)
+    const int v = (sh.key[c] == cls ? sh.items[c] - 1 : 0) + (sh.keyl[c] == cls ? 1 : 0);
     int incl = v;  // inclusive prefix sum over the wave
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -1670,9 +1684,11 @@ __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane
       const int j = __builtin_ctzll(hit);
       const int end = __builtin_amdgcn_readfirstlane(__shfl(incl, j, 64));
       const int cnt = __builtin_amdgcn_readfirstlane(__shfl(v, j, 64));
+      const int key = __builtin_amdgcn_readfirstlane(__shfl(sh.key[c], j, 64));
+      const int items = __builtin_amdgcn_readfirstlane(__shfl(sh.items[c], j, 64));
       qlen = __builtin_amdgcn_readfirstlane(__shfl(sh.len[c], j, 64));
       qx = c0 + j;
-      part = (int)(t - (end - cnt));
+      part = key == cls ? (int)(t - (end - cnt)) : items - 1;
       return true;
     }
     t -= tot;
