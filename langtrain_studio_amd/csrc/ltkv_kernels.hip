@@ -1698,10 +1698,26 @@ __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane
 
 // The weight operand's part for this lane: the lo part on lo lanes, else
 // the hi part (columns past the group are discarded, any finite value does).
+// For q8_0 weights x = p d the compiler forms both parts with the product
+// inside v_fma_mixlo_f16 (d an f16 operand): two instructions and a select.
 __device__ __forceinline__ _Float16 weight_part(float x, bool lo_lane) {
   const _Float16 h = (_Float16)x;
   const _Float16 l = (_Float16)(x - (float)h);
   return lo_lane ? l : h;
+}
+
+// weight_part of four f32 weights: lo_mult is -1 on lo lanes and 0 on the
+// others, in a register, so f16(fma(f16(x), lo_mult, x)) is either part, one
+// v_fma_mix on the packed hi parts per element.
+__device__ __forceinline__ h4 weight_parts(const float (&x)[4], float lo_mult) {
+  const h2 h01 = __builtin_convertvector(f32x2{x[0], x[1]}, h2);
+  const h2 h23 = __builtin_convertvector(f32x2{x[2], x[3]}, h2);
+  h4 r;
+  r[0] = (_Float16)__builtin_fmaf((float)h01[0], lo_mult, x[0]);
+  r[1] = (_Float16)__builtin_fmaf((float)h01[1], lo_mult, x[1]);
+  r[2] = (_Float16)__builtin_fmaf((float)h23[0], lo_mult, x[2]);
+  r[3] = (_Float16)__builtin_fmaf((float)h23[1], lo_mult, x[3]);
+  return r;
 }
 
 // Stored quants x 8 -> f16 x 8 of 1152 + x (exact; the bias is taken out
@@ -1772,6 +1788,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // 15 - j the lo part of query head j; a column is nonzero only in the
   // operand of its query head's kv head (j / G).
   const bool hi_lane = lr < NQ, lo_lane = lr >= 16 - NQ;
+  float lo_mult = lo_lane ? -1.f : 0.f;  // weight_parts: opaque to the optimiser
+  asm volatile("" : "+v"(lo_mult));
   const int qj = hi_lane ? lr : (lo_lane ? 15 - lr : 0);  // the column's query head in the wave
   const int my_head = qj / G;                             // its kv head in the wave
   // The query operand is fetched (fetch_q) and converted (convert_q) apart:
@@ -1833,9 +1851,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   const int64_t block_bytes = block_stride * (int64_t)sizeof(T);
 
   float m_ref = -INFINITY, l_run = 0.f;  // softmax reference and sum of this lane's column
+  // Set with the reference: the raise threshold (m_ref + slack) and the
+  // exponent offset (m_ref, 0 while there is none).
+  float m_thr = -INFINITY, m_off = 0.f;
   f32x4 o[DT];
   auto reset = [&]() __attribute__((always_inline)) {
     m_ref = -INFINITY;
+    m_thr = -INFINITY;
+    m_off = 0.f;
     l_run = 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2086,33 +2109,34 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
 
     // Softmax against the column's common reference, raised (with the
-    // accumulators rescaled) only when a score exceeds it by the slack.
-    const float lmax = __builtin_fmaxf(__builtin_fmaxf(sc[0], sc[1]), __builtin_fmaxf(sc[2], sc[3]));
-    if (__builtin_amdgcn_ballot_w64(lmax > m_ref + kDecodeSlack)) {
+    // accumulators rescaled) only when a score exceeds it by the slack. The
+    // maxima are NaN-propagating (v_maximum3_f32, no canonicalisation): a
+    // NaN score makes the column's output NaN either way.
+    const float lmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[0], sc[1]),
+                                                     __builtin_elementwise_maximum(sc[2], sc[3]));
+    if (__builtin_amdgcn_ballot_w64(lmax > m_thr)) {
       float mx = __builtin_fmaxf(lmax, __shfl_xor(lmax, 16));
       mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-      if (mx > m_ref + kDecodeSlack) {
+      if (mx > m_thr) {
         const float alpha = __builtin_amdgcn_exp2f(m_ref - mx);
         m_ref = mx;
+        m_thr = mx + kDecodeSlack;
+        m_off = mx;
         l_run *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
       }
     }
-    const float mref = m_ref == -INFINITY ? 0.f : m_ref;
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_off);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
     // O^T += V_a^T P'_a^T for each kv head a of the wave, per 16-row tile
     // of d; P'_a holds the weights of a's query heads (zero elsewhere) and,
     // for q8_0, the V scale of the tile's 32-element group.
     h4 pf = {};
-    if constexpr (!Q8) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = weight_part(p[i], lo_lane);
-    }
+    if constexpr (!Q8) pf = weight_parts(p, lo_mult);
 #pragma unroll
     for (int g = 0; g < KS; ++g) {
       h4 pw = pf;
