@@ -79,6 +79,7 @@ struct AttnPlan {
   size_t n_pass = 0;         // queries of the per-query pass (the rest are completed by groups)
   size_t max_suffix = 0;     // longest remainder (tokens) of a per-query-pass query
   bool empty_with_groups = false;  // a query with group partials and no remainder
+  bool pass_empty = false;         // every per-query-pass query is such a query
   bool f16_products = false;       // LTKV_PLAN_F16_PRODUCTS
   size_t off_tables = 0, off_stables = 0, off_slens = 0, off_pre = 0, off_qmap = 0,
          off_members = 0, off_jobs = 0, bytes = 0;
@@ -697,6 +698,14 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   for (const auto &gr : groups) units += (gr.members.size() + per_job - 1) / per_job * n_kv_heads;
   const size_t waves = (size_t)ltkv::mq_rows((int)c->elem, (int)head_dim) / 32;
   const size_t target = 8 * (size_t)c->device_count_cu / waves;  // two waves per SIMD
+  // Work-groups run one per CU and take their jobs longest first, so no job
+  // should be longer than the average load of one: a group whose range is
+  // longer than the mean tokens per work-group slot is cut into ranges of
+  // about that length (prefill 8 x 512 at contexts up to 7k: the longest
+  // chunk's jobs alone set the kernel's end, 19% past the mean load).
+  size_t work = 0;  // token-rows of all jobs, counted as full ranges
+  for (const auto &gr : groups) work += (gr.members.size() + per_job - 1) / per_job * n_kv_heads * gr.tokens;
+  const size_t mean_tokens = std::max<size_t>(1, work / std::max<size_t>(1, target));
   std::vector<ltkv::MqJob> jobs;
   std::vector<int32_t> members;
   std::vector<int32_t> pre_parts(n, 0);
@@ -708,7 +717,8 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     const Group &gr = groups[gi];
     const size_t tokens = gr.tokens;
     const size_t max_split = std::max<size_t>(1, tokens / kMinPrefixPart);
-    const size_t split = std::max(std::min(max_split, std::max<size_t>(1, (target + units - 1) / units)),
+    const size_t fill = std::max<size_t>((target + units - 1) / units, (tokens + mean_tokens - 1) / mean_tokens);
+    const size_t split = std::max(std::min(max_split, std::max<size_t>(1, fill)),
                                   (tokens + ltkv::kMqMaxRange - 1) / ltkv::kMqMaxRange);
     const size_t pt = ((tokens + split - 1) / split + 31) / 32 * 32;
     const size_t parts = (tokens + pt - 1) / pt;
@@ -776,13 +786,14 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     return fail(LTKV_ERR_ARG, "block tables of this batch are too large");
   std::vector<int32_t> qmap;  // queries left for the per-query pass
   size_t max_suffix = 0;
-  bool empty_with_groups = false;
+  bool empty_with_groups = false, pass_empty = true;
   for (size_t i = 0; i < n; ++i)
     if (pre_parts[i] >= 0) {
       qmap.push_back((int32_t)i);
       const size_t rem = lens[i] > pre_tokens[i] ? lens[i] - pre_tokens[i] : 0;
       max_suffix = std::max(max_suffix, rem);
       if (pre_parts[i] > 0 && rem == 0) empty_with_groups = true;
+      if (pre_parts[i] == 0 || rem > 0) pass_empty = false;
     }
   const bool groups_only = qmap.empty();
 
@@ -800,6 +811,7 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
   P.n_pass = qmap.size();
   P.max_suffix = max_suffix;
   P.empty_with_groups = empty_with_groups;
+  P.pass_empty = pass_empty && !groups_only;
   P.off_tables = 0;
   P.off_stables = align8(P.off_tables + groups.size() * gstride);
   P.off_slens = align8(P.off_stables + n * sstride);
@@ -1599,6 +1611,7 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   // Short remainders in one partition each and no group-only queries: the
   // decode kernel writes every output itself (folding group partials).
   a.merge_free = grouped && part > 0 && P.max_suffix <= (size_t)(part / split) && !P.empty_with_groups;
+  a.pass_empty = grouped && P.pass_empty;
   a.tables = d + P.off_stables;
   a.table_stride = (int64_t)P.sstride;
   a.max_len = (int64_t)(P.sstride * LTKV_BLOCK);

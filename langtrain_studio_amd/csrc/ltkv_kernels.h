@@ -107,6 +107,10 @@ struct AttnArgs {
   // partition, and none with group partials has an empty remainder (the
   // matrix-core kernel folds group partials of single-partition queries).
   bool merge_free;
+  // The caller knows the context kernel has nothing to do: every query has
+  // group partials and an empty remainder, so only the merge runs (it folds
+  // the group partials by itself).
+  bool pass_empty;
   // Fused append (f16 pools, matrix-core kernel): query i's new K/V row
   // (new_k/new_v row i, f32, row stride new_stride) is written to cell
   // new_slots[i], which must be position lens[i] - 1 of the query's table,

@@ -3385,6 +3385,11 @@ hipError_t launch_attn_any_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s
 
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
+  if (a.pass_empty && a.pre_parts) {  // only group partials to fold (a chunk cut into ranges)
+    if (a.head_dim == 64) return launch_merge<64>(a, s, true);
+    if (a.head_dim == 128) return launch_merge<128>(a, s, true);
+    return hipErrorInvalidValue;
+  }
   if (!attention_tuned(g.elem, a.head_dim, a.n_heads / a.n_kv_heads)) {
     // the generic kernel takes whole contexts: no partials, no group partials
     if (a.pre_parts || !attention_supported(g.elem, a.head_dim, a.n_heads / a.n_kv_heads))
