@@ -1696,17 +1696,28 @@ __device__ __forceinline__ bool decode_order_find(int64_t t, int64_t n, int lane
   return false;
 }
 
-// The weight operand's part for this lane: the lo part on lo lanes, else
-// the hi part (columns past the group are discarded, any finite value does).
-// For q8_0 weights x = p d the compiler forms both parts with the product
-// inside v_fma_mixlo_f16 (d an f16 operand): two instructions and a select.
-__device__ __forceinline__ _Float16 weight_part(float x, bool lo_lane) {
-  const _Float16 h = (_Float16)x;
-  const _Float16 l = (_Float16)(x - (float)h);
-  return lo_lane ? l : h;
+// The weight operand's part for each lane: the lo part f16(x - f16(x)) on lo
+// lanes, else the hi part f16(x) (columns past the group are discarded, any
+// finite value does).
+//
+// q8_0 weights x = p d (d the token's V scale, f16): hi = f16(p d), then
+// f16(p d + c) with c = hi * lo_m2 (lo_m2 = -1 on lo lanes, 0 on the others,
+// one v_pk_mul_f16 per pair) is the lo part on lo lanes and hi on the others;
+// p d is exact inside v_fma_mix, so the lo part is f16(p d - hi).
+__device__ __forceinline__ h4 weight_parts_scaled(const float (&p)[4], const h4 &d, const h2 &lo_m2) {
+  h4 r;
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const h2 hi = h2{(_Float16)__builtin_fmaf(p[i], (float)d[i], 0.f),
+                     (_Float16)__builtin_fmaf(p[i + 1], (float)d[i + 1], 0.f)};
+    const h2 c = hi * lo_m2;
+    r[i] = (_Float16)__builtin_fmaf(p[i], (float)d[i], (float)c[0]);
+    r[i + 1] = (_Float16)__builtin_fmaf(p[i + 1], (float)d[i + 1], (float)c[1]);
+  }
+  return r;
 }
 
-// weight_part of four f32 weights: lo_mult is -1 on lo lanes and 0 on the
+// The parts of four f32 weights: lo_mult is -1 on lo lanes and 0 on the
 // others, in a register, so f16(fma(f16(x), lo_mult, x)) is either part, one
 // v_fma_mix on the packed hi parts per element.
 __device__ __forceinline__ h4 weight_parts(const float (&x)[4], float lo_mult) {
@@ -1790,6 +1801,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   const bool hi_lane = lr < NQ, lo_lane = lr >= 16 - NQ;
   float lo_mult = lo_lane ? -1.f : 0.f;  // weight_parts: opaque to the optimiser
   asm volatile("" : "+v"(lo_mult));
+  h2 lo_m2 = lo_lane ? h2{-1.f16, -1.f16} : h2{0.f16, 0.f16};  // weight_parts_scaled
+  asm volatile("" : "+v"(lo_m2));
   const int qj = hi_lane ? lr : (lo_lane ? 15 - lr : 0);  // the column's query head in the wave
   const int my_head = qj / G;                             // its kv head in the wave
   // The query operand is fetched (fetch_q) and converted (convert_q) apart:
@@ -1854,14 +1867,21 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // Set with the reference: the raise threshold (m_ref + slack) and the
   // exponent offset (m_ref, 0 while there is none).
   float m_thr = -INFINITY, m_off = 0.f;
-  f32x4 o[DT];
+  // O^T accumulators. q8_0 pairs keep one set per kv head of the pair (the
+  // lane's own head's set is taken at the end), so the weight operand needs
+  // no per-head zeroing in every scale group; f16 pairs share one set (their
+  // registers are full) and zero the other head's columns once per tile.
+  constexpr int OS = Q8 ? NH : 1;
+  f32x4 oacc[OS][DT];
   auto reset = [&]() __attribute__((always_inline)) {
     m_ref = -INFINITY;
     m_thr = -INFINITY;
     m_off = 0.f;
     l_run = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < OS; ++a)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[a][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
   // One item: a partition [tok0, tok1) of query qi (tiles b0 .. b1 - 1).
@@ -2124,7 +2144,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         m_off = mx;
         l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        for (int a = 0; a < OS; ++a)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[a][dt] *= alpha;
       }
     }
     float p[4];
@@ -2142,24 +2164,34 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       h4 pw = pf;
       if constexpr (Q8) {
         const h4 d = *reinterpret_cast<const h4 *>(&ssc[1][(my_head * KS + g) * 16 + 4 * lq]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pw[i] = weight_part(p[i] * (float)d[i], lo_lane);
+        pw = weight_parts_scaled(p, d, lo_m2);
       }
       h4 pb[NH];
 #pragma unroll
-      for (int a = 0; a < NH; ++a) pb[a] = (NH == 1 || a == my_head) ? pw : h4{};
+      for (int a = 0; a < NH; ++a) pb[a] = (NH == 1 || OS > 1 || a == my_head) ? pw : h4{};
 #pragma unroll
       for (int dt = 2 * g; dt < 2 * g + 2; ++dt)
 #pragma unroll
         for (int a = 0; a < NH; ++a) {
           const hf4 v = lds_read_tr(sv[a] + (4 * lq + (lr >> 2)) * VPITCH + (dt * 16 + 4 * (lr & 3)) * 2);
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, v), pb[a], o[dt], 0, 0, 0);
+          f32x4 &acc = oacc[OS > 1 ? a : 0][dt];
+          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, v), pb[a], acc, 0, 0, 0);
         }
     }
   };
 
   // The item's result: the output (one partition) or its partial.
   auto finish = [&](const Item &it) __attribute__((always_inline)) {
+    // The lane's own head's accumulators.
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = oacc[0][dt];
+    if constexpr (OS > 1) {
+#pragma unroll
+      for (int a = 1; a < OS; ++a)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = a == my_head ? oacc[a][dt] : o[dt];
+    }
     // Column sums over the four lane rows; hi + lo parts of the numerators.
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
