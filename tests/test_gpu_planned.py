@@ -238,6 +238,17 @@ def test_prefill_chunk_causal(gpu, n_heads, n_kv, head_dim, ctx, chunk):
     assert stats["groups"] == 1 and stats["grouped"] == chunk
 
 
+def test_prefill_chunks_with_one_long_context(gpu):
+    """Several prefill chunks, one after a context much longer than the
+    others: the planner cuts only that chunk's range (it exceeds the mean
+    load of a work-group slot), and with no decode queries the per-query
+    pass is the merge alone, which folds every group partial."""
+    rng = np.random.default_rng(46)
+    g, o, seqs, lens = _prefill_state(rng, 4 * 128, [(0, 3000, 128), (1, 200, 128), (2, 90, 96), (3, 0, 64)])
+    stats, *_ = _run(gpu, g, o, seqs, lens, 28, 128, rng)
+    assert stats["groups"] == 4 and stats["grouped"] == 128 + 128 + 96 + 64
+
+
 def test_mixed_step_prefill_decode_and_forks(gpu):
     """A continuous-batching step: two prefill chunks, decode queries that
     share nothing, and decode queries of forked sequences, in one plan."""
