@@ -456,6 +456,17 @@ def bench_long_context(args):
         "attention_frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "attention_bytes": a_bytes,
         "tokens_per_s": round(B / (a_us * 1e-6), 1),
     }
+    if not args.partition:
+        # The default partitions (a function of each query's own length, so
+        # a query's bits do not depend on its batch) favour small batches of
+        # long queries; an engine that knows it runs 32 of them can fix
+        # 4096-token partitions (ltkv_set_attention_partition): 1024 items,
+        # one per SIMD.
+        kv.set_attention_partition(4096)
+        p_us = _time_op(lambda: kv.decode_attention(0, q, tables, lens, n_heads, hd, out=out), reps=10)
+        kv.set_attention_partition(0)
+        line["attention_partition_4096_us"] = round(p_us, 1)
+        line["attention_partition_4096_frac"] = round(a_bytes / (p_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
     del k_out, v_out
     if not args.no_cpu:
         # the oracle on the same state: same allocator order and claims, pool read back
