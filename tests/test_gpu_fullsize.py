@@ -129,6 +129,12 @@ def test_long_context_full_size(gpu):
     o = _oracle_with_pool(kv, n_blocks)
     want = o.attention_tables(0, tables, lens.cpu().numpy(), q.cpu().numpy(), N_HEADS, HD, threads=16)
     attention_close(out, want, "f16")
+    # the same step with 4096-token partitions fixed (8 a query instead of 32),
+    # the setting an engine running dozens of long queries would choose
+    kv.set_attention_partition(4096)
+    out4 = kv.decode_attention(0, q, d_tables, lens, N_HEADS, HD).cpu().numpy()
+    kv.set_attention_partition(0)
+    attention_close(out4, want, "f16")
 
 
 def test_prefix_sharing_full_size(gpu):
