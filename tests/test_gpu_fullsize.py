@@ -6,6 +6,8 @@ properties where it would not.
 * decode step, 64 sequences, contexts U[2048, 4096]: attention against the
   oracle on the read-back pool (tolerance), batch invariance and attention by
   resident rows (bit-exact);
+* the same step on a q8_0 cache: attention against the oracle over the
+  read-back quants and scales, batch invariance (bit-exact);
 * long context, 32 x 32 768 tokens, fully permuted pool (4.3 GB): the gather
   of every sequence equals the f16 rounding of the rows written, in order
   (bit-exact), and attention matches the oracle;
@@ -27,12 +29,12 @@ N_HEADS, N_KV, HD = 32, 8, 128
 KVD = N_KV * HD
 
 
-def _cache(n_blocks, seed):
+def _cache(n_blocks, seed, dtype="f16"):
     import torch
 
     from langtrain_studio_amd import KvCache
 
-    kv = KvCache(1, KVD, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv = KvCache(1, KVD, n_blocks * BLOCK, dtype=dtype, device=0, stream=torch.cuda.current_stream())
     kv.init_free_order(np.random.default_rng(seed).permutation(n_blocks))
     return kv
 
@@ -98,6 +100,41 @@ def test_llama3_decode_step_full_size(gpu):
     rows = torch.from_numpy(kv.seq_rows(np.arange(B, dtype=np.uint32))).cuda()
     by_rows = kv.decode_attention_rows(0, q, rows, d_lens, N_HEADS, HD).cpu().numpy()
     np.testing.assert_array_equal(by_rows.view(np.uint32), out.view(np.uint32))
+
+
+def test_llama3_decode_step_full_size_q8(gpu):
+    """The headline step on a q8_0 cache (the decode-q8 workload): attention
+    against the oracle over the same quants and scales read back from the
+    pool, and batch invariance bit for bit."""
+    import torch
+
+    from oracle import OracleKv
+
+    rng = np.random.default_rng(2025)
+    B = 64
+    ctx = rng.integers(2048, 4097, B)
+    n_blocks = int(np.ceil(sum(-(-(int(c) + 1) // BLOCK) for c in ctx) * 1.1))
+    kv = _cache(n_blocks, 11, dtype="q8_0")
+    seqs = np.repeat(np.arange(B, dtype=np.uint32), ctx + 1)
+    pos = np.concatenate([np.arange(int(c) + 1, dtype=np.uint64) for c in ctx])
+    _write_random(kv, kv.append_batch(seqs, pos), 12)
+    lens = (ctx + 1).astype(np.int32)
+    tables = kv.block_tables(np.arange(B, dtype=np.uint32))
+    q = torch.randn((B, N_HEADS * HD), generator=torch.Generator(device="cuda").manual_seed(13), device="cuda")
+    d_tables, d_lens = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    out = kv.decode_attention(0, q, d_tables, d_lens, N_HEADS, HD).cpu().numpy()
+
+    o = OracleKv(1, KVD, n_blocks * BLOCK, dtype="q8_0")
+    o.load_pool(0, *kv.read_pool(0))
+    ks, vs = kv.read_scales(0)  # [block][group][slot] -> the oracle's [block][slot][group]
+    o.load_scales(0, ks.transpose(0, 2, 1), vs.transpose(0, 2, 1))
+    want = o.attention_tables(0, tables, lens, q.cpu().numpy(), N_HEADS, HD, threads=16)
+    attention_close(out, want, "q8_0")
+
+    sub = np.array([3, 31, 62])
+    alone = kv.decode_attention(0, q[sub].contiguous(), d_tables[sub].contiguous(), d_lens[sub].contiguous(),
+                                N_HEADS, HD).cpu().numpy()
+    np.testing.assert_array_equal(alone.view(np.uint32), out[sub].view(np.uint32))
 
 
 def test_long_context_full_size(gpu):
