@@ -173,7 +173,11 @@ LTKV_API int ltkv_write_rope(ltkv_cache *c, size_t layer, size_t n, const int32_
 /* Kernel 2, block copy: the copy-on-write body of kv.rs:99-110 (all layers,
  * K and V) for n pairs d_pairs[2i] = src block, d_pairs[2i+1] = dst block.
  * ltkv_append and ltkv_append_batch launch it themselves; exposed for bulk
- * use. Pairs with an out-of-range block are skipped. */
+ * use. Pairs with an out-of-range block are skipped. One call takes at most
+ * (2^32 - 1) / (n_layers * 2 * ceil(16 * kv_dim * elem / 16 KiB)) pairs
+ * (4096 pairs and more; 8 KiB chunks below that) and INT32_MAX in any case,
+ * e.g. 33 554 431 pairs for 32 layers of kv_dim 1024 f16; more is
+ * LTKV_ERR_ARG. */
 LTKV_API int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs);
 
 /* Kernel 3, gather: KvCache::rows(layer, seq, len) collected (kv.rs:133-150)
@@ -195,7 +199,12 @@ LTKV_API int ltkv_gather(ltkv_cache *c, size_t layer, size_t n, const int32_t *d
  * 64 or 128 with groups of 1..8 take the tuned kernels, other shapes a
  * generic one (one work-group per query head, whole contexts).
  * d_lens[i] == 0 yields zeros. A table entry outside the pool is read as
- * block 0 and reported by ltkv_synchronize (the reference panics, kv.rs:147). */
+ * block 0 and reported by ltkv_synchronize (the reference panics, kv.rs:147).
+ * Q may have any finite magnitude, as the reference's f32 scores allow
+ * (model.rs:450,455-461): the matrix-core kernels (f16 and Q8_0 pools) take
+ * q * scale * log2(e) as f16 hi + lo operands, and a query head whose
+ * elements reach 65504 (|q| ~ 5.1e5 at head_dim 128) enters the products
+ * scaled by 2^-e, its scores multiplied by 2^e afterwards (both exact). */
 LTKV_API int ltkv_decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size_t head_dim,
                           float scale, const float *d_q, const int32_t *d_tables,
                           size_t table_stride, const int32_t *d_lens, float *d_out);

@@ -170,6 +170,7 @@ pub struct KvCache {
     raw: *mut ltkv_cache,
     /// kv.rs:18 `pub kv_dim`.
     pub kv_dim: usize,
+    dtype: Dtype,
 }
 
 // The handle is owned by one engine thread at a time (scheduler.rs:103-114).
@@ -192,7 +193,11 @@ impl KvCache {
         };
         let mut raw = std::ptr::null_mut();
         check(unsafe { ltkv_create(n_layers, kv_dim, n_tokens, code, device, &mut raw) })?;
-        Ok(Self { raw, kv_dim })
+        Ok(Self { raw, kv_dim, dtype })
+    }
+
+    pub fn dtype(&self) -> Dtype {
+        self.dtype
     }
 
     pub fn as_raw(&self) -> *mut ltkv_cache {
@@ -260,10 +265,21 @@ impl KvCache {
         check(unsafe { ltkv_write_row(self.raw, layer, block, slot, k.as_ptr(), v.as_ptr()) })
     }
 
-    /// kv.rs:133-150 collected: the first `n` K and V rows of `seq` (f16 bits).
+    /// kv.rs:133-150 collected: the first `n` K and V rows of `seq` (f16 bits)
+    /// of an F16 cache (`rows_f32` for an F32 cache; Q8_0 has no rows form).
     pub fn rows(&mut self, layer: usize, seq: u32, n: usize) -> anyhow::Result<(Vec<u16>, Vec<u16>)> {
+        anyhow::ensure!(self.dtype == Dtype::F16, "rows gives f16 rows: the cache holds {:?}", self.dtype);
         let mut k = vec![0u16; n * self.kv_dim];
         let mut v = vec![0u16; n * self.kv_dim];
+        check(unsafe { ltkv_rows(self.raw, layer, seq, n, k.as_mut_ptr().cast(), v.as_mut_ptr().cast()) })?;
+        Ok((k, v))
+    }
+
+    /// The first `n` K and V rows of `seq` of an F32 cache.
+    pub fn rows_f32(&mut self, layer: usize, seq: u32, n: usize) -> anyhow::Result<(Vec<f32>, Vec<f32>)> {
+        anyhow::ensure!(self.dtype == Dtype::F32, "rows_f32 gives f32 rows: the cache holds {:?}", self.dtype);
+        let mut k = vec![0f32; n * self.kv_dim];
+        let mut v = vec![0f32; n * self.kv_dim];
         check(unsafe { ltkv_rows(self.raw, layer, seq, n, k.as_mut_ptr().cast(), v.as_mut_ptr().cast()) })?;
         Ok((k, v))
     }
@@ -349,7 +365,13 @@ impl KvCache {
         Ok((t, l, stride, rows))
     }
 
+    /// The resident tables on the host: `tables` takes stride * rows entries
+    /// and `lengths` rows entries, as `resident_tables` reports them.
     pub fn read_resident_tables(&mut self, tables: &mut [i32], lengths: &mut [i32]) -> anyhow::Result<()> {
+        let (_, _, stride, rows) = self.resident_tables()?;
+        anyhow::ensure!(tables.len() >= stride * rows && lengths.len() >= rows,
+                        "buffers hold {} table entries and {} lengths; the tables need {} and {}",
+                        tables.len(), lengths.len(), stride * rows, rows);
         check(unsafe { ltkv_read_resident_tables(self.raw, tables.as_mut_ptr(), lengths.as_mut_ptr()) })
     }
 
@@ -365,7 +387,12 @@ impl KvCache {
         check(ltkv_read_pool(self.raw, layer, h_k, h_v))
     }
 
+    /// One layer's K and V scale pools of a Q8_0 cache: n_blocks * (kv_dim / 32)
+    /// * 16 f16 bits each, [block][group][slot].
     pub fn read_scales(&mut self, layer: usize, h_k: &mut [u16], h_v: &mut [u16]) -> anyhow::Result<()> {
+        let need = self.n_blocks() * (self.kv_dim / 32) * 16;
+        anyhow::ensure!(h_k.len() >= need && h_v.len() >= need,
+                        "scale buffers hold {} and {} entries; a layer has {}", h_k.len(), h_v.len(), need);
         check(unsafe { ltkv_read_scales(self.raw, layer, h_k.as_mut_ptr(), h_v.as_mut_ptr()) })
     }
 

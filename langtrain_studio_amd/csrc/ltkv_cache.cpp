@@ -134,10 +134,10 @@ struct ltkv_cache {
   int32_t *d_order_counts = nullptr, *d_order_pairs = nullptr;
   size_t order_cap = 0;  // pairs
 
-  // Fault word of the device ops (int32[2], zeroed at creation): kernels OR
-  // in fault bits (a block-table entry outside the pool, a fused append's
-  // cell that is not the query's position len - 1); ltkv_synchronize reports
-  // and clears them.
+  // Fault word of the device ops (int32[4], zeroed at creation): kernels OR
+  // fault bits (a block-table entry outside the pool, a fused append's cell
+  // that is not the query's position len - 1) into word 0 and the query into
+  // word 1; ltkv_synchronize takes them (words 2..3 receive what was taken).
   int32_t *d_status = nullptr;
 
   // Attention workspace (partition partials), grown on demand.
@@ -369,6 +369,26 @@ struct ltkv_cache {
 };
 
 namespace {
+
+// Takes the device ops' fault word in stream order (after everything enqueued
+// before it on the cache's stream): one kernel swaps it to zero on the device,
+// then the taken value is read back. LTKV_OK, or the first fault as
+// LTKV_ERR_RANGE / LTKV_ERR_ARG.
+int take_status(ltkv_cache *c) {
+  HIP_TRY(ltkv::launch_status_take(c->d_status, c->stream), "status launch");
+  int32_t st[2] = {0, 0};
+  HIP_TRY(hipMemcpyAsync(st, c->d_status + 2, sizeof st, hipMemcpyDeviceToHost, c->stream),
+          "hipMemcpyAsync(status)");
+  HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
+  if (st[0] == 0) return LTKV_OK;
+  if (st[0] & 1)  // kv.rs:147 panics on such an index
+    return fail(LTKV_ERR_RANGE,
+                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
+                "block 0 in its place (attention) or copied nothing (gather)",
+                st[1]);
+  return fail(LTKV_ERR_ARG,
+              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
+}
 
 int check_attention_shape(const ltkv_cache *c, size_t n_heads, size_t head_dim, size_t *group) {
   if (head_dim == 0 || c->kv_dim % head_dim != 0)
@@ -954,8 +974,8 @@ int ltkv_create(size_t n_layers, size_t kv_dim, size_t n_tokens, int dtype, int 
     else if ((e = hipMemset(c->v, c->q8() ? 0x80 : 0, bytes)) != hipSuccess) rc = hip_fail(e, "hipMemset(V pool)");
   }
   if (rc == LTKV_OK) {
-    if ((e = hipMalloc((void **)&c->d_status, 2 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMalloc(status)");
-    else if ((e = hipMemset(c->d_status, 0, 2 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMemset(status)");
+    if ((e = hipMalloc((void **)&c->d_status, 4 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMalloc(status)");
+    else if ((e = hipMemset(c->d_status, 0, 4 * sizeof(int32_t))) != hipSuccess) rc = hip_fail(e, "hipMemset(status)");
   }
   const size_t sbytes = c->q8() ? n_layers * c->layer_scales() * 2 : 0;
   if (rc == LTKV_OK && sbytes > 0) {
@@ -1110,13 +1130,17 @@ int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n) {
   return LTKV_OK;
 }
 
-int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
-               const float *d_k, const float *d_v, size_t src_stride) {
+namespace {
+
+// Kernel 1 over n launch rows: source row i, or order[i] of n_rows with an order.
+int write_rows(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping, const float *d_k,
+               const float *d_v, size_t src_stride, const int32_t *d_order, size_t n_rows) {
   if (!c) return fail(LTKV_ERR_ARG, "cache is null");
   if (c->device == LTKV_NO_DEVICE) return no_device();
   if (layer >= c->n_layers) return fail(LTKV_ERR_RANGE, "layer %zu out of range (%zu)", layer, c->n_layers);
   if (n == 0) return LTKV_OK;
   if (!d_slot_mapping || !d_k || !d_v) return fail(LTKV_ERR_ARG, "null device pointer");
+  if (n_rows > (size_t)INT32_MAX) return fail(LTKV_ERR_ARG, "%zu rows exceed 2^31 - 1", n_rows);
   if (src_stride < c->kv_dim) return fail(LTKV_ERR_ARG, "src_stride must be >= kv_dim");
   if (c->kv_dim % 8 == 0) {  // 16-byte row pieces (other row lengths move element-wise)
     if (src_stride % 4 != 0) return fail(LTKV_ERR_ARG, "src_stride must be a multiple of 4");
@@ -1131,12 +1155,59 @@ int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapp
   if (c->q8())
     HIP_TRY(ltkv::launch_write_q8(c->geom, c->k_layer(layer), c->v_layer(layer), c->k_scales(layer),
                                   c->v_scales(layer), d_slot_mapping, d_k, d_v, (int64_t)n,
-                                  (int64_t)src_stride, c->stream),
+                                  (int64_t)src_stride, c->stream, d_order, (int64_t)n_rows),
             "write launch");
   else
     HIP_TRY(ltkv::launch_write(c->geom, c->k_layer(layer), c->v_layer(layer), d_slot_mapping, d_k,
-                               d_v, (int64_t)n, (int64_t)src_stride, c->stream),
+                               d_v, (int64_t)n, (int64_t)src_stride, c->stream, d_order, (int64_t)n_rows),
             "write launch");
+  return LTKV_OK;
+}
+
+}  // namespace
+
+int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+               const float *d_k, const float *d_v, size_t src_stride) {
+  return write_rows(c, layer, n, d_slot_mapping, d_k, d_v, src_stride, nullptr, n);
+}
+
+int ltkv_write_ordered(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+                       const float *d_k, const float *d_v, size_t src_stride, size_t m,
+                       const int32_t *d_order) {
+  if (m > 0 && !d_order) return fail(LTKV_ERR_ARG, "null device pointer");
+  return write_rows(c, layer, m, d_slot_mapping, d_k, d_v, src_stride, d_order, n);
+}
+
+int ltkv_cell_order(const ltkv_cache *c, size_t n, const int32_t *slot_mapping, int32_t *order,
+                    size_t *m) {
+  if (!c || !m) return fail(LTKV_ERR_ARG, "null argument");
+  *m = 0;
+  if (n == 0) return LTKV_OK;
+  if (!slot_mapping || !order) return fail(LTKV_ERR_ARG, "null host pointer");
+  if (n > (size_t)INT32_MAX) return fail(LTKV_ERR_ARG, "%zu rows exceed 2^31 - 1", n);
+  const int64_t n_cells = (int64_t)c->n_blocks * LTKV_BLOCK;
+  size_t k = 0;
+  if ((uint64_t)c->n_blocks > 4 * (uint64_t)n) {
+    // few rows against the pool: sort (cell, row) pairs
+    std::vector<std::pair<int32_t, int32_t>> v;
+    v.reserve(n);
+    for (size_t i = 0; i < n; ++i)
+      if (slot_mapping[i] >= 0 && slot_mapping[i] < n_cells) v.emplace_back(slot_mapping[i], (int32_t)i);
+    std::sort(v.begin(), v.end());
+    for (const auto &e : v) order[k++] = e.second;
+  } else {
+    // counting sort by block, stable: a block's rows in a batch are one
+    // sequence's positions in increasing order (kv.rs:85-121 claims them so),
+    // hence in increasing slot order
+    std::vector<int32_t> start(c->n_blocks + 1, 0);
+    for (size_t i = 0; i < n; ++i)
+      if (slot_mapping[i] >= 0 && slot_mapping[i] < n_cells) ++start[(slot_mapping[i] >> 4) + 1];
+    for (size_t b = 0; b < c->n_blocks; ++b) start[b + 1] += start[b];
+    k = (size_t)start[c->n_blocks];
+    for (size_t i = 0; i < n; ++i)
+      if (slot_mapping[i] >= 0 && slot_mapping[i] < n_cells) order[start[slot_mapping[i] >> 4]++] = (int32_t)i;
+  }
+  *m = k;
   return LTKV_OK;
 }
 
@@ -1225,6 +1296,10 @@ int ltkv_copy_blocks(ltkv_cache *c, size_t n, const int32_t *d_pairs) {
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   if (n > (size_t)INT32_MAX) return fail(LTKV_ERR_ARG, "%zu copy pairs exceed 2^31 - 1", n);
+  const int64_t max_pairs = ltkv::copy_max_pairs(c->geom, (int)c->n_layers, n >= kCopyOrderMinPairs);
+  if ((int64_t)n > max_pairs)
+    return fail(LTKV_ERR_ARG, "%zu copy pairs exceed the %lld one launch takes at this pool shape", n,
+                (long long)max_pairs);
   const int32_t *pairs = d_pairs;
   if (n >= kCopyOrderMinPairs) {
     // Large batch: bucket the pairs by destination first (three small
@@ -1339,8 +1414,12 @@ int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size
   const size_t max_parts = (size_t)parts * split;
   if ((uint64_t)n * (n_heads / group) * max_parts * 256 >= (1ull << 32))
     return fail(LTKV_ERR_ARG, "attention grid too large for one launch");
+  // Shapes outside the tuned kernels run the generic kernel over whole
+  // contexts: no partition partials, so no workspace.
+  const bool tuned = ltkv::attention_tuned((int)c->elem, (int)head_dim, (int)group);
   const ltkv::AttnWorkspace ws =
-      ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts);
+      tuned ? ltkv::attention_workspace((int64_t)n, (int)n_heads, (int)head_dim, (int)max_parts)
+            : ltkv::AttnWorkspace{0, 0, 0};
   uint8_t *base = nullptr;
   if (use_scratch) {
     if ((size_t)ws.bytes > ltkv::kScratchBytes)
@@ -1525,18 +1604,7 @@ int ltkv_read_resident_tables(ltkv_cache *c, int32_t *h_tables, int32_t *h_lengt
                          c->stream),
           "hipMemcpyAsync(resident table lengths)");
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  int32_t st[2] = {0, 0};
-  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
-  if (st[0] == 0) return LTKV_OK;
-  const int32_t zero[2] = {0, 0};
-  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
-  if (st[0] & 1)  // kv.rs:147 panics on such an index
-    return fail(LTKV_ERR_RANGE,
-                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
-                "block 0 in its place (attention) or copied nothing (gather)",
-                st[1]);
-  return fail(LTKV_ERR_ARG,
-              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
+  return take_status(c);
 }
 
 int ltkv_table_uploads(const ltkv_cache *c, uint64_t *entries) {
@@ -1672,18 +1740,7 @@ int ltkv_synchronize(ltkv_cache *c) {
   DeviceGuard dg(c->device);
   if (!dg.ok) return fail(LTKV_ERR_HIP, "hipSetDevice(%d) failed", c->device);
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  int32_t st[2] = {0, 0};
-  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
-  if (st[0] == 0) return LTKV_OK;
-  const int32_t zero[2] = {0, 0};
-  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
-  if (st[0] & 1)  // kv.rs:147 panics on such an index
-    return fail(LTKV_ERR_RANGE,
-                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
-                "block 0 in its place (attention) or copied nothing (gather)",
-                st[1]);
-  return fail(LTKV_ERR_ARG,
-              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
+  return take_status(c);
 }
 
 int ltkv_read_pool(ltkv_cache *c, size_t layer, void *h_k, void *h_v) {
@@ -1716,18 +1773,7 @@ int ltkv_read_scales(ltkv_cache *c, size_t layer, uint16_t *h_k, uint16_t *h_v) 
   HIP_TRY(hipMemcpyAsync(h_k, c->k_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read K scales");
   HIP_TRY(hipMemcpyAsync(h_v, c->v_scales(layer), bytes, hipMemcpyDeviceToHost, c->stream), "read V scales");
   HIP_TRY(c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize(), "synchronize");
-  int32_t st[2] = {0, 0};
-  HIP_TRY(hipMemcpy(st, c->d_status, sizeof st, hipMemcpyDeviceToHost), "hipMemcpy(status)");
-  if (st[0] == 0) return LTKV_OK;
-  const int32_t zero[2] = {0, 0};
-  HIP_TRY(hipMemcpy(c->d_status, zero, sizeof zero, hipMemcpyHostToDevice), "hipMemcpy(status)");
-  if (st[0] & 1)  // kv.rs:147 panics on such an index
-    return fail(LTKV_ERR_RANGE,
-                "a device op read a block-table entry outside the pool (query or sequence %d); it read "
-                "block 0 in its place (attention) or copied nothing (gather)",
-                st[1]);
-  return fail(LTKV_ERR_ARG,
-              "fused append + attention: the cell of query %d is not position len - 1 of its table", st[1]);
+  return take_status(c);
 }
 
 int ltkv_rows(ltkv_cache *c, size_t layer, uint32_t seq, size_t n, void *h_k, void *h_v) {

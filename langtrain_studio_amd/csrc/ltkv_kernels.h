@@ -23,13 +23,16 @@ struct PoolGeom {
 
 // Kernel 1 for q8_0 cells (elem 1): quants into k/v_layer, per-32 f16 scales
 // into k/v_scale ([cell][kv_dim / 32]).
+// With order (n entries), launch row i is source row order[i]; entries outside
+// [0, n_rows) are skipped.
 hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale,
                            void *v_scale, const int32_t *slots, const float *k, const float *v,
-                           int64_t n, int64_t src_stride, hipStream_t s);
+                           int64_t n, int64_t src_stride, hipStream_t s, const int32_t *order = nullptr,
+                           int64_t n_rows = 0);
 
 hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
                         const float *k, const float *v, int64_t n, int64_t src_stride,
-                        hipStream_t s);
+                        hipStream_t s, const int32_t *order = nullptr, int64_t n_rows = 0);
 
 // RoPE geometry: table [max_pos][rope_dim / 2] of (cos, sin) of pos * inv_freq[i].
 struct RopeGeom {
@@ -53,6 +56,8 @@ hipError_t launch_write_rope_q8(const PoolGeom &g, void *k_layer, void *v_layer,
 
 // Kernel 2 over (src, dst) block pairs of every layer; `bulk` selects the
 // form for large batches (pairs in destination order, see launch_copy_order).
+// Most pairs one launch_copy_blocks call takes for this pool geometry.
+int64_t copy_max_pairs(const PoolGeom &g, int n_layers, bool bulk);
 hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
                               const int32_t *pairs, int64_t n_pairs, bool bulk, hipStream_t s);
 
@@ -70,6 +75,9 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
                          const int64_t *out_offsets, int64_t n, void *k_out, void *v_out,
                          int32_t *status, hipStream_t s);
 
+// Fault word int32[4]: moves words 0..1 (fault bits, query) into words 2..3
+// and clears them, in stream order.
+hipError_t launch_status_take(int32_t *status, hipStream_t s);
 // Resident block tables: updates (row, col, value) triples (col -1: the
 // row's length in blocks), and the slot mapping of (row, position) tokens.
 hipError_t launch_table_update(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,

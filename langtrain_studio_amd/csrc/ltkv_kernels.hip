@@ -92,12 +92,15 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 //    1024; the same form on a 4216-token step whose sources sat in the
 //    caches was 37% slower, the loads missing them).
 // ----------------------------------------------------------------------------
+// With `order` (ltkv_write_ordered), launch row i is source row order[i] (rows
+// outside [0, n_rows) are skipped): a batch's rows taken in ascending cell
+// order store into the pool in ascending address order.
 template <int ELEM, bool STREAM>
 __global__ void __launch_bounds__(256)
 write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
              const int32_t *__restrict__ slots, const float *__restrict__ k,
              const float *__restrict__ v, int64_t n, int64_t src_stride, int kv_dim,
-             int64_t n_slots) {
+             int64_t n_slots, const int32_t *__restrict__ order, int64_t n_rows) {
   constexpr int kWriteRows = STREAM ? 2 : 1;
   const int chunks = kv_dim >> 3;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -110,8 +113,14 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
   int32_t s[kWriteRows];
 #pragma unroll
   for (int j = 0; j < kWriteRows; ++j) {
-    const int64_t row = row0 + j < n ? row0 + j : row0;  // a missing second row reloads the first
-    s[j] = row0 + j < n ? slots[row] : -1;
+    int64_t row = row0 + j < n ? row0 + j : row0;  // a missing second row reloads the first
+    bool live = row0 + j < n;
+    if (order) {
+      row = order[row];
+      live = live && row >= 0 && row < n_rows;
+      row = live ? row : 0;
+    }
+    s[j] = live ? slots[row] : -1;
     const f32x4 *ks = reinterpret_cast<const f32x4 *>(k + row * src_stride + col);
     const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
     if constexpr (STREAM) {
@@ -211,12 +220,14 @@ __global__ void __launch_bounds__(256)
 write_q8_kernel(int8_t *__restrict__ kpool, int8_t *__restrict__ vpool, uint16_t *__restrict__ kscale,
                 uint16_t *__restrict__ vscale, const int32_t *__restrict__ slots,
                 const float *__restrict__ k, const float *__restrict__ v, int64_t n, int64_t src_stride,
-                int kv_dim, int64_t n_slots) {
+                int kv_dim, int64_t n_slots, const int32_t *__restrict__ order, int64_t n_rows) {
   const int e8 = kv_dim >> 3;  // 8-element eighths of a K (or V) row
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / (2 * e8);
-  if (row >= n) return;  // whole 4-lane groups leave together (2 e8 is a multiple of 4)
-  const int u = (int)(gid - row * 2 * e8);
+  const int64_t i = gid / (2 * e8);
+  if (i >= n) return;  // whole 4-lane groups leave together (2 e8 is a multiple of 4)
+  const int u = (int)(gid - i * 2 * e8);
+  const int64_t row = order ? order[i] : i;  // write_kernel's order
+  if (order && (row < 0 || row >= n_rows)) return;
   const int32_t s = slots[row];
   if (s < 0 || (int64_t)s >= n_slots) return;
   const bool is_v = u >= e8;
@@ -1581,6 +1592,19 @@ __device__ __forceinline__ h8 i8x8_to_h8(const u32x2 &w) {
 
 constexpr float kDecodeSlack = 8.f;  // log2 headroom of the softmax reference
 
+// The matrix-core products take Q as f16 operands. A query head whose scaled
+// Q (x = q * scale * log2 e) reaches the f16 range (|x| >= 65504) enters them
+// as x * 2^-e, e the smallest exponent that brings its largest element below
+// 2^15 (exact: a power of two), and its scores are taken times 2^e after the
+// product, so the result is the f32 computation's wherever that is finite.
+// Heads inside the range keep e = 0 (factor 1: bits unchanged). amax is the
+// head's largest |x| (NaN elements are ignored; an infinite one keeps e = 0
+// and its scores are infinite or NaN, as in f32).
+__device__ __forceinline__ int q_range_exp(float amax) {
+  if (!(amax >= 65504.f) || !(amax <= 3.40282347e38f)) return 0;
+  return __builtin_amdgcn_frexp_expf(amax) - 15;
+}
+
 // ----------------------------------------------------------------------------
 // Work order of the decode grid. The grid's items are (query, partition)
 // pairs (times the kv-head groups, fastest). Taken in query order, a batch of
@@ -1818,12 +1842,28 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       qr[2 * ks + 1] = *reinterpret_cast<const f32x4 *>(qp + 32 * ks + 4);
     }
   };
+  // Heads beyond the f16 range (q_range_exp): the column's factor 2^e for
+  // its scores, and whether any column of the wave has one (uniform).
+  float qmul = 1.f;
+  bool qscaled = false;
   auto convert_q = [&](const f32x4 (&qr)[2 * KS], h8 (&qb)[NH][KS], float (&qbias)[KS]) __attribute__((always_inline)) {
+    float amax = 0.f;  // over the column's head: its 128 (64) elements lie in lanes lr + 16 lq
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        amax = __builtin_fmaxf(amax, __builtin_fabsf((e < 4 ? qr[2 * ks][e] : qr[2 * ks + 1][e - 4]) * qscale));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32));
+    const int qex = q_range_exp(amax);
+    const float qinv = __builtin_ldexpf(1.f, -qex);
+    qmul = __builtin_ldexpf(1.f, qex);
+    qscaled = __builtin_amdgcn_ballot_w64(qex != 0) != 0;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = (e < 4 ? qr[2 * ks][e] : qr[2 * ks + 1][e - 4]) * qscale;
+        const float x = (e < 4 ? qr[2 * ks][e] : qr[2 * ks + 1][e - 4]) * qscale * qinv;
         const _Float16 h = (_Float16)x;
         const _Float16 part_x = hi_lane ? h : (lo_lane ? (_Float16)(x - (float)h) : (_Float16)0.f);
 #pragma unroll
@@ -2121,6 +2161,10 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     float sc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[i] = s[i] + dpp<0x140>(s[i]);  // hi + lo (row_mirror: lane ^ 15)
+    if (qscaled) {  // uniform: heads beyond the f16 range entered the product as Q' 2^-e
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] *= qmul;
+    }
     const int valid = (int)(cur.tok1 - (int64_t)b * 16);  // rows of this tile inside the context
     if (valid < 16) {
 #pragma unroll
@@ -2525,6 +2569,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   h8 qh[2][KS], ql[2][KS];
   int limit[2];
   int64_t slot[2], qrow[2];
+  float qmul[2];  // per row tile: the lane's row's factor 2^e for its scores (q_range_exp)
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int r = wave * 32 + rt * 16 + lr;
@@ -2555,6 +2600,22 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
         }
       }
     }
+    // a row beyond the f16 range enters the products as x 2^-e (q_range_exp);
+    // its 128 (64) elements lie in lanes lr + 16 lq
+    float amax = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[ks][e]));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32));
+    const int qex = q_range_exp(amax);
+    const float qinv = __builtin_ldexpf(1.f, -qex);
+    qmul[rt] = __builtin_ldexpf(1.f, qex);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[ks][e] *= qinv;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if constexpr (F16P) {
@@ -2565,6 +2626,9 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
       }
     }
   }
+  // Whether any row of the wave entered the products scaled (uniform): its
+  // score accumulators then start at 0 and take s 2^e - reference afterwards.
+  const bool qscaled = __builtin_amdgcn_ballot_w64(qmul[0] != 1.f || qmul[1] != 1.f) != 0;
   // q8_0 K is staged as 1152 + k (exact in f16): 1152 times the row's sum of
   // each k step of Q (hi + lo) comes off every score of that step.
   float qbias[2][KS];
@@ -2736,7 +2800,7 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   };
   auto score = [&](int st, const h8 (&ka)[KS][2], f32x4 (&sc)[2][2]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) sc[0][rt] = sc[1][rt] = sinit[rt];
+    for (int rt = 0; rt < 2; ++rt) sc[0][rt] = sc[1][rt] = qscaled ? f32x4{0.f, 0.f, 0.f, 0.f} : sinit[rt];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const h8 a[2] = {ka[ks][0], ka[ks][1]};
@@ -2768,6 +2832,14 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
               sc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt], ql[rt][ks], sc[tt][rt], 0, 0, 0);
         }
       }
+    }
+    if (qscaled) {  // uniform: rows beyond the f16 range entered as Q 2^-e
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[tt][rt][i] = __builtin_fmaf(sc[tt][rt][i], qmul[rt], sinit[rt][i]);
     }
   };
 
@@ -3016,11 +3088,13 @@ template <int ELEM>
 __global__ void __launch_bounds__(256)
 write_any_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool, const int32_t *__restrict__ slots,
                  const float *__restrict__ k, const float *__restrict__ v, int64_t n, int64_t src_stride,
-                 int64_t kv_dim, int64_t n_slots) {
+                 int64_t kv_dim, int64_t n_slots, const int32_t *__restrict__ order, int64_t n_rows) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid / kv_dim;
-  if (row >= n) return;
-  const int64_t e = gid - row * kv_dim;
+  const int64_t i = gid / kv_dim;
+  if (i >= n) return;
+  const int64_t e = gid - i * kv_dim;
+  const int64_t row = order ? order[i] : i;  // write_kernel's order
+  if (order && (row < 0 || row >= n_rows)) return;
   const int32_t s = slots[row];
   if (s < 0 || (int64_t)s >= n_slots) return;
   const int64_t dst = (int64_t)s * kv_dim + e;
@@ -3192,6 +3266,16 @@ table_update_kernel(int32_t *__restrict__ tables, int32_t *__restrict__ counts, 
     tables[(int64_t)r * width + c] = v;
 }
 
+// Takes the fault word: atomic exchanges with zero, so a fault raised by work
+// running beside this kernel is either taken here or left for the next take.
+__global__ void __launch_bounds__(64) status_take_kernel(int32_t *status) {
+  if (threadIdx.x != 0) return;
+  const int32_t bits = __hip_atomic_exchange(status, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int32_t who = __hip_atomic_exchange(status + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  status[2] = bits;
+  status[3] = who;
+}
+
 // Token i at position pos[i] of the sequence in row rows[i]: cell
 // block * 16 + pos % 16 with block = tables[row][pos / 16] (kv.rs:95-121's
 // (block, slot), flattened as the write kernels take it), or -1 when the row
@@ -3216,31 +3300,33 @@ slot_mapping_kernel(const int32_t *__restrict__ tables, const int32_t *__restric
 
 hipError_t launch_write_q8(const PoolGeom &g, void *k_layer, void *v_layer, void *k_scale,
                            void *v_scale, const int32_t *slots, const float *k, const float *v,
-                           int64_t n, int64_t src_stride, hipStream_t s) {
+                           int64_t n, int64_t src_stride, hipStream_t s, const int32_t *order,
+                           int64_t n_rows) {
   if (n <= 0) return hipSuccess;
   const int64_t threads = n * (g.kv_dim >> 2);
   const int64_t blocks = (threads + 255) / 256;
   write_q8_kernel<<<(unsigned)blocks, 256, 0, s>>>(
       static_cast<int8_t *>(k_layer), static_cast<int8_t *>(v_layer), static_cast<uint16_t *>(k_scale),
-      static_cast<uint16_t *>(v_scale), slots, k, v, n, src_stride, g.kv_dim, g.n_blocks * 16);
+      static_cast<uint16_t *>(v_scale), slots, k, v, n, src_stride, g.kv_dim, g.n_blocks * 16, order, n_rows);
   return hipGetLastError();
 }
 
 template <int ELEM, bool STREAM>
 hipError_t launch_write_form(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
-                             const float *k, const float *v, int64_t n, int64_t src_stride, hipStream_t s) {
+                             const float *k, const float *v, int64_t n, int64_t src_stride, hipStream_t s,
+                             const int32_t *order, int64_t n_rows) {
   constexpr int rows = STREAM ? 2 : 1;
   const int64_t threads = (n + rows - 1) / rows * (g.kv_dim >> 3);
   const int64_t blocks = (threads + 255) / 256;
   write_kernel<ELEM, STREAM><<<(unsigned)blocks, 256, 0, s>>>(
       static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n, src_stride, g.kv_dim,
-      g.n_blocks * 16);
+      g.n_blocks * 16, order, n_rows);
   return hipGetLastError();
 }
 
 hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
                         const float *k, const float *v, int64_t n, int64_t src_stride,
-                        hipStream_t s) {
+                        hipStream_t s, const int32_t *order, int64_t n_rows) {
   if (n <= 0) return hipSuccess;
   if (g.kv_dim % 8 != 0) {  // rows of any length: element-wise
     const int64_t blocks = (n * g.kv_dim + 255) / 256;
@@ -3248,20 +3334,20 @@ hipError_t launch_write(const PoolGeom &g, void *k_layer, void *v_layer, const i
     if (g.elem == 2)
       write_any_kernel<2><<<(unsigned)blocks, 256, 0, s>>>(static_cast<uint8_t *>(k_layer),
                                                            static_cast<uint8_t *>(v_layer), slots, k, v, n,
-                                                           src_stride, g.kv_dim, g.n_blocks * 16);
+                                                           src_stride, g.kv_dim, g.n_blocks * 16, order, n_rows);
     else
       write_any_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(static_cast<uint8_t *>(k_layer),
                                                            static_cast<uint8_t *>(v_layer), slots, k, v, n,
-                                                           src_stride, g.kv_dim, g.n_blocks * 16);
+                                                           src_stride, g.kv_dim, g.n_blocks * 16, order, n_rows);
     return hipGetLastError();
   }
   constexpr int64_t kLastLevelCache = 256ll << 20;  // MALL bytes
   const bool stream = n * (int64_t)g.kv_dim * 8 > kLastLevelCache;
   if (g.elem == 2)
-    return stream ? launch_write_form<2, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s)
-                  : launch_write_form<2, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s);
-  return stream ? launch_write_form<4, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s)
-                : launch_write_form<4, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s);
+    return stream ? launch_write_form<2, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s, order, n_rows)
+                  : launch_write_form<2, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s, order, n_rows);
+  return stream ? launch_write_form<4, true>(g, k_layer, v_layer, slots, k, v, n, src_stride, s, order, n_rows)
+                : launch_write_form<4, false>(g, k_layer, v_layer, slots, k, v, n, src_stride, s, order, n_rows);
 }
 
 hipError_t launch_write_rope(const PoolGeom &g, void *k_layer, void *v_layer, const int32_t *slots,
@@ -3308,10 +3394,18 @@ hipError_t launch_copy_form(const PoolGeom &g, int n_layers, void *k_pool, void 
   constexpr int64_t chunk = (int64_t)THREADS * VEC * 16;
   const int chunks = (int)((block_bytes + chunk - 1) / chunk);
   const int64_t wgs = (int64_t)n_layers * n_pairs * 2 * chunks;
+  if (wgs >= (int64_t{1} << 32)) return hipErrorInvalidValue;  // the grid's x dimension is 32 bits
   copy_blocks_kernel<THREADS, VEC, LAYER_MAJOR><<<(unsigned)wgs, THREADS, 0, s>>>(
       static_cast<uint8_t *>(k_pool), static_cast<uint8_t *>(v_pool), pairs, n_pairs, n_layers, g.n_blocks,
       block_bytes, layer_bytes, chunks);
   return hipGetLastError();
+}
+
+int64_t copy_max_pairs(const PoolGeom &g, int n_layers, bool bulk) {
+  // one work-group per (pair, layer, K or V, chunk); the grid's x dimension is 32 bits
+  const int64_t chunk = bulk ? (int64_t)kCopyBulkThreads * 16 : 256 * 2 * 16;
+  const int64_t chunks = (g.block_stride * g.elem + chunk - 1) / chunk;
+  return ((int64_t{1} << 32) - 1) / ((int64_t)n_layers * 2 * chunks);
 }
 
 hipError_t launch_copy_blocks(const PoolGeom &g, int n_layers, void *k_pool, void *v_pool,
@@ -3380,6 +3474,11 @@ hipError_t launch_slot_mapping(const int32_t *tables, const int32_t *counts, int
   if ((n + 255) / 256 >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   slot_mapping_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tables, counts, width, n_rows, rows,
                                                                   pos, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_status_take(int32_t *status, hipStream_t s) {
+  status_take_kernel<<<1, 64, 0, s>>>(status);
   return hipGetLastError();
 }
 

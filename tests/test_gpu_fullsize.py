@@ -6,6 +6,9 @@ properties where it would not.
 * decode step, 64 sequences, contexts U[2048, 4096]: attention against the
   oracle on the read-back pool (tolerance), batch invariance and attention by
   resident rows (bit-exact);
+* the same step as one fused append + attention launch (the timed entry
+  point): bit-equal to write + attention on a twin cache, within tolerance
+  of the oracle on both attention engines;
 * the same step on a q8_0 cache: attention against the oracle over the
   read-back quants and scales, batch invariance (bit-exact);
 * long context, 32 x 32 768 tokens, fully permuted pool (4.3 GB): the gather
@@ -100,6 +103,62 @@ def test_llama3_decode_step_full_size(gpu):
     rows = torch.from_numpy(kv.seq_rows(np.arange(B, dtype=np.uint32))).cuda()
     by_rows = kv.decode_attention_rows(0, q, rows, d_lens, N_HEADS, HD).cpu().numpy()
     np.testing.assert_array_equal(by_rows.view(np.uint32), out.view(np.uint32))
+
+
+def test_llama3_fused_step_full_size(gpu):
+    """The decode step as the headline times it: ltkv_append_decode_attention
+    (model.rs:414-475 for one layer in one launch: the new K/V rows written
+    by the waves of each query's last partition, attention over len = ctx + 1)
+    at 64 sequences x U[2048, 4096] over a permuted pool, 64 queries x 4
+    partitions taken longest first.
+    * outputs and pools bit-equal to write + decode_attention on a twin cache;
+    * outputs within the f16 tolerance of the oracle on the read-back pool;
+    * the same step on the vector-ALU engine within the same tolerance."""
+    import torch
+
+    rng = np.random.default_rng(2026)
+    B = 64
+    ctx = rng.integers(2048, 4097, B)
+    n_blocks = int(np.ceil(sum(-(-(int(c) + 1) // BLOCK) for c in ctx) * 1.1))
+    fused, twin = _cache(n_blocks, 21), _cache(n_blocks, 21)
+    seqs = np.repeat(np.arange(B, dtype=np.uint32), ctx)
+    pos = np.concatenate([np.arange(int(c), dtype=np.uint64) for c in ctx])
+    sm = fused.append_batch(seqs, pos)
+    np.testing.assert_array_equal(twin.append_batch(seqs, pos), sm)
+    _write_random(fused, sm, 22)
+    _write_random(twin, sm, 22)
+    step_seqs, step_pos = np.arange(B, dtype=np.uint32), ctx.astype(np.uint64)
+    step_sm = fused.append_batch(step_seqs, step_pos)
+    np.testing.assert_array_equal(twin.append_batch(step_seqs, step_pos), step_sm)
+    assert (step_sm % BLOCK == 0).any() and (step_sm % BLOCK != 0).any()
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    k = torch.randn((B, KVD), generator=gen, device="cuda")
+    v = torch.randn((B, KVD), generator=gen, device="cuda")
+    q = torch.randn((B, N_HEADS * HD), generator=gen, device="cuda")
+    lens = (ctx + 1).astype(np.int32)
+    tables = fused.block_tables(step_seqs)
+    d_sm, d_tables, d_lens = (torch.from_numpy(x).cuda() for x in (step_sm, tables, lens))
+
+    one = fused.append_decode_attention(0, d_sm, k, v, q, d_tables, d_lens, N_HEADS, HD).cpu().numpy()
+    twin.write_batch(0, d_sm, k, v)
+    two = twin.decode_attention(0, q, d_tables, d_lens, N_HEADS, HD).cpu().numpy()
+    np.testing.assert_array_equal(one.view(np.uint32), two.view(np.uint32))
+    fk, fv = fused.read_pool(0)
+    tk, tv = twin.read_pool(0)
+    np.testing.assert_array_equal(fk, tk)
+    np.testing.assert_array_equal(fv, tv)
+    del fk, fv, tk, tv, twin
+
+    o = _oracle_with_pool(fused, n_blocks)
+    want = o.attention_tables(0, tables, lens, q.cpu().numpy(), N_HEADS, HD, threads=16)
+    attention_close(one, want, "f16")
+
+    # the vector-ALU engine runs the same entry point as write + attention
+    fused.set_attention_engine("valu")
+    valu = fused.append_decode_attention(0, d_sm, k, v, q, d_tables, d_lens, N_HEADS, HD).cpu().numpy()
+    fused.set_attention_engine("auto")
+    attention_close(valu, want, "f16")
+    assert not np.array_equal(valu.view(np.uint32), one.view(np.uint32))
 
 
 def test_llama3_decode_step_full_size_q8(gpu):

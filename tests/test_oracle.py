@@ -342,6 +342,61 @@ def test_attention_thread_count_does_not_change_bits():
     np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32", "q8_0"])
+def test_attention_tables_front_end_equals_attention_by_sequence(dtype):
+    """ora_attention_tables, the checker of the GPU parity tests, is the
+    by-sequence attention (model.rs:431-475 over the kv.rs tables) with the
+    block tables handed in: the same bits on a permuted pool with forks that
+    share blocks, queries at earlier positions than a sequence's end, rows
+    padded with -1 past each length and a stride wider than any table. A -1
+    or out-of-pool entry inside a length, or a stride too short for a length,
+    is refused (kv.rs:147 panics there)."""
+    rng = np.random.default_rng(21 + len(dtype))
+    kvd, hd, n_heads = 256, 64, 12  # four kv heads, group 3
+    n_blocks = 96
+    kv = OracleKv(1, kvd, n_blocks * BLOCK, dtype=dtype)
+    kv.init_free_order(rng.permutation(n_blocks))
+    lens = {0: 200, 1: 17, 2: 1, 3: 64, 4: 0}
+    for s, n in lens.items():
+        if n:
+            k = rng.standard_normal((n, kvd), dtype=np.float32) * 3
+            v = rng.standard_normal((n, kvd), dtype=np.float32)
+            kv.write_batch(0, kv.append_batch(np.full(n, s, np.uint32), np.arange(n, dtype=np.uint64)), k, v)
+    kv.share(0, 5, 150)  # a fork; its next token copies the shared partial block
+    sm = kv.append_batch(np.full(11, 5, np.uint32), np.arange(150, 161, dtype=np.uint64))
+    kv.write_batch(0, sm, rng.standard_normal((11, kvd), dtype=np.float32),
+                   rng.standard_normal((11, kvd), dtype=np.float32))
+    assert kv.cow_copies() == 1
+    seqs = np.array([0, 1, 2, 3, 5, 0, 5, 3], dtype=np.uint32)
+    pos = np.array([199, 16, 0, 63, 160, 100, 15, 31], dtype=np.uint64)
+    q = rng.standard_normal((seqs.size, n_heads * hd), dtype=np.float32)
+    want = kv.attention(0, seqs, pos, q, n_heads, hd, threads=2)
+
+    stride = 20  # wider than any table (13 blocks)
+    tables = np.full((seqs.size, stride), -1, dtype=np.int32)
+    for i, (s, p) in enumerate(zip(seqs, pos)):
+        nb = -(-(int(p) + 1) // BLOCK)
+        tables[i, :nb] = kv.block_table(int(s))[:nb]
+    lens_a = (pos + 1).astype(np.int32)
+    got = kv.attention_tables(0, tables, lens_a, q, n_heads, hd, threads=3)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the same with the real table entries past each length left in place
+    full = np.full((seqs.size, stride), -1, dtype=np.int32)
+    for i, s in enumerate(seqs):
+        t = kv.block_table(int(s))
+        full[i, :t.size] = t
+    got = kv.attention_tables(0, full, lens_a, q, n_heads, hd)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+    for bad in (-1, n_blocks):
+        t = tables.copy()
+        t[0, 12] = bad  # the last block of seq 0 at position 199
+        with pytest.raises(OracleError):
+            kv.attention_tables(0, t, lens_a, q, n_heads, hd)
+    with pytest.raises(OracleError):
+        kv.attention_tables(0, tables[:, :12].copy(), lens_a, q, n_heads, hd)
+
+
 # ---------------------------------------------------------------------------- pool
 def test_pool_runs_every_task_exactly_once():
     """pool.rs:217-227."""
