@@ -382,7 +382,9 @@ def bench_copy_bulk(args):
 def bench_append_sweep(args):
     """Bulk slot-mapped append at the Llama-3-8B layer shape (kv_dim 1024, f16):
     512 sequences x 512 tokens claimed through the allocator over a permuted
-    pool; the first n slots of that mapping are written for each size."""
+    pool; the first n slots of that mapping are written for each size, in
+    batch order (ltkv_write) and in ascending cell order (ltkv_cell_order +
+    ltkv_write_ordered)."""
     import torch
 
     from langtrain_studio_amd import KvCache
@@ -404,8 +406,15 @@ def bench_append_sweep(args):
     for n in (64, 256, 1024, 4096, 16384, 65536, 262144):
         us = _time_op(lambda: kv.write_batch(0, d_sm[:n], k[:n], v[:n]), reps=20)
         nbytes = n * kvd * (4 + 4 + 2 + 2) + n * 4
+        # the same rows in ascending cell order (ltkv_cell_order on the host,
+        # once per claim; the order array is 4 more bytes per token)
+        d_order = torch.from_numpy(kv.cell_order(sm[:n])).cuda()
+        us_o = _time_op(lambda: kv.write_batch_ordered(0, d_sm[:n], k[:n], v[:n], d_order), reps=20)
+        obytes = nbytes + n * 4
         rows.append({"tokens": n, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-                     "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)})
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                     "ordered_us": round(us_o, 2), "ordered_GBps": round(obytes / (us_o * 1e-6) / 1e9, 1),
+                     "ordered_frac": round(obytes / (us_o * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)})
     print(json.dumps({"workload": "append-sweep", "shape": "kv_dim 1024 f32->f16", "rows": rows}), flush=True)
 
 

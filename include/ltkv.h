@@ -152,6 +152,28 @@ LTKV_API int ltkv_init_free_order(ltkv_cache *c, const uint32_t *order, size_t n
 LTKV_API int ltkv_write(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
                const float *d_k, const float *d_v, size_t src_stride);
 
+/* Host only: the rows of a claimed batch (slot_mapping[0..n), host memory, as
+ * ltkv_append_batch returned it) grouped by block in ascending block order,
+ * rows of one block in batch order (a block's rows in a claim are one
+ * sequence's increasing positions, kv.rs:85-121, so in increasing slot
+ * order): order[0..*m) receives the row indices; skipped cells (negative or
+ * past the pool) are left out. A counting sort over the cache's blocks, or a
+ * sort of the rows when they are few against the pool. No counterpart in the
+ * reference (its write loop, model.rs:414-429, takes tokens in batch order):
+ * bulk appends written in this order (ltkv_write_ordered) store into the
+ * pool in ascending address order, which HBM takes faster than the scattered
+ * order of a fragmented pool. */
+LTKV_API int ltkv_cell_order(const ltkv_cache *c, size_t n, const int32_t *slot_mapping, int32_t *order,
+                    size_t *m);
+
+/* ltkv_write over the m rows d_order[0..m) (device memory) of a batch of n
+ * rows: row d_order[j] of d_k / d_v goes to cell d_slot_mapping[d_order[j]];
+ * entries outside [0, n) are skipped. The same cells and bits as ltkv_write
+ * of the batch when d_order lists each row once (as ltkv_cell_order gives). */
+LTKV_API int ltkv_write_ordered(ltkv_cache *c, size_t layer, size_t n, const int32_t *d_slot_mapping,
+                       const float *d_k, const float *d_v, size_t src_stride, size_t m,
+                       const int32_t *d_order);
+
 /* RoPE of Model::rope (model.rs:291-308) with the table of model.rs:263-265:
  * inv_freq[i] = base^(-2i / rope_dim), angle = pos * inv_freq[i], cos/sin by
  * the host libm (as the reference), pairs (2i, 2i+1) or, with neox, (i, i +

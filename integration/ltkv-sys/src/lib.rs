@@ -72,6 +72,11 @@ pub mod ffi {
         // device ops (enqueued on the cache's stream)
         pub fn ltkv_write(c: *mut ltkv_cache, layer: usize, n: usize, d_slot_mapping: *const i32,
                           d_k: *const f32, d_v: *const f32, src_stride: usize) -> c_int;
+        pub fn ltkv_cell_order(c: *const ltkv_cache, n: usize, slot_mapping: *const i32, order: *mut i32,
+                               m: *mut usize) -> c_int;
+        pub fn ltkv_write_ordered(c: *mut ltkv_cache, layer: usize, n: usize, d_slot_mapping: *const i32,
+                                  d_k: *const f32, d_v: *const f32, src_stride: usize, m: usize,
+                                  d_order: *const i32) -> c_int;
         pub fn ltkv_rope_init(c: *mut ltkv_cache, base: f32, rope_dim: usize, head_dim: usize, neox: c_int,
                               max_positions: usize) -> c_int;
         pub fn ltkv_write_rope(c: *mut ltkv_cache, layer: usize, n: usize, d_slot_mapping: *const i32,
@@ -406,6 +411,25 @@ impl KvCache {
     pub unsafe fn write_device(&mut self, layer: usize, n: usize, d_slot_mapping: *const i32, d_k: *const f32,
                                d_v: *const f32, src_stride: usize) -> anyhow::Result<()> {
         check(ltkv_write(self.raw, layer, n, d_slot_mapping, d_k, d_v, src_stride))
+    }
+
+    /// The rows of a claimed batch grouped by block in ascending block order
+    /// (host only), for `write_ordered`.
+    pub fn cell_order(&self, slot_mapping: &[i32]) -> anyhow::Result<Vec<i32>> {
+        let mut order = vec![0i32; slot_mapping.len()];
+        let mut m = 0usize;
+        check(unsafe {
+            ltkv_cell_order(self.raw, slot_mapping.len(), slot_mapping.as_ptr(), order.as_mut_ptr(), &mut m)
+        })?;
+        order.truncate(m);
+        Ok(order)
+    }
+
+    /// Kernel 1 over the rows `d_order[0..m)` of a batch of `n` rows.
+    pub unsafe fn write_ordered(&mut self, layer: usize, n: usize, d_slot_mapping: *const i32, d_k: *const f32,
+                                d_v: *const f32, src_stride: usize, m: usize,
+                                d_order: *const i32) -> anyhow::Result<()> {
+        check(ltkv_write_ordered(self.raw, layer, n, d_slot_mapping, d_k, d_v, src_stride, m, d_order))
     }
 
     /// RoPE (model.rs:291-308) fused into kernel 1; Q rotated in place.

@@ -45,6 +45,8 @@ SIGNATURES = {
     "ltkv_block_tables": (_int, [_vp, _sz, _vp, _vp, _sz]),
     "ltkv_init_free_order": (_int, [_vp, _vp, _sz]),
     "ltkv_write": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _sz]),
+    "ltkv_cell_order": (_int, [_vp, _sz, _vp, _vp, _P(_sz)]),
+    "ltkv_write_ordered": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _sz, _sz, _vp]),
     "ltkv_rope_init": (_int, [_vp, _f32, _sz, _sz, _int, _sz]),
     "ltkv_write_rope": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz]),
     "ltkv_copy_blocks": (_int, [_vp, _sz, _vp]),

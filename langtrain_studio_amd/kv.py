@@ -223,6 +223,28 @@ class KvCache:
             _dev_ptr(k, torch.float32, "k", self.device), _dev_ptr(v, torch.float32, "v", self.device),
             k.shape[1]))
 
+    def cell_order(self, slot_mapping) -> np.ndarray:
+        """Host: the rows of a claimed batch grouped by block in ascending
+        block order (ltkv_cell_order), skipped cells left out (int32)."""
+        sm = np.ascontiguousarray(slot_mapping, dtype=np.int32)
+        order = np.empty(sm.size, dtype=np.int32)
+        m = C.c_size_t(0)
+        _check(self._lib.ltkv_cell_order(self._h, sm.size, _np_ptr(sm), _np_ptr(order), C.byref(m)))
+        return order[:m.value]
+
+    def write_batch_ordered(self, layer: int, slot_mapping, k, v, order) -> None:
+        """Kernel 1 over the rows order[m] (int32, device) of a batch:
+        row order[j] of k, v into cell slot_mapping[order[j]]."""
+        import torch
+
+        n = slot_mapping.numel()
+        if k.dim() != 2 or k.shape != v.shape or k.shape[0] != n or k.shape[1] < self.kv_dim:
+            raise ValueError("k and v must be [n][>=kv_dim] and match slot_mapping")
+        _check(self._lib.ltkv_write_ordered(
+            self._h, layer, n, _dev_ptr(slot_mapping, torch.int32, "slot_mapping", self.device),
+            _dev_ptr(k, torch.float32, "k", self.device), _dev_ptr(v, torch.float32, "v", self.device),
+            k.shape[1], order.numel(), _dev_ptr(order, torch.int32, "order", self.device)))
+
     def rope_init(self, base: float, rope_dim: int, head_dim: int, neox: bool, max_positions: int) -> None:
         """RoPE table of Model::rope (model.rs:263-265, 291-308) for write_rope."""
         _check(self._lib.ltkv_rope_init(self._h, float(base), rope_dim, head_dim, 1 if neox else 0,

@@ -170,3 +170,32 @@ def test_init_free_order_validation():
     kv.append(0, 0)
     with pytest.raises(KvError, match="no sequences"):
         kv.init_free_order([0, 1, 2, 3])
+
+
+@pytest.mark.parametrize("n_seqs,per_seq,slack", [(64, 40, 1.1), (3, 5, 200.0)])
+def test_cell_order_groups_rows_by_ascending_block(n_seqs, per_seq, slack):
+    """ltkv_cell_order on a claimed batch over a permuted pool (both the
+    counting sort and, with few rows against the pool, the sorting form):
+    every written row once, skipped cells left out, cells ascending (a
+    block's rows in a claim are one sequence's increasing positions)."""
+    from langtrain_studio_amd import KvCache
+
+    rng = np.random.default_rng(n_seqs)
+    n_blocks = int(n_seqs * -(-per_seq // 16) * slack) + 4
+    kv = KvCache(1, 64, n_blocks * 16, device=None)
+    kv.init_free_order(rng.permutation(n_blocks))
+    # interleave the sequences' tokens, as a mixed step claims them
+    order_tok = rng.permutation(np.repeat(np.arange(n_seqs), per_seq))
+    seqs, pos, nxt = [], [], np.zeros(n_seqs, dtype=np.int64)
+    for s in order_tok:
+        seqs.append(s)
+        pos.append(nxt[s])
+        nxt[s] += 1
+    sm = kv.append_batch(np.array(seqs, np.uint32), np.array(pos, np.uint64)).copy()
+    sm[::7] = -1  # skipped cells
+    order = kv.cell_order(sm)
+    assert order.dtype == np.int32
+    np.testing.assert_array_equal(np.sort(order), np.flatnonzero(sm >= 0))
+    cells = sm[order]
+    assert (np.diff(cells) > 0).all()
+    assert kv.cell_order(np.zeros(0, np.int32)).size == 0

@@ -116,6 +116,40 @@ def test_write_bulk_streaming(gpu, dtype):
         _assert_pools_equal(g, o, (0,))
 
 
+@pytest.mark.parametrize("dtype,kv_dim,n", [("f16", 1024, 40000), ("f32", 1024, 3001), ("q8_0", 256, 5000),
+                                             ("f16", 12, 777)])
+def test_write_ordered_equals_write(gpu, dtype, kv_dim, n):
+    """ltkv_write_ordered over ltkv_cell_order's rows writes the oracle's
+    cells bit for bit (streaming and cached forms, q8_0 quants and scales,
+    rows that move element-wise), skipped and out-of-range cells left alone;
+    order entries outside the batch are skipped."""
+    import torch
+
+    rng = np.random.default_rng(n + kv_dim)
+    n_blocks = n // BLOCK + 64
+    g, o = _caches(1, kv_dim, n_blocks * BLOCK, dtype, rng.permutation(n_blocks))
+    per = 500 if n >= 500 else 37
+    seqs = np.repeat(np.arange(-(-n // per), dtype=np.uint32), per)[:n]
+    pos = np.concatenate([np.arange(per, dtype=np.uint64)] * -(-n // per))[:n]
+    sm = g.append_batch(seqs, pos)
+    np.testing.assert_array_equal(sm, o.append_batch(seqs, pos))
+    sm = sm.copy()
+    sm[rng.choice(n, 50, replace=False)] = -1
+    sm[rng.choice(n, 5, replace=False)] = n_blocks * BLOCK + 3
+    order = g.cell_order(sm)
+    assert order.size == n - int((sm < 0).sum()) - int((sm >= n_blocks * BLOCK).sum())
+    d_order = torch.from_numpy(np.concatenate([order, np.array([-1, n, n + 7], np.int32)])).to(gpu)
+    k = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    g.write_batch_ordered(0, torch.from_numpy(sm).to(gpu), torch.from_numpy(k).to(gpu),
+                          torch.from_numpy(v).to(gpu), d_order)
+    o.write_batch(0, np.where(sm >= n_blocks * BLOCK, -1, sm), k, v)
+    _assert_pools_equal(g, o, (0,))
+    if dtype == "q8_0":
+        for a, b in zip(g.read_scales(0), o.scales(0)):
+            np.testing.assert_array_equal(a, b.transpose(0, 2, 1))
+
+
 # ---------------------------------------------------------------------------- kv.rs tests, on the GPU cache
 def test_share_then_diverge_copies_on_write(gpu):
     """kv.rs:202-217 with the K/V data living in HBM, at the test's own kv_dim 4."""
