@@ -55,7 +55,7 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "copy-bulk", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed", "prefill", "rope-append", "decode-q8", "descriptor"],
+                            "mixed", "prefill", "rope-append", "decode-q8", "descriptor", "descriptor-long"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -988,7 +988,7 @@ def bench_mixed(args):
     print(json.dumps(line), flush=True)
 
 
-def bench_descriptor(args):
+def bench_descriptor(args, n_dec=120, ctx=(512, 8193), n_pre=8):
     """The step descriptor two ways, on the continuous-batching step of the
     Qwen2.5-7B layer (120 decode sequences, contexts U[512, 8192], 2% finish
     per step and arrivals take their slot, plus 8 prefill streams of 512-token
@@ -1005,17 +1005,19 @@ def bench_descriptor(args):
     positions on the device for RoPE would upload) instead of uploading the
     host's. All run the same appends and attention; timed per step on the
     host clock (claim + descriptor + launches + stream synchronisation), and
-    the block tables' host-to-device bytes are counted."""
+    the block tables' host-to-device bytes are counted. descriptor-long runs
+    the decode part alone at 256 sequences x U[8192, 16384] tokens, where a
+    step's full tables are 1 MB."""
     import torch
 
     from langtrain_studio_amd import KvCache
 
-    n_heads, n_kv, hd, n_dec, n_pre, chunk = 28, 4, 128, 120, 8, 512
+    n_heads, n_kv, hd, chunk = 28, 4, 128, 512
     steps = max(args.steps, 1)
     kvd = n_kv * hd
     dev = torch.device("cuda", 0)
-    stride = (8192 + steps + chunk) // BLOCK + 2
-    n_blocks = int((n_dec + n_pre) * 8192 // BLOCK * 1.1) + (n_dec + n_pre) * (steps // BLOCK + 2)
+    stride = (ctx[1] + steps + chunk) // BLOCK + 2
+    n_blocks = int((n_dec + n_pre) * ctx[1] // BLOCK * 1.1) + (n_dec + n_pre) * (steps // BLOCK + 2)
     results = {}
     for mode in ("tables", "resident", "resident-slots"):
         rng = np.random.default_rng(args.seed)
@@ -1031,8 +1033,8 @@ def bench_descriptor(args):
                 kv.append_batch(np.full(ctx, sid, np.uint32), np.arange(ctx, dtype=np.uint64))
             return sid
 
-        dec = [new_seq(int(rng.integers(512, 8193))) for _ in range(n_dec)]
-        pre = [(new_seq(0), int(rng.integers(512, 8193))) for _ in range(n_pre)]
+        dec = [new_seq(int(rng.integers(*ctx))) for _ in range(n_dec)]
+        pre = [(new_seq(0), int(rng.integers(*ctx))) for _ in range(n_pre)]
         kn = torch.randn((n_pre * chunk + n_dec, kvd), device=dev)
         q = torch.randn((n_dec, n_heads * hd), device=dev)
         out = torch.empty_like(q)
@@ -1044,6 +1046,7 @@ def bench_descriptor(args):
         up0 = 0
         wall, table_bytes = [], 0
         d_dec_rows = torch.empty((n_dec,), dtype=torch.int32, device=dev)
+        h_dec_rows = torch.empty((n_dec,), dtype=torch.int32).pin_memory()
         rows_stale = True
         for s in range(steps + 3):
             t0 = time.perf_counter()
@@ -1073,7 +1076,8 @@ def bench_descriptor(args):
             elif mode == "resident":
                 d_sm = torch.from_numpy(sm).to(dev, non_blocking=True)
                 if rows_stale:  # a decode sequence arrived: refresh the rows the step reads
-                    d_dec_rows.copy_(torch.from_numpy(kv.seq_rows(np.array(dec, np.uint32))))
+                    h_dec_rows.numpy()[:] = kv.seq_rows(np.array(dec, np.uint32))
+                    d_dec_rows.copy_(h_dec_rows, non_blocking=True)  # pinned, as the tables' upload
                     rows_stale = False
                 kv.write_batch(0, d_sm, kn[:n_tok], kn[:n_tok])
                 kv.decode_attention_rows(0, q, d_dec_rows, lens, n_heads, hd, out=out)
@@ -1095,11 +1099,11 @@ def bench_descriptor(args):
             for i, (sid, target) in enumerate(pre):
                 if kv.len(sid) >= target:
                     kv.truncate(sid, 0)
-                    pre[i] = (new_seq(0), int(rng.integers(512, 8193)))
+                    pre[i] = (new_seq(0), int(rng.integers(*ctx)))
             for i, sid in enumerate(dec):
                 if rng.random() < 0.02:
                     kv.truncate(sid, 0)
-                    dec[i] = new_seq(int(rng.integers(512, 8193)))
+                    dec[i] = new_seq(int(rng.integers(*ctx)))
                     rows_stale = True
         if mode != "tables":
             kv.sync_tables()
@@ -1109,8 +1113,10 @@ def bench_descriptor(args):
                          "step_wall_us_p50": round(float(np.median(wall)) * 1e6, 1),
                          "table_h2d_bytes_per_step": round(table_bytes / steps)}
         del kv
+    what = (f"{n_pre}x512 prefill append + {n_dec} decode ctx U[{ctx[0]},{ctx[1] - 1}]" if n_pre
+            else f"{n_dec} decode ctx U[{ctx[0]},{ctx[1] - 1}]")
     print(json.dumps({
-        "workload": f"descriptor qwen2.5-7b f16: 8x512 prefill append + 120 decode, 2% churn, {steps} steps",
+        "workload": f"descriptor qwen2.5-7b f16: {what}, 2% churn, {steps} steps",
         "tables": results["tables"], "resident": results["resident"],
         "resident_slots": results["resident-slots"],
         "h2d_ratio": round(results["tables"]["table_h2d_bytes_per_step"]
@@ -1234,7 +1240,8 @@ def main():
     extra = {"copy": bench_copy, "copy-bulk": bench_copy_bulk, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
              "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
              "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8,
-             "descriptor": bench_descriptor}
+             "descriptor": bench_descriptor,
+             "descriptor-long": lambda a: bench_descriptor(a, n_dec=256, ctx=(8192, 16385), n_pre=0)}
     if args.workload in extra:
         extra[args.workload](args)
         return

@@ -170,6 +170,7 @@ struct ltkv_cache {
   std::vector<int32_t> rt_free;                  // released rows, reused last-in first-out
   std::vector<uint32_t> rt_lo, rt_hi;            // per row: changed entries [lo, hi)
   std::vector<char> rt_dirty;                    // per row: changed since the last sync
+  std::vector<uint32_t> rt_nb;                   // per row: table length in blocks as last synced
   std::vector<int32_t> rt_dirty_rows;
   std::vector<int32_t> rt_upd;                   // (row, col, value) triples being built
   int32_t *h_rt_upd = nullptr, *d_rt_upd = nullptr;  // pinned staging -> device
@@ -213,6 +214,7 @@ struct ltkv_cache {
       rt_lo.push_back(0);
       rt_hi.push_back(0);
       rt_dirty.push_back(0);
+      rt_nb.push_back(0);
     }
     rt_row.emplace(seq, r);
     rt_seq[r] = seq;
@@ -439,6 +441,7 @@ int sync_tables(ltkv_cache *c) {
   u.clear();
   auto row_updates = [&](int32_t r, size_t lo, size_t hi) {
     const std::vector<int32_t> *b = row_blocks(r);
+    if ((size_t)r < c->rt_nb.size()) c->rt_nb[r] = b ? (uint32_t)b->size() : 0;
     if (!b) {  // released: an empty table
       u.insert(u.end(), {r, -1, 0});
       return;
@@ -474,6 +477,18 @@ int sync_tables(ltkv_cache *c) {
   c->rt_dirty_rows.clear();
 
   const size_t n = u.size() / 3;
+  if (n <= (size_t)ltkv::kTableUpdateArgs) {
+    // A step's few changes (new blocks, copy-on-write replacements, lengths)
+    // travel in the update kernel's arguments: no staging copy, no event.
+    ltkv::TableUpdates args;
+    args.n = (int32_t)n;
+    std::memcpy(args.t, u.data(), n * 3 * sizeof(int32_t));
+    HIP_TRY(ltkv::launch_table_update_args(c->d_rt, c->d_rt_nb, (int64_t)c->rt_width, (int64_t)c->rt_rows, args,
+                                           c->stream),
+            "table update launch");
+    c->rt_uploaded += n;
+    return LTKV_OK;
+  }
   if (c->rt_in_flight) {  // the staging buffer may still be read by the last upload
     HIP_TRY(hipEventSynchronize(c->rt_done), "hipEventSynchronize");
     c->rt_in_flight = false;
@@ -506,12 +521,10 @@ int sync_tables(ltkv_cache *c) {
 }
 
 // Longest table (blocks) of a live sequence.
+// Longest resident table (blocks), as of the last sync_tables.
 size_t max_table_blocks(const ltkv_cache *c) {
-  size_t m = 0;
-  for (const auto &kv : c->rt_row) {
-    const auto it = c->seqs.find(kv.first);
-    if (it != c->seqs.end()) m = std::max(m, it->second.blocks.size());
-  }
+  uint32_t m = 0;
+  for (uint32_t nb : c->rt_nb) m = std::max(m, nb);
   return m;
 }
 

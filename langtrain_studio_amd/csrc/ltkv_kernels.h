@@ -80,6 +80,14 @@ hipError_t launch_gather(const PoolGeom &g, const void *k_layer, const void *v_l
 hipError_t launch_status_take(int32_t *status, hipStream_t s);
 // Resident block tables: updates (row, col, value) triples (col -1: the
 // row's length in blocks), and the slot mapping of (row, position) tokens.
+// Up to kTableUpdateArgs triples passed by value (kernel arguments hold 4 KB).
+constexpr int kTableUpdateArgs = 320;
+struct TableUpdates {
+  int32_t n;
+  int32_t t[3 * kTableUpdateArgs];
+};
+hipError_t launch_table_update_args(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,
+                                    const TableUpdates &u, hipStream_t s);
 hipError_t launch_table_update(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,
                                const int32_t *upd, int64_t n, hipStream_t s);
 hipError_t launch_slot_mapping(const int32_t *tables, const int32_t *counts, int64_t width,

@@ -672,7 +672,7 @@ __device__ __forceinline__ const int32_t *table_of(const int32_t *tables, int64_
                                                    const int32_t *rows, int64_t n_rows, int64_t qi) {
   int64_t r = qi;
   if (rows) {
-    r = rows[qi];
+    r = ((const __attribute__((address_space(4))) int32_t *)rows)[qi];  // uniform: the scalar cache
     if (r < 0 || r >= n_rows) r = 0;
   }
   return tables + r * stride;
@@ -1973,13 +1973,17 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     it.tok1 = len < tok0 + pt ? len : tok0 + pt;
     it.b0 = (int)(tok0 >> 4);
     it.b1 = (int)((it.tok1 + 15) >> 4);
-    it.tab = table_of(tables, table_stride, rows, n_rows, qi);
-    // A resident row outside the tables is a fault when the query has tokens
-    // (table entries are checked as their tiles load).
-    if (rows && it.b1 > it.b0) {
-      const int32_t r = rows[qi];
-      if (r < 0 || r >= n_rows) report_fault(status, kFaultTable, qi);
+    // A resident row outside the tables reads row 0 and is a fault when the
+    // query has tokens (table entries are checked as their tiles load).
+    int64_t trow = qi;
+    if (rows) {
+      trow = scalar_read(rows, qi);
+      if (trow < 0 || trow >= n_rows) {
+        if (it.b1 > it.b0) report_fault(status, kFaultTable, qi);
+        trow = 0;
+      }
     }
+    it.tab = tables + trow * table_stride;
     fetch_q(qi, qr);
 
     // Fused append (f16, decode steps): the wave of the query's last partition
@@ -2315,7 +2319,15 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   int b = cur.b0;
   // Table entries are read one tile ahead of their loads (the first ones
   // together), so no load waits on its own scalar read.
-  auto entry_of = [&](int bb) __attribute__((always_inline)) { return bb < cur.b1 ? scalar_read(cur.tab, bb) : 0; };
+  // The item's first 64 table entries come in with one vector load (lane i:
+  // entry b0 + i), so a table that is not in the caches (resident tables,
+  // last written steps ago) costs one round trip instead of one per 16
+  // entries; later entries of longer items are read through the scalar cache.
+  const int32_t tabv = lane < cur.b1 - cur.b0 ? cur.tab[cur.b0 + lane] : 0;
+  auto entry_of = [&](int bb) __attribute__((always_inline)) {
+    return bb < cur.b1 ? (bb - cur.b0 < 64 ? __builtin_amdgcn_readlane(tabv, bb - cur.b0) : scalar_read(cur.tab, bb))
+                       : 0;
+  };
   auto load_b = [&](int bb, int32_t entry, Stage &st) __attribute__((always_inline)) {
     load_tile(entry, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
   };
@@ -3266,6 +3278,22 @@ table_update_kernel(int32_t *__restrict__ tables, int32_t *__restrict__ counts, 
     tables[(int64_t)r * width + c] = v;
 }
 
+// The same for a step's few updates passed by value in the kernel arguments
+// (no staging copy, no event).
+__global__ void __launch_bounds__(256)
+table_update_args_kernel(int32_t *__restrict__ tables, int32_t *__restrict__ counts, int64_t width,
+                         int64_t n_rows, TableUpdates u) {
+  const int i = (int)threadIdx.x;
+  for (int k = i; k < u.n; k += 256) {
+    const int32_t r = u.t[3 * k], c = u.t[3 * k + 1], v = u.t[3 * k + 2];
+    if (r < 0 || r >= n_rows) continue;
+    if (c == -1)
+      counts[r] = v;
+    else if (c >= 0 && c < width)
+      tables[(int64_t)r * width + c] = v;
+  }
+}
+
 // Takes the fault word: atomic exchanges with zero, so a fault raised by work
 // running beside this kernel is either taken here or left for the next take.
 __global__ void __launch_bounds__(64) status_take_kernel(int32_t *status) {
@@ -3464,6 +3492,14 @@ hipError_t launch_table_update(int32_t *tables, int32_t *counts, int64_t width, 
   if (n <= 0) return hipSuccess;
   if ((n + 255) / 256 >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   table_update_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tables, counts, width, n_rows, upd, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_table_update_args(int32_t *tables, int32_t *counts, int64_t width, int64_t n_rows,
+                                    const TableUpdates &u, hipStream_t s) {
+  if (u.n <= 0) return hipSuccess;
+  if (u.n > kTableUpdateArgs) return hipErrorInvalidValue;
+  table_update_args_kernel<<<1, 256, 0, s>>>(tables, counts, width, n_rows, u);
   return hipGetLastError();
 }
 
