@@ -653,14 +653,26 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
       ltkv::attention_tuned((int)c->elem, (int)head_dim, (int)group)) {
     std::vector<char> taken(n, 0);
     {
-      std::unordered_map<uint32_t, size_t> seq_of;
+      // Queries of one sequence (in query order), sequences in the order of
+      // their first query: a sort of (sequence, query) pairs, no per-sequence
+      // containers.
+      std::vector<std::pair<uint32_t, int32_t>> bys;
+      bys.reserve(n);
+      for (size_t i = 0; i < n; ++i)
+        if (lens[i] > 0) bys.emplace_back(seqs[i], (int32_t)i);
+      std::sort(bys.begin(), bys.end());
       std::vector<std::vector<int32_t>> by_seq;
-      for (size_t i = 0; i < n; ++i) {
-        if (lens[i] == 0) continue;
-        auto ins = seq_of.emplace(seqs[i], by_seq.size());
-        if (ins.second) by_seq.emplace_back();
-        by_seq[ins.first->second].push_back((int32_t)i);
+      for (size_t a = 0; a < bys.size();) {
+        size_t e = a + 1;
+        while (e < bys.size() && bys[e].first == bys[a].first) ++e;
+        if (e - a >= 2) {
+          by_seq.emplace_back();
+          for (size_t k = a; k < e; ++k) by_seq.back().push_back(bys[k].second);
+        }
+        a = e;
       }
+      std::sort(by_seq.begin(), by_seq.end(),
+                [](const std::vector<int32_t> &x, const std::vector<int32_t> &y) { return x[0] < y[0]; });
       for (auto &b : by_seq) {
         if (b.size() < 2) continue;
         Group gr;
@@ -694,8 +706,10 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
       lcp.reserve(b.size());
       for (int32_t m : b) {
         const size_t cap = std::min<size_t>(lens[m] / LTKV_BLOCK, ref_full);
+        const int32_t *x = sq[m]->blocks.data(), *y = ref.data();
         size_t k = 0;
-        while (k < cap && sq[m]->blocks[k] == ref[k]) ++k;
+        while (k + 16 <= cap && std::memcmp(x + k, y + k, 16 * sizeof(int32_t)) == 0) k += 16;
+        while (k < cap && x[k] == y[k]) ++k;
         lcp.emplace_back(k, m);
       }
       std::stable_sort(lcp.begin(), lcp.end(),
