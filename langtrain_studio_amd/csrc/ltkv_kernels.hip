@@ -2319,15 +2319,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   int b = cur.b0;
   // Table entries are read one tile ahead of their loads (the first ones
   // together), so no load waits on its own scalar read.
-  // The item's first 64 table entries come in with one vector load (lane i:
-  // entry b0 + i), so a table that is not in the caches (resident tables,
-  // last written steps ago) costs one round trip instead of one per 16
-  // entries; later entries of longer items are read through the scalar cache.
-  const int32_t tabv = lane < cur.b1 - cur.b0 ? cur.tab[cur.b0 + lane] : 0;
-  auto entry_of = [&](int bb) __attribute__((always_inline)) {
-    return bb < cur.b1 ? (bb - cur.b0 < 64 ? __builtin_amdgcn_readlane(tabv, bb - cur.b0) : scalar_read(cur.tab, bb))
-                       : 0;
-  };
+  auto entry_of = [&](int bb) __attribute__((always_inline)) { return bb < cur.b1 ? scalar_read(cur.tab, bb) : 0; };
   auto load_b = [&](int bb, int32_t entry, Stage &st) __attribute__((always_inline)) {
     load_tile(entry, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
   };
