@@ -55,7 +55,8 @@ def _args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "copy", "copy-bulk", "append-sweep", "long-context", "tinyllama", "prefix-cow",
-                            "mixed", "prefill", "rope-append", "decode-q8", "descriptor", "descriptor-long"],
+                            "mixed", "prefill", "rope-append", "decode-q8", "descriptor", "descriptor-long",
+                            "decode-timeline", "decode-shapes"],
                    help="decode = the headline line; the others print measurement lines of their own")
     return p.parse_args()
 
@@ -206,7 +207,7 @@ class Llama3Decode:
 
     n_heads, n_kv, head_dim, batch = 32, 8, 128, 64
 
-    def __init__(self, steps: int, seed: int, partition: int, dtype: str = "f16"):
+    def __init__(self, steps: int, seed: int, partition: int, dtype: str = "f16", ctx=None):
         import torch
 
         from langtrain_studio_amd import KvCache
@@ -220,6 +221,8 @@ class Llama3Decode:
         self.kvd = kvd
         self.steps = steps
         self.ctx = rng.integers(2048, 4097, B)
+        if ctx is not None:  # the same seeded pool order and data, other lengths
+            self.ctx = np.asarray(ctx, dtype=np.int64)
         need = sum(math.ceil((int(c) + steps) / BLOCK) for c in self.ctx)
         self.n_blocks = int(math.ceil(need * 1.1))
         stream = torch.cuda.current_stream(dev)
@@ -690,7 +693,7 @@ def _unique_tokens(tables: np.ndarray, lens: np.ndarray) -> int:
     return int(best.sum())
 
 
-def bench_prefix_cow(args):
+def bench_prefix_cow(args, timeline=None):
     """Prefix sharing at the Llama-3-8B layer shape: 256 sequences hold a
     4088-token prefix (256 blocks, the last holding 8 tokens, refcount 256);
     step 0 appends a 64-token private suffix to every sequence, which copies
@@ -749,6 +752,17 @@ def bench_prefix_cow(args):
     def write_step(s):
         for layer in range(L):
             kv.write_batch(layer, d_sm[s], kd[s], kd[s])
+
+    if timeline is not None:
+        # Profiling build: the stamps of step 0's planned per-query pass (the
+        # decode kernel's launch after the grouped kernel), layer 0.
+        kv.plan_attention(seqs, lens[0], n_heads, hd, shared_prefix=True)
+        write_step(0)
+        for _ in range(5):
+            kv.planned_attention(0, q[0], out=out)
+        timeline("prefix-cow planned step, per-query pass (256 forks of a 4088-token prefix, "
+                 "llama3-8b layer, f16)")
+        return
 
     # Per-query decode attention (every sequence reads its whole table). One
     # untimed call on the last layer first keeps the queue busy, so the timed
@@ -1199,6 +1213,131 @@ def _time_decode_graph(w: Llama3Decode, steps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
+def _use_timeline_library():
+    """Points the binding at the profiling build (libltkv_timeline.so: the
+    same kernels with per-wave phase stamps) before anything loads the
+    product library; returns the stamp reader."""
+    import ctypes
+
+    from langtrain_studio_amd import _lib
+    from langtrain_studio_amd.build import TIMELINE_LIB
+
+    if _lib._lib is not None:
+        raise RuntimeError("the product library is already loaded")
+    if not os.path.exists(TIMELINE_LIB):
+        print(json.dumps({"error": f"{TIMELINE_LIB} is missing: python -m langtrain_studio_amd.build"}))
+        sys.exit(1)
+    _lib.LIB_PATH = TIMELINE_LIB
+    lib = _lib.load()
+    lib.ltkv_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.ltkv_timeline_read.restype = ctypes.c_int
+
+    def read() -> np.ndarray:
+        buf = np.zeros(65536 * 8, dtype=np.uint64)
+        if lib.ltkv_timeline_read(buf.ctypes.data, buf.size) != 0:
+            raise RuntimeError("ltkv_timeline_read failed")
+        return buf.reshape(-1, 8)
+
+    return read
+
+
+def _timeline_stats(t: np.ndarray) -> dict:
+    """Per-wave phase times of one decode-kernel launch, in µs from the first
+    wave's entry (s_memrealtime runs at 100 MHz)."""
+    t = t[t[:, 0] > 0].astype(np.int64)
+    t0 = int(t[:, 0].min())
+    names = ["entry", "item_found", "first_loads_issued", "first_tile_computed", "tile_loop_done",
+             "result_written"]
+    phases = {}
+    for i, name in enumerate(names):
+        v = (t[:, i][t[:, i] > 0] - t0) / 100.0
+        phases[name] = {q: round(float(np.percentile(v, p)), 2) for q, p in
+                        (("p10", 10), ("p50", 50), ("p90", 90), ("max", 100))}
+    streaming = (t[:, 2] > 0) & (t[:, 6] > 0)
+    s0, s1 = (t[streaming, 3] - t0) / 100.0, (t[streaming, 4] - t0) / 100.0
+    span = float((t[:, 5].max() - t0) / 100.0)
+    live = {f"{x:.0f}": int(((s0 <= x) & (s1 > x)).sum()) for x in np.arange(0.0, span + 10.0, 10.0)}
+    tiles = t[streaming, 6]
+    rate = tiles / np.maximum((t[streaming, 4] - t[streaming, 2]) / 100.0, 1e-3)
+    return {"waves": int(len(t)), "span_us": round(span, 2), "phases_us": phases,
+            "streaming_waves_at_us": live, "tiles_per_wave": {"min": int(tiles.min()),
+                                                                "mean": round(float(tiles.mean()), 1),
+                                                                "max": int(tiles.max())},
+            "tiles_per_us_per_wave": round(float(rate.mean()), 3)}
+
+
+def bench_decode_timeline(args):
+    """Per-wave timeline of the headline decode launch (unfused attention,
+    64 queries x U[2048, 4096]) from the profiling build: when each wave found
+    its item, issued its first loads, computed its first tile and finished,
+    and how many waves stream at each 10 µs. One line per launch of the last
+    `--steps` steps (at most 5), then the prefix-cow planned step's per-query
+    pass."""
+    import torch
+
+    read = _use_timeline_library()
+    steps = max(1, min(args.steps, 5))
+    w = Llama3Decode(steps, args.seed, args.partition)
+    for s in range(steps):
+        w.append(s)
+        w.attend(s)
+    torch.cuda.synchronize()
+    read()
+    # Each reading takes the last of five back-to-back launches (the stamps
+    # of a launch overwrite the previous one's), so the GPU is in its running
+    # state rather than just out of the synchronisation of the reading.
+    for s in range(steps):
+        for _ in range(5):
+            w.attend(s)
+        print(json.dumps({"workload": "decode-timeline llama3-8b-layer decode, 64 seqs ctx U[2048,4096], f16, "
+                                      "unfused attention launch", "step": s, **_timeline_stats(read())}),
+              flush=True)
+    del w
+    torch.cuda.synchronize()
+
+    def emit(what):
+        print(json.dumps({"workload": "decode-timeline " + what, **_timeline_stats(read())}), flush=True)
+
+    bench_prefix_cow(args, timeline=emit)
+
+
+def bench_decode_shapes(args):
+    """How much the headline launch's uneven items cost: the same 64-query
+    decode attention (unfused, HIP events over `--steps` launches) with every
+    context equal (2048 / 3072 / 4096 tokens; 3072 is the mean of the
+    headline's U[2048, 4096]) and, on the headline's contexts, with fixed
+    partitions of 256-1024 tokens (ltkv_set_attention_partition) against the
+    per-query default."""
+    import torch
+
+    reps = max(10, args.steps)
+    out = {"workload": "decode-shapes llama3-8b-layer decode attention, 64 seqs, f16"}
+
+    def timed(w):
+        for _ in range(5):
+            w.attend(0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            w.attend(0)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        return {"us": round(us, 2), "frac": round(w.attention_bytes(0) / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+    w = Llama3Decode(1, args.seed, 0)
+    out["random_U2048_4096"] = {"default": timed(w)}
+    for p in (256, 512, 768, 1024):
+        w.kv.set_attention_partition(p)
+        out["random_U2048_4096"][f"partition_{p}"] = timed(w)
+    del w
+    for n in (2048, 3072, 4096):
+        w = Llama3Decode(1, args.seed, 0, ctx=np.full(64, n))
+        out[f"equal_{n}"] = timed(w)
+        del w
+    print(json.dumps(out), flush=True)
+
+
 def bench_decode_q8(args):
     """The Llama-3-8B decode step on a q8_0 KV cache (int8 quants plus one f16
     scale per 32 elements: 1.06 bytes per element instead of 2)."""
@@ -1240,7 +1379,8 @@ def main():
     extra = {"copy": bench_copy, "copy-bulk": bench_copy_bulk, "append-sweep": bench_append_sweep, "long-context": bench_long_context,
              "tinyllama": bench_tinyllama, "prefix-cow": bench_prefix_cow, "mixed": bench_mixed,
              "prefill": bench_prefill, "rope-append": bench_rope_append, "decode-q8": bench_decode_q8,
-             "descriptor": bench_descriptor,
+             "descriptor": bench_descriptor, "decode-timeline": bench_decode_timeline,
+             "decode-shapes": bench_decode_shapes,
              "descriptor-long": lambda a: bench_descriptor(a, n_dec=256, ctx=(8192, 16385), n_pre=0)}
     if args.workload in extra:
         extra[args.workload](args)

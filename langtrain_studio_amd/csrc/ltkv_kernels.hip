@@ -38,6 +38,23 @@
 // hipGetSymbolAddress returns on each device (scratch_address below).
 static __device__ __align__(256) uint8_t scratch[ltkv::kScratchBytes];
 
+// Profiling build only (compiled with -DLTKV_TIMELINE into
+// libltkv_timeline.so; the product library has none of it): each wave of the
+// matrix-core decode kernel records s_memrealtime stamps (100 MHz) of its
+// phases in g_timeline[work-group][8], read and cleared by
+// ltkv_timeline_read: 0 entry, 1 item found, 2 first tiles' loads issued,
+// 3 first tile computed, 4 tile loop done, 5 result written, 6 tiles of the
+// item, 7 query << 16 | partition << 8 | first kv head.
+#ifdef LTKV_TIMELINE
+constexpr int kTimelineWaves = 65536;
+static __device__ unsigned long long g_timeline[kTimelineWaves * 8];
+#define LTKV_STAMP(i) (tl_[i] = __builtin_amdgcn_s_memrealtime())
+#define LTKV_STAMP_ONCE(i) (tl_[i] = tl_[i] ? tl_[i] : __builtin_amdgcn_s_memrealtime())
+#else
+#define LTKV_STAMP(i) ((void)0)
+#define LTKV_STAMP_ONCE(i) ((void)0)
+#endif
+
 namespace ltkv {
 namespace {
 
@@ -1780,6 +1797,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int max_pre_parts, const int32_t *__restrict__ new_slots,
                  const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
                  T *kdst, T *vdst, int64_t n_queries, int order, int32_t *__restrict__ status) {
+#ifdef LTKV_TIMELINE
+  unsigned long long tl_[8] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0, 0, 0};
+#endif
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -2315,6 +2335,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   f32x4 qr[2 * KS], kr[2], vr[2];
   make_item(cur, qr, kr, vr);
   if (!cur.valid) return;
+  LTKV_STAMP(1);
   reset();
   int b = cur.b0;
   // Table entries are read one tile ahead of their loads (the first ones
@@ -2330,12 +2351,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       int32_t en = entry_of(b + 2);
       load_b(b, e0, s0);
       load_b(b + 1, e1, s1);
+      LTKV_STAMP(2);
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
         int32_t ea = entry_of(b + 3);
         load_b(b + 2, en, s2);
         compute_tile(b, s0);
+        LTKV_STAMP_ONCE(3);
         if (++b >= cur.b1) break;
         en = entry_of(b + 3);
         load_b(b + 2, ea, s0);
@@ -2352,12 +2375,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       const int32_t e0 = entry_of(b);
       int32_t en = entry_of(b + 1);
       load_b(b, e0, s0);
+      LTKV_STAMP(2);
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
         int32_t ea = entry_of(b + 2);
         load_b(b + 1, en, s1);
         compute_tile(b, s0);
+        LTKV_STAMP_ONCE(3);
         if (++b >= cur.b1) break;
         en = entry_of(b + 2);
         load_b(b + 1, ea, s0);
@@ -2366,7 +2391,15 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       }
     }
   }
+  LTKV_STAMP(4);
   finish(cur);
+#ifdef LTKV_TIMELINE
+  LTKV_STAMP(5);
+  tl_[6] = (unsigned long long)(cur.b1 - cur.b0);
+  tl_[7] = (unsigned long long)cur.qi << 16 | (unsigned long long)cur.part << 8 | (unsigned long long)kvh0;
+  if (lane == 0 && blockIdx.x < kTimelineWaves)
+    for (int i = 0; i < 8; ++i) g_timeline[blockIdx.x * 8 + i] = tl_[i];
+#endif
   if (fault_q >= 0) report_fault(status, kFaultTable, fault_q);
 }
 
@@ -3640,3 +3673,18 @@ hipError_t scratch_address(int device, void **ptr) {
 }
 
 }  // namespace ltkv
+
+#ifdef LTKV_TIMELINE
+// Copies the stamps of the last decode launch (n entries of the [work-group][8]
+// array) to host memory and clears them; profiling build only.
+extern "C" __attribute__((visibility("default"))) int ltkv_timeline_read(unsigned long long *h, size_t n) {
+  if (n > (size_t)kTimelineWaves * 8) n = (size_t)kTimelineWaves * 8;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  if (hipMemcpyFromSymbol(h, HIP_SYMBOL(g_timeline), n * 8, 0, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  static unsigned long long zeros[4096];
+  for (size_t i = 0; i < (size_t)kTimelineWaves * 8; i += 4096)
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), zeros, sizeof zeros, i * 8, hipMemcpyHostToDevice) != hipSuccess)
+      return -1;
+  return 0;
+}
+#endif
