@@ -112,7 +112,10 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 // With `order` (ltkv_write_ordered), launch row i is source row order[i] (rows
 // outside [0, n_rows) are skipped): a batch's rows taken in ascending cell
 // order store into the pool in ascending address order.
-template <int ELEM, bool STREAM>
+// PARTS: 3 writes K and V; 1 only K, 2 only V (the streaming form runs as a
+// K launch then a V launch: one read and one write stream per wave instead
+// of two each, 1-3% more bandwidth on bulk appends, the same bits).
+template <int ELEM, bool STREAM, int PARTS = 3>
 __global__ void __launch_bounds__(256)
 write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
              const int32_t *__restrict__ slots, const float *__restrict__ k,
@@ -140,16 +143,25 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
     s[j] = live ? slots[row] : -1;
     const f32x4 *ks = reinterpret_cast<const f32x4 *>(k + row * src_stride + col);
     const f32x4 *vs = reinterpret_cast<const f32x4 *>(v + row * src_stride + col);
+    a[j][0] = a[j][1] = a[j][2] = a[j][3] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (STREAM) {
-      a[j][0] = __builtin_nontemporal_load(ks);
-      a[j][1] = __builtin_nontemporal_load(ks + 1);
-      a[j][2] = __builtin_nontemporal_load(vs);
-      a[j][3] = __builtin_nontemporal_load(vs + 1);
+      if constexpr ((PARTS & 1) != 0) {
+        a[j][0] = __builtin_nontemporal_load(ks);
+        a[j][1] = __builtin_nontemporal_load(ks + 1);
+      }
+      if constexpr ((PARTS & 2) != 0) {
+        a[j][2] = __builtin_nontemporal_load(vs);
+        a[j][3] = __builtin_nontemporal_load(vs + 1);
+      }
     } else {
-      a[j][0] = ks[0];
-      a[j][1] = ks[1];
-      a[j][2] = vs[0];
-      a[j][3] = vs[1];
+      if constexpr ((PARTS & 1) != 0) {
+        a[j][0] = ks[0];
+        a[j][1] = ks[1];
+      }
+      if constexpr ((PARTS & 2) != 0) {
+        a[j][2] = vs[0];
+        a[j][3] = vs[1];
+      }
     }
   }
 #pragma unroll
@@ -170,15 +182,19 @@ write_kernel(uint8_t *__restrict__ kpool, uint8_t *__restrict__ vpool,
       // caches, and the attention after the append keeps its cache lines
       // (continuous-batching step of 4216 tokens: append 4%, attention 2%
       // faster; bulk appends unchanged)
-      __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kpool + dst * 2));
-      __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vpool + dst * 2));
+      if constexpr ((PARTS & 1) != 0) __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kpool + dst * 2));
+      if constexpr ((PARTS & 2) != 0) __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vpool + dst * 2));
     } else {
       f32x4 *kd = reinterpret_cast<f32x4 *>(kpool + dst * 4);
       f32x4 *vd = reinterpret_cast<f32x4 *>(vpool + dst * 4);
-      kd[0] = a[j][0];
-      kd[1] = a[j][1];
-      vd[0] = a[j][2];
-      vd[1] = a[j][3];
+      if constexpr ((PARTS & 1) != 0) {
+        kd[0] = a[j][0];
+        kd[1] = a[j][1];
+      }
+      if constexpr ((PARTS & 2) != 0) {
+        vd[0] = a[j][2];
+        vd[1] = a[j][3];
+      }
     }
   }
 }
@@ -3371,9 +3387,17 @@ hipError_t launch_write_form(const PoolGeom &g, void *k_layer, void *v_layer, co
   constexpr int rows = STREAM ? 2 : 1;
   const int64_t threads = (n + rows - 1) / rows * (g.kv_dim >> 3);
   const int64_t blocks = (threads + 255) / 256;
-  write_kernel<ELEM, STREAM><<<(unsigned)blocks, 256, 0, s>>>(
-      static_cast<uint8_t *>(k_layer), static_cast<uint8_t *>(v_layer), slots, k, v, n, src_stride, g.kv_dim,
-      g.n_blocks * 16, order, n_rows);
+  if (blocks >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  uint8_t *kp = static_cast<uint8_t *>(k_layer), *vp = static_cast<uint8_t *>(v_layer);
+  if constexpr (STREAM) {  // K, then V
+    write_kernel<ELEM, true, 1><<<(unsigned)blocks, 256, 0, s>>>(kp, vp, slots, k, v, n, src_stride, g.kv_dim,
+                                                                  g.n_blocks * 16, order, n_rows);
+    write_kernel<ELEM, true, 2><<<(unsigned)blocks, 256, 0, s>>>(kp, vp, slots, k, v, n, src_stride, g.kv_dim,
+                                                                  g.n_blocks * 16, order, n_rows);
+  } else {
+    write_kernel<ELEM, false><<<(unsigned)blocks, 256, 0, s>>>(kp, vp, slots, k, v, n, src_stride, g.kv_dim,
+                                                                g.n_blocks * 16, order, n_rows);
+  }
   return hipGetLastError();
 }
 
