@@ -41,7 +41,7 @@ static __device__ __align__(256) uint8_t scratch[ltkv::kScratchBytes];
 // Profiling build only (compiled with -DLTKV_TIMELINE into
 // libltkv_timeline.so; the product library has none of it): each wave of the
 // matrix-core decode kernel records s_memrealtime stamps (100 MHz) of its
-// phases in g_timeline[work-group][8], read and cleared by
+// phases in g_timeline[wave of the grid][8], read and cleared by
 // ltkv_timeline_read: 0 entry, 1 item found, 2 first tiles' loads issued,
 // 3 first tile computed, 4 tile loop done, 5 result written, 6 tiles of the
 // item, 7 query << 16 | partition << 8 | first kv head.
@@ -1683,6 +1683,7 @@ struct OrderShapes {
   int key[kOrderChunks], keyl[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
 };
 
+template <bool FIRST_WAVE_COUNTS = false>
 __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
                                                    int part_tokens, int split, int lane, int32_t *hist,
                                                    OrderShapes &sh) {
@@ -1697,8 +1698,12 @@ __device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ l
     if ((int64_t)c * 64 + lane < n) {
       decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.keyl[c],
                         sh.items[c], sh.len[c]);
-      if (sh.items[c] > 1) atomicAdd(hist + sh.key[c], sh.items[c] - 1);  // LDS
-      atomicAdd(hist + sh.keyl[c], 1);
+      // (several waves per work-group: every wave finds the shapes, the
+      // first one counts them)
+      if (!FIRST_WAVE_COUNTS || threadIdx.x < 64) {
+        if (sh.items[c] > 1) atomicAdd(hist + sh.key[c], sh.items[c] - 1);  // LDS
+        atomicAdd(hist + sh.keyl[c], 1);
+      }
     }
   }
   __syncthreads();
@@ -1799,8 +1804,21 @@ __device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
   return __builtin_bit_cast(h8, r);
 }
 
+// Waves per work-group of the matrix-core decode kernel: four consecutive
+// waves of the grid, i.e. the kv-head groups of one (query, partition) item
+// on one CU, which then reads whole pool rows together (each wave still
+// streams its own item; bit-identical results). Measured against one wave
+// per work-group: the Llama-3-8B fused decode step 140.9 -> 137.9 us (the
+// kernel ~134 us in the plain, graph and fused passes alike instead of
+// 133-137), q8_0 decode 3.5% and the Qwen2.5-7B step 2% faster, 32 x 32k
+// decode within the noise, config 3's per-query pass 1.4% slower. The wave
+// index is made scalar (readfirstlane) and the grid index kept 32-bit: as a
+// vector value or a 64-bit division it cost SGPR spills and 10%.
+template <int NH>
+constexpr int kDecodeWaves = 4;
+
 template <typename T, int HD, int G, int NH>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * kDecodeWaves<NH>)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
                  const int32_t *__restrict__ tables, int64_t table_stride,
                  const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
@@ -1835,9 +1853,15 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   static_assert(NQ <= 8, "hi and lo columns of the wave's query heads must fit 16");
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
   static_assert(LPR <= 64 && RPI * NLD == 16, "row segment must split over the wave");
-  __shared__ __attribute__((aligned(16))) char sk[NH][16 * KPITCH];
-  __shared__ __attribute__((aligned(16))) char sv[NH][16 * VPITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t ssc[2][Q8 ? NSC : 1];  // q8_0: K, V scales of a tile
+  constexpr int NW = kDecodeWaves<NH>;
+  // the wave in its work-group (uniform: kept in a scalar register)
+  const int wv = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  __shared__ __attribute__((aligned(16))) char sk_w[NW][NH][16 * KPITCH];
+  __shared__ __attribute__((aligned(16))) char sv_w[NW][NH][16 * VPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t ssc_w[NW][2][Q8 ? NSC : 1];  // q8_0: K, V scales of a tile
+  auto &sk = sk_w[wv];
+  auto &sv = sv_w[wv];
+  auto &ssc = ssc_w[wv];
 
   __shared__ int32_t shist[kOrderClasses];
 
@@ -1846,13 +1870,14 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // query w / max_parts; with `order`, item w of the longest-first list
   // (decode_order_find).
   const int n_groups = n_kv_heads / NH;
-  const int kvh0 = (int)(blockIdx.x % n_groups) * NH;
+  const unsigned gw = blockIdx.x * NW + wv;  // the grid's wave (the launch keeps it below 2^32)
+  const int kvh0 = (int)(gw % n_groups) * NH;
   const int lane = threadIdx.x & 63;
   const int lr = lane & 15, lq = lane >> 4;
   const int n_heads = n_kv_heads * G;
-  const int64_t wave_idx = blockIdx.x / n_groups;
+  const int64_t wave_idx = gw / n_groups;
   OrderShapes osh;
-  if (order) decode_order_setup(lens, n_queries, max_len, part_tokens, split, lane, shist, osh);
+  if (order) decode_order_setup<(NW > 1)>(lens, n_queries, max_len, part_tokens, split, lane, shist, osh);
 
   // B operands Q'_a^T of the score product, one per kv head a of the wave:
   // column lr < NQ holds the hi part of query head lr of the wave, column
@@ -1985,6 +2010,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     } else {
       part = (int)(wave_idx % max_parts);
       qx = wave_idx / max_parts;
+      if (NW > 1 && qx >= n_queries) return;  // waves past the grid's last item
     }
     const int64_t qi = qmap ? qmap[qx] : qx;
     int64_t len;
@@ -2413,8 +2439,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   LTKV_STAMP(5);
   tl_[6] = (unsigned long long)(cur.b1 - cur.b0);
   tl_[7] = (unsigned long long)cur.qi << 16 | (unsigned long long)cur.part << 8 | (unsigned long long)kvh0;
-  if (lane == 0 && blockIdx.x < kTimelineWaves)
-    for (int i = 0; i < 8; ++i) g_timeline[blockIdx.x * 8 + i] = tl_[i];
+  if (lane == 0 && gw < kTimelineWaves)
+    for (int i = 0; i < 8; ++i) g_timeline[gw * 8 + i] = tl_[i];
 #endif
   if (fault_q >= 0) report_fault(status, kFaultTable, fault_q);
 }
@@ -2430,8 +2456,9 @@ inline bool decode_ordered(const AttnArgs &a) {
 // heads.
 template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  const unsigned grid = (unsigned)(a.n * (a.n_kv_heads / NH) * a.max_parts);
-  attn_mfma_kernel<T, HD, G, NH><<<grid, 64, 0, s>>>(
+  constexpr int nw = kDecodeWaves<NH>;
+  const unsigned grid = (unsigned)((a.n * (a.n_kv_heads / NH) * a.max_parts + nw - 1) / nw);
+  attn_mfma_kernel<T, HD, G, NH><<<grid, 64 * nw, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
@@ -3699,7 +3726,7 @@ hipError_t scratch_address(int device, void **ptr) {
 }  // namespace ltkv
 
 #ifdef LTKV_TIMELINE
-// Copies the stamps of the last decode launch (n entries of the [work-group][8]
+// Copies the stamps of the last decode launch (n entries of the [wave][8]
 // array) to host memory and clears them; profiling build only.
 extern "C" __attribute__((visibility("default"))) int ltkv_timeline_read(unsigned long long *h, size_t n) {
   if (n > (size_t)kTimelineWaves * 8) n = (size_t)kTimelineWaves * 8;
