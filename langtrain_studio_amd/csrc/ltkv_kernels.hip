@@ -1561,7 +1561,8 @@ attn16_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const fl
 // FMA; with 1-byte q8_0 elements (or G > 4) that keeps the VALU busy for
 // longer than the tile's bytes take to arrive. Here both products of a
 // 16-token tile run on MFMA, one wave per (query, NH adjacent kv heads,
-// partition); NH = 2 when the 2 G query heads fit the 16 columns (G <= 4),
+// partition), four waves to a work-group (kDecodeWaves); NH = 2 when the
+// 2 G query heads fit the 16 columns (G <= 4),
 // so each row segment read is two heads wide (512 B for f16), and each
 // product then runs once per kv head, its Q' / P' zero outside that head's
 // columns:
