@@ -564,7 +564,7 @@ constexpr size_t kMinSharedBlocks = 2;
 // Tokens per group partition are at least this (a multiple of the kernel's
 // 32-token staging step).
 constexpr size_t kMinPrefixPart = 256;
-// Longest per-query remainder for which grouped plans use single-wave work-groups.
+// Longest per-query remainder for which grouped plans size the per-query pass's items themselves.
 constexpr size_t kShortRemainder = 512;
 
 size_t align8(size_t x) { return (x + 7) / 8 * 8; }
@@ -826,7 +826,7 @@ int build_plan(ltkv_cache *c, size_t n, const uint32_t *seqs, const uint32_t *le
     suffix_tokens += lens[i] - pre_tokens[i];
   }
   // With groups the per-query pass covers the (usually short) remainders:
-  // single-wave work-groups, about eight per CU, whatever the batch.
+  // one wave per item, about eight items per CU, whatever the batch.
   const uint64_t per_wg = suffix_tokens * n_kv_heads / (8 * (uint64_t)c->device_count_cu) + 1;
   P.suffix_part = (int)std::min<uint64_t>(1024, std::max<uint64_t>(64, (per_wg + 63) / 64 * 64));
   if ((uint64_t)n * sstride + (uint64_t)groups.size() * gstride > (uint64_t)INT32_MAX / 2)
