@@ -41,6 +41,19 @@ def test_library_exports_every_declared_symbol():
     assert exported == set(_declared()), exported ^ set(_declared())
 
 
+def test_profiling_build_adds_only_the_timeline_reader():
+    """libltkv_timeline.so (-DLTKV_TIMELINE) is the product's ABI plus
+    ltkv_timeline_read; the product library has no instrumentation symbol."""
+    from langtrain_studio_amd.build import TIMELINE_LIB
+
+    if not os.path.exists(TIMELINE_LIB):
+        pytest.skip("profiling build not built (python -m langtrain_studio_amd.build)")
+    out = subprocess.run(["nm", "-D", "--defined-only", TIMELINE_LIB], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if l.strip()}
+    exported = {e for e in exported if not e.startswith("__hip_cuid")}
+    assert exported == set(_declared()) | {"ltkv_timeline_read"}, exported ^ set(_declared())
+
+
 def test_header_compiles_as_c():
     src = f'#include "{HEADER}"\nint main(void) {{ return LTKV_BLOCK == 16 ? 0 : 1; }}\n'
     res = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-x", "c", "-", "-o", "/dev/null"],
