@@ -1435,7 +1435,9 @@ int decode_attention(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, size
   // ltkv_set_attention_partition), so its result is bit-identical whatever
   // else is in the batch (the reference's property, engine/README.md:102).
   // max_len only bounds the grid.
-  const int part = (int)c->attn_part_tokens;  // 0: per-query policy
+  int part = (int)c->attn_part_tokens;  // 0: the shape's per-query policy
+  const bool valu = c->attn_engine == LTKV_ENGINE_VALU && c->elem == 2;
+  if (part == 0) part = ltkv::attention_part_policy((int)c->elem, (int)group, (int)(c->kv_dim / head_dim), valu);
   const int parts = ltkv::max_partitions((int64_t)max_len, part);
   const int split = ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / head_dim));
   const size_t max_parts = (size_t)parts * split;
@@ -1683,6 +1685,9 @@ int ltkv_planned_attention(ltkv_cache *c, size_t layer, float scale, const float
   int part = (int)c->attn_part_tokens;
   const bool short_rem = grouped && part == 0 && P.sstride * LTKV_BLOCK <= kShortRemainder;
   if (short_rem) part = P.suffix_part;
+  else if (part == 0)
+    part = ltkv::attention_part_policy((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim),
+                                       c->attn_engine == LTKV_ENGINE_VALU && c->elem == 2);
   const int parts = ltkv::max_partitions((int64_t)(P.sstride * LTKV_BLOCK), part);
   const int split =
       short_rem ? 1 : ltkv::attention_split((int)c->elem, (int)group, (int)(c->kv_dim / P.head_dim));

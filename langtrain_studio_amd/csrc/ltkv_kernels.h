@@ -107,7 +107,7 @@ struct AttnArgs {
   int64_t n;
   int n_heads, n_kv_heads, head_dim;
   float scale;
-  int part_tokens, max_parts;  // part_tokens 0: per-query partition_tokens(len)
+  int part_tokens, max_parts;  // part_tokens 0 or kPartCap: per-query partition_tokens(len, part_tokens)
   // The matrix-core decode kernel cuts each partition into `split`
   // (partition_tokens(len) / split tokens each, split 1 or 2); max_parts
   // counts the finer partitions. attention_split gives it for a shape.
@@ -154,18 +154,24 @@ struct AttnArgs {
   int32_t *status;
 };
 
-// Context tokens per attention partition when none is fixed: four
-// partitions of a query up to 4096 tokens (at least 64 tokens each), 1024
-// tokens beyond. It depends on the query's own length only, so a query's
-// result never depends on the rest of the batch.
+// Partition policy kPartCap (part_tokens -1): 1024-token partitions (the
+// last one the rest) for queries over 2048 tokens, four equal ones below.
+constexpr int kPartCap = -1;
+
+// Context tokens per attention partition when none is fixed (part_tokens 0):
+// four partitions of a query up to 4096 tokens (at least 64 tokens each),
+// 1024 tokens beyond; with kPartCap already beyond 2048 tokens. Either way it
+// depends on the query's own length only, so a query's result never depends
+// on the rest of the batch.
 __host__ __device__ inline int partition_tokens(int64_t len, int fixed) {
   if (fixed > 0) return fixed;
-  if (len > 4096) return 1024;
+  if (len > (fixed == kPartCap ? 2048 : 4096)) return 1024;
   const int64_t p = ((len + 3) / 4 + 63) / 64 * 64;
   return p < 64 ? 64 : (int)p;
 }
 
-// Upper bound of partitions per query for contexts up to max_tokens.
+// Upper bound of partitions per query for contexts up to max_tokens (the
+// same for both per-query policies: at most four up to 4096 tokens).
 inline int max_partitions(int64_t max_tokens, int fixed) {
   if (fixed > 0) return (int)((max_tokens + fixed - 1) / fixed);
   const int64_t beyond = (max_tokens + 1023) / 1024;
@@ -192,6 +198,9 @@ bool attention_supported(int elem, int head_dim, int group);
 // partition divisor (1 or 2) of such a shape, 1 otherwise. It never depends
 // on the batch: a query's result bits depend on its own inputs only.
 int attention_split(int elem, int group, int n_kv_heads);
+// The per-query partition policy of a shape (and engine: valu for
+// LTKV_ENGINE_VALU) when none is fixed: kPartCap or 0.
+int attention_part_policy(int elem, int group, int n_kv_heads, bool valu);
 hipError_t launch_decode_attention(const PoolGeom &g, const AttnArgs &a, hipStream_t s);
 
 // One work-group of shared-prefix attention (mq_attn_kernel): the query rows
