@@ -280,9 +280,8 @@ LTKV_API int ltkv_append_decode_attention(ltkv_cache *c, size_t layer, size_t n,
 /* Tokens per context partition of the decode attention split (multiple of
  * 64), or 0 (the default) for the per-query policy: a query is split into
  * four partitions of ceil(len/4) rounded up to 64 tokens (at least 64) up to
- * 4096 tokens, and into 1024-token partitions beyond; on f16 pools with at
- * most 4 query heads per kv head (and an even kv head count), on the
- * matrix-core engine, the 1024-token partitions start beyond 2048 tokens.
+ * 4096 tokens, and into 1024-token partitions beyond; on f16 pools (the
+ * matrix-core engine) the 1024-token partitions start beyond 2048 tokens.
  * Either way a query's result depends only on its own inputs, the cache's
  * shape and its engine, never on the rest of the batch. Tuning knob. */
 LTKV_API int ltkv_set_attention_partition(ltkv_cache *c, size_t tokens);

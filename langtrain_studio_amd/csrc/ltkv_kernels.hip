@@ -3669,14 +3669,18 @@ int attention_split(int elem, int group, int n_kv_heads) {
 int attention_part_policy(int elem, int group, int n_kv_heads, bool valu) {
   // Measured at the Llama-3-8B decode shape (64 queries x U[2048, 4096], f16,
   // two kv heads a wave, four waves a work-group): 1024-token partitions for
-  // queries over 2048 tokens (2-4 per query: about 768 waves, the last
-  // partition of a query short) 127.9 us per fused step against 137.4-137.9
-  // with four equal partitions (1024 waves); 768- or 2048-token ones 157 /
-  // 178 us. q8_0 pools (partitions cut in two) and one-kv-head waves lose
-  // with it (91.0 against 87.8 us; Qwen2.5-7B step 202.8 against 200.1 us)
-  // and keep four equal partitions, as does the vector-ALU engine (147.6
-  // against 144.8 us with kPartCap). A function of the shape and engine only.
-  return !valu && elem == 2 && group <= 4 && n_kv_heads % 2 == 0 ? kPartCap : 0;
+  // queries over 2048 tokens (2-4 per query: about 900 waves, most of them
+  // whole 64-tile partitions that end together, the last partition of a
+  // query short) 127.9 us per fused step against 137.4-137.9 with four equal
+  // partitions (1024 waves); 768- or 2048-token ones for every query 157 /
+  // 178 us. The Qwen2.5-7B step (one kv head a wave) gains too (196.4-196.8
+  // against 199.7 us). q8_0 pools (partitions cut in two) lose with it
+  // (91.0 against 87.8 us), as does the vector-ALU engine (147.6 against
+  // 144.8 us): they keep four equal partitions. A function of the shape and
+  // engine only.
+  (void)group;
+  (void)n_kv_heads;
+  return !valu && elem == 2 ? kPartCap : 0;
 }
 
 int mq_rows(int, int) { return 32 * kMqWaves; }
