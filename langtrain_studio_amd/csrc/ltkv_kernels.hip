@@ -1815,11 +1815,10 @@ __device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
 // decode within the noise, config 3's per-query pass 1.4% slower. The wave
 // index is made scalar (readfirstlane) and the grid index kept 32-bit: as a
 // vector value or a 64-bit division it cost SGPR spills and 10%.
-template <int NH>
 constexpr int kDecodeWaves = 4;
 
 template <typename T, int HD, int G, int NH>
-__global__ void __launch_bounds__(64 * kDecodeWaves<NH>)
+__global__ void __launch_bounds__(64 * kDecodeWaves)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
                  const int32_t *__restrict__ tables, int64_t table_stride,
                  const int32_t *__restrict__ lens, float *__restrict__ out, float *__restrict__ part_o,
@@ -1854,7 +1853,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   static_assert(NQ <= 8, "hi and lo columns of the wave's query heads must fit 16");
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
   static_assert(LPR <= 64 && RPI * NLD == 16, "row segment must split over the wave");
-  constexpr int NW = kDecodeWaves<NH>;
+  constexpr int NW = kDecodeWaves;
   // the wave in its work-group (uniform: kept in a scalar register)
   const int wv = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ __attribute__((aligned(16))) char sk_w[NW][NH][16 * KPITCH];
@@ -2457,7 +2456,7 @@ inline bool decode_ordered(const AttnArgs &a) {
 // heads.
 template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
-  constexpr int nw = kDecodeWaves<NH>;
+  constexpr int nw = kDecodeWaves;
   const unsigned grid = (unsigned)((a.n * (a.n_kv_heads / NH) * a.max_parts + nw - 1) / nw);
   attn_mfma_kernel<T, HD, G, NH><<<grid, 64 * nw, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
