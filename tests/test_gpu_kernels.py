@@ -395,21 +395,31 @@ def test_attention_partitions(gpu, partition):
     attention_close(out, want, "f16")
 
 
-@pytest.mark.parametrize("lens,fixed", [
-    ([1537, 1600, 1580], 448),     # ceil(len/4) in (384, 448]
-    ([2, 40, 255, 256], 64),       # the 64-token floor
-    ([4097, 9000, 5000], 1024),    # beyond 4096 tokens
+@pytest.mark.parametrize("dtype,engine,lens,fixed", [
+    ("f16", "auto", [1537, 1600, 1580], 448),     # ceil(len/4) in (384, 448]
+    ("f16", "auto", [2, 40, 255, 256], 64),       # the 64-token floor
+    ("f16", "auto", [2048, 2000, 1985], 512),     # four equal partitions up to 2048 tokens
+    ("f16", "auto", [2049, 3000, 4096], 1024),    # f16 matrix cores: 1024 tokens past 2048
+    ("f16", "auto", [4097, 9000, 5000], 1024),    # beyond 4096 tokens
+    ("f16", "valu", [3000, 2990, 2945], 768),     # the vector-ALU engine: four up to 4096
+    ("f16", "valu", [4097, 5000], 1024),
+    ("q8_0", "auto", [3000, 2990, 2945], 768),    # q8_0 pools: four up to 4096
+    ("q8_0", "auto", [4097, 6000], 1024),
+    ("f32", "auto", [3000, 2990], 768),           # f32 pools: four up to 4096
 ])
-def test_attention_default_policy_is_per_query_partition(gpu, lens, fixed):
+def test_attention_default_policy_is_per_query_partition(gpu, dtype, engine, lens, fixed):
     """With no fixed partition a query of len tokens is split into partitions
-    of roundup64(ceil(len/4)) tokens (at least 64; 1024 past 4096 tokens):
-    the output equals, bit for bit, the one with that partition fixed."""
+    of roundup64(ceil(len/4)) tokens (at least 64), and of 1024 tokens past
+    4096 tokens, or past 2048 tokens on f16 pools on the matrix cores: the
+    output equals, bit for bit, the one with that partition fixed."""
     import torch
 
-    rng = np.random.default_rng(fixed)
+    rng = np.random.default_rng(fixed + len(lens))
     kv_dim = 1024
     blocks = sum(-(-n // BLOCK) for n in lens) + 4
-    g, o = _caches(1, kv_dim, blocks * BLOCK, "f16", rng.permutation(blocks))
+    g, o = _caches(1, kv_dim, blocks * BLOCK, dtype, rng.permutation(blocks))
+    if engine != "auto":
+        g.set_attention_engine(engine)
     fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, kv_dim)
     tables, la = tables_and_lens(g, list(range(len(lens))), lens)
     q = torch.from_numpy(rng.standard_normal((len(lens), 32 * 128), dtype=np.float32)).to(gpu)
@@ -417,9 +427,9 @@ def test_attention_default_policy_is_per_query_partition(gpu, lens, fixed):
     auto = g.decode_attention(0, q, dt, dl, 32, 128).cpu().numpy()
     g.set_attention_partition(fixed)
     pinned = g.decode_attention(0, q, dt, dl, 32, 128).cpu().numpy()
-    np.testing.assert_array_equal(auto, pinned)
+    np.testing.assert_array_equal(auto.view(np.uint32), pinned.view(np.uint32))
     want = o.attention_tables(0, tables, la, q.cpu().numpy(), 32, 128, threads=8)
-    attention_close(auto, want, "f16")
+    attention_close(auto, want, dtype)
 
 
 def test_attention_config_tinyllama_f32(gpu):
