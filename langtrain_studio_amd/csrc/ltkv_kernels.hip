@@ -2452,8 +2452,9 @@ inline bool decode_ordered(const AttnArgs &a) {
   return !a.qmap && !a.pre_parts && a.n > 1 && a.n <= kOrderMaxQueries;
 }
 
-// One wave per work-group and item: each streams a whole partition of NH kv
-// heads.
+// One wave per item (a partition of NH kv heads of one query), kDecodeWaves
+// consecutive items per work-group; the grid is rounded up to whole
+// work-groups and the waves past the last item leave at once.
 template <typename T, int HD, int G, int NH>
 hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
   constexpr int nw = kDecodeWaves;
