@@ -1294,11 +1294,62 @@ def bench_decode_timeline(args):
               flush=True)
     del w
     torch.cuda.synchronize()
+    _timeline_qwen_decode(read, args.seed)
 
     def emit(what):
         print(json.dumps({"workload": "decode-timeline " + what, **_timeline_stats(read())}), flush=True)
 
     bench_prefix_cow(args, timeline=emit)
+
+
+def _timeline_qwen_decode(read, seed):
+    """Per-wave timeline of one decode launch at the Qwen2.5-7B shape (28 q
+    heads, 4 kv heads, head_dim 128, f16: one kv head a wave, two waves per
+    SIMD), 120 queries of contexts U[512, 8192] over a permuted pool: about
+    2500 items on 2048 wave slots, so waves share SIMDs and some start when
+    others end. Also reports the waves started in the launch's first 50 us
+    (two per SIMD) by half: the first 1024 of the grid against the rest."""
+    import torch
+
+    from langtrain_studio_amd import KvCache
+
+    n_heads, n_kv, hd, n_q = 28, 4, 128, 120
+    kvd = n_kv * hd
+    rng = np.random.default_rng(seed)
+    n_blocks = n_q * 8192 // BLOCK + 64
+    kv = KvCache(1, kvd, n_blocks * BLOCK, dtype="f16", device=0, stream=torch.cuda.current_stream())
+    kv.init_free_order(rng.permutation(n_blocks))
+    _fill_pool_random(kv, kvd, n_blocks, seed)
+    lens = rng.integers(512, 8193, size=n_q)
+    for i, n in enumerate(lens):
+        kv.append_batch(np.full(int(n), i, np.uint32), np.arange(int(n), dtype=np.uint64))
+    tables = torch.from_numpy(kv.block_tables(np.arange(n_q, dtype=np.uint32), 8192 // BLOCK)).cuda()
+    d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
+    q = torch.randn((n_q, n_heads * hd), device="cuda")
+    out = torch.empty_like(q)
+    for _ in range(3):
+        kv.decode_attention(0, q, tables, d_lens, n_heads, hd, out=out)
+    torch.cuda.synchronize()
+    read()
+    for _ in range(5):
+        kv.decode_attention(0, q, tables, d_lens, n_heads, hd, out=out)
+    t = read()
+    stats = _timeline_stats(t)
+    t = t[t[:, 0] > 0].astype(np.int64)
+    t0 = int(t[:, 0].min())
+    early = (t[:, 0] - t0) < 5000  # entered in the first 50 us
+    halves = {}
+    for name, sel in (("grid_waves_0_1023", early & (np.arange(len(t)) < 1024)),
+                      ("grid_waves_1024_up", early & (np.arange(len(t)) >= 1024))):
+        if sel.any():
+            halves[name] = {"waves": int(sel.sum()),
+                            "first_loads_issued_p50_us": round(float(np.median(t[sel, 2] - t0)) / 100.0, 2),
+                            "result_written_p50_us": round(float(np.median(t[sel, 5] - t0)) / 100.0, 2)}
+    print(json.dumps({"workload": "decode-timeline qwen2.5-7b-layer decode, 120 seqs ctx U[512,8192], f16, "
+                                  "unfused attention launch", **stats, "first_round_by_grid_half": halves}),
+          flush=True)
+    del kv
+    torch.cuda.synchronize()
 
 
 def bench_decode_shapes(args):

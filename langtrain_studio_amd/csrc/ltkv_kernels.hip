@@ -1834,6 +1834,16 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 #ifdef LTKV_TIMELINE
   unsigned long long tl_[8] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0, 0, 0};
 #endif
+  // Issue priority (s_setprio) among the waves of a SIMD: the highest until
+  // the first tiles' loads are issued, then by tiles left (wave_priority).
+  // Where two waves share a SIMD, the one that arrived first otherwise wins
+  // nearly every vector-memory issue slot while the memory system is
+  // saturated: a wave arriving beside a streaming one took ~15 us to issue
+  // its first loads, and the first waves finished long before the second
+  // ones (Qwen2.5-7B step, 120 queries: first waves done at ~89 us, second
+  // ones at ~156 us, a tail of one wave per SIMD after them). Priorities
+  // change nothing for correctness.
+  __builtin_amdgcn_s_setprio(3);
   constexpr bool Q8 = std::is_same_v<T, int8_t>;
   constexpr int KS = HD / 32;              // score k steps: one q8_0 scale group each
   constexpr int DT = HD / 16;              // 16-row tiles of O^T
@@ -2386,6 +2396,15 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   auto load_b = [&](int bb, int32_t entry, Stage &st) __attribute__((always_inline)) {
     load_tile(entry, cur.qi, cur.tok1, cur.b_new, cur.r_new, bb < cur.b1, bb, st);
   };
+  // More tiles left, more priority: the waves of a SIMD end their items
+  // together instead of one after the other (Qwen2.5-7B step 197.5-198.0
+  // -> 189.7-191.6 us; thresholds 40 / 16 or 32 / 12 tiles measured within
+  // 1% of these; one wave per SIMD, as at the Llama-3-8B shape, is unchanged).
+  auto wave_priority = [&](int left) __attribute__((always_inline)) {
+    if (left > 48) __builtin_amdgcn_s_setprio(2);
+    else if (left > 24) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+  };
   if (b < cur.b1) {
     if constexpr (STAGES == 3) {
       Stage s0, s1, s2;
@@ -2397,6 +2416,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
+        wave_priority(cur.b1 - b);
         int32_t ea = entry_of(b + 3);
         load_b(b + 2, en, s2);
         compute_tile(b, s0);
@@ -2421,6 +2441,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
       convert_q(qr, qb, qbias);
       commit_new(cur, kr, vr, nk, nv);
       for (;;) {
+        wave_priority(cur.b1 - b);
         int32_t ea = entry_of(b + 2);
         load_b(b + 1, en, s1);
         compute_tile(b, s0);
