@@ -556,6 +556,7 @@ ltkv::AttnArgs attn_args(ltkv_cache *c, size_t layer, size_t n, size_t n_heads, 
   a.split = 1;
   a.valu = c->attn_engine == LTKV_ENGINE_VALU && c->elem == 2;
   a.status = c->d_status;
+  a.cu_count = c->device_count_cu;
   return a;
 }
 

@@ -119,6 +119,9 @@ struct AttnArgs {
   // Lengths are cut to max_len tokens (at most table_stride * 16); the grid's
   // max_parts covers max_len.
   int64_t max_len;
+  // Compute units of the device (the matrix-core decode kernel's wave slots;
+  // 0: no runs of partitions per wave).
+  int cu_count;
   // The caller knows no query needs the merge pass: every query has one
   // partition, and none with group partials has an empty remainder (the
   // matrix-core kernel folds group partials of single-partition queries).

@@ -1644,70 +1644,99 @@ __device__ __forceinline__ int q_range_exp(float amax) {
 // pairs (times the kv-head groups, fastest). Taken in query order, a batch of
 // mixed lengths leaves the SIMDs whose waves drew short partitions idle while
 // the longest ones finish, and the chip stops being bandwidth-bound well
-// before the end. So the items are taken by descending partition size class
-// (64-token classes), then query index, then partition: the hardware hands
+// before the end. So the items are taken by descending size class (32-token
+// classes), then query index, then partition: the hardware hands
 // work-groups to freed SIMDs in grid order, which makes this longest-first
 // list scheduling. Each wave finds its item from the lengths alone (one
 // histogram in LDS, one prefix scan per 64 queries), so nothing is computed
 // or uploaded per step on the host; a query's partitions and result bits do
 // not depend on where its items land.
+//
+// When the batch holds at least twice as many partitions (times the kv-head
+// groups) as the chip holds waves at once, an item is a run of k consecutive
+// partitions of one query, k = partitions / wave slots: one wave streams
+// them back to back and writes each partition's partial as it passes its
+// end, so every partial (and every output bit) is the one a wave per
+// partition writes, while each wave pays its start (order scan, first table
+// entries and loads: ~7 us) once per k partitions (32 queries x 32768
+// tokens: 4096 partition items on 1024 slots, k = 4). Size classes then
+// count 32 k tokens.
 // ----------------------------------------------------------------------------
-constexpr int kOrderClasses = 32;  // 32-token size classes of an item
+constexpr int kOrderClasses = 32;  // size classes of an item (32 k tokens each)
 constexpr int kOrderMaxQueries = 256;  // beyond this, query order (the scans would cost more)
 constexpr int kOrderChunks = kOrderMaxQueries / 64;
 
-__device__ __forceinline__ int order_class(int tokens) {
-  return tokens >> 5 < kOrderClasses - 1 ? tokens >> 5 : kOrderClasses - 1;
+__device__ __forceinline__ int order_class(int tokens, int k) {
+  const int c = (tokens / k) >> 5;
+  return c < kOrderClasses - 1 ? c : kOrderClasses - 1;
 }
 
-// Query q's items: `items` partitions, all but the last of the partition's
-// size (class key), the last of the tokens left (class keyl; 0 tokens for an
-// empty query).
-__device__ __forceinline__ void decode_item_shape(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
-                                                  int part_tokens, int split, int &key, int &keyl, int &items,
-                                                  int &clen) {
+// Query q's length (clamped), partition size and partition count.
+__device__ __forceinline__ void decode_query_parts(const int32_t *__restrict__ lens, int64_t q, int64_t max_len,
+                                                   int part_tokens, int split, int &clen, int &pt, int &np) {
   int64_t len = lens[q];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
   clen = (int)len;
-  const int pt = partition_tokens(len, part_tokens) / split;
-  items = len > 0 ? (int)((len + pt - 1) / pt) : 1;
-  key = order_class(pt);
-  keyl = order_class(len > 0 ? (int)(len - (int64_t)(items - 1) * pt) : 0);
+  pt = partition_tokens(len, part_tokens) / split;
+  np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
 }
 
 // Size classes and item counts of queries lane, 64 + lane, ... (n <=
 // kOrderMaxQueries; zero past n), and the items per class in `hist`
-// (kOrderClasses ints of LDS): a query's last partition counts in the class
-// of its own length, so the list is longest first item by item. One wave.
+// (kOrderClasses ints of LDS): a query's items are runs of k partitions, all
+// but the last of k partitions (class key), the last of the tokens left
+// (class keyl; 0 tokens for an empty query), so the list is longest first
+// item by item. One wave; returns k (the same in every wave: it depends on
+// the lengths, the grid's kv-head groups, the wave slots and max_run only).
 struct OrderShapes {
   int key[kOrderChunks], keyl[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
 };
 
 template <bool FIRST_WAVE_COUNTS = false>
-__device__ __forceinline__ void decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
-                                                   int part_tokens, int split, int lane, int32_t *hist,
-                                                   OrderShapes &sh) {
+__device__ __forceinline__ int decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
+                                                  int part_tokens, int split, int lane, int32_t *hist,
+                                                  OrderShapes &sh, int n_groups, int slots, int max_run) {
   if (lane < kOrderClasses) hist[lane] = 0;
   __syncthreads();
+  int pt[kOrderChunks];
+  int total = 0;
 #pragma unroll
   for (int c = 0; c < kOrderChunks; ++c) {
     sh.key[c] = 0;
     sh.keyl[c] = 0;
     sh.items[c] = 0;
     sh.len[c] = 0;
+    pt[c] = 1;
     if ((int64_t)c * 64 + lane < n) {
-      decode_item_shape(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.key[c], sh.keyl[c],
-                        sh.items[c], sh.len[c]);
+      decode_query_parts(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.len[c], pt[c],
+                         sh.items[c]);
+      total += sh.items[c];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+  const int64_t waves = (int64_t)__builtin_amdgcn_readfirstlane(total) * n_groups;
+  int k = slots > 0 && waves >= 2 * (int64_t)slots ? (int)(waves / slots) : 1;
+  k = k < max_run ? k : max_run;
+#pragma unroll
+  for (int c = 0; c < kOrderChunks; ++c) {
+    if ((int64_t)c * 64 + lane < n) {
+      const int np = sh.items[c], len = sh.len[c];
+      const int items = (np + k - 1) / k;
+      sh.items[c] = items;
+      sh.key[c] = order_class(k * pt[c], k);
+      sh.keyl[c] = order_class(len > 0 ? len - (items - 1) * k * pt[c] : 0, k);
       // (several waves per work-group: every wave finds the shapes, the
       // first one counts them)
       if (!FIRST_WAVE_COUNTS || threadIdx.x < 64) {
-        if (sh.items[c] > 1) atomicAdd(hist + sh.key[c], sh.items[c] - 1);  // LDS
+        if (items > 1) atomicAdd(hist + sh.key[c], items - 1);  // LDS
         atomicAdd(hist + sh.keyl[c], 1);
       }
     }
   }
   __syncthreads();
+  return k;
 }
 
 // Item t of the ordered list: its query qx and partition part, or false when
@@ -1817,7 +1846,7 @@ __device__ __forceinline__ h8 i8x8_to_h8_biased(const u32x2 &w) {
 // vector value or a 64-bit division it cost SGPR spills and 10%.
 constexpr int kDecodeWaves = 4;
 
-template <typename T, int HD, int G, int NH>
+template <typename T, int HD, int G, int NH, bool RUNS>
 __global__ void __launch_bounds__(64 * kDecodeWaves)
 attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const float *__restrict__ q,
                  const int32_t *__restrict__ tables, int64_t table_stride,
@@ -1830,7 +1859,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
                  int max_pre_parts, const int32_t *__restrict__ new_slots,
                  const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
-                 T *kdst, T *vdst, int64_t n_queries, int order, int32_t *__restrict__ status) {
+                 T *kdst, T *vdst, int64_t n_queries, int order, int slots, int32_t *__restrict__ status) {
 #ifdef LTKV_TIMELINE
   unsigned long long tl_[8] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0, 0, 0};
 #endif
@@ -1872,13 +1901,29 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   auto &sk = sk_w[wv];
   auto &sv = sv_w[wv];
   auto &ssc = ssc_w[wv];
+  // RUNS (ordered launches with many more partitions than wave slots, f16
+  // two-head waves): a wave may stream a run of up to kRunSlots + 1
+  // partitions. The partials of a run's partitions before its last stay in
+  // LDS until the wave's end: stores inside the tile loop make the waits for
+  // the loads issued after them wait for the stores too (vector memory
+  // operations complete in order), and under the loop's load traffic such a
+  // store took ~19 us to complete (32 x 32768 tokens: 686 us with the
+  // partials stored as they end, 630 us without the stores). The slots fit
+  // beside the tiles at one work-group per CU. The run logic costs registers
+  // and a scheduling boundary per tile, so launches that cannot form runs
+  // take the kernel without it (RUNS false): kernels at two waves per SIMD
+  // (q8_0, one-head waves) lost their occupancy or 3% with it.
+  static_assert(!RUNS || (NH == 2 && !Q8), "runs of partitions: f16 two-head waves");
+  constexpr int kRunSlots = RUNS ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) f32x4 srun_o[NW][kRunSlots][RUNS ? DT : 1][RUNS ? NQ * 4 : 1];
+  __shared__ float srun_ml[NW][kRunSlots][RUNS ? NQ : 1][2];
 
   __shared__ int32_t shist[kOrderClasses];
 
   // 1-D grid of (wave, NH-head group), the head group fastest. Wave w of a
   // head group streams one item: without `order`, partition w % max_parts of
   // query w / max_parts; with `order`, item w of the longest-first list
-  // (decode_order_find).
+  // (decode_order_find), a run of `run` consecutive partitions of a query.
   const int n_groups = n_kv_heads / NH;
   const unsigned gw = blockIdx.x * NW + wv;  // the grid's wave (the launch keeps it below 2^32)
   const int kvh0 = (int)(gw % n_groups) * NH;
@@ -1887,7 +1932,10 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   const int n_heads = n_kv_heads * G;
   const int64_t wave_idx = gw / n_groups;
   OrderShapes osh;
-  if (order) decode_order_setup<(NW > 1)>(lens, n_queries, max_len, part_tokens, split, lane, shist, osh);
+  int run = 1;
+  if (order)
+    run = decode_order_setup<(NW > 1)>(lens, n_queries, max_len, part_tokens, split, lane, shist, osh, n_groups,
+                                       slots, RUNS ? kRunSlots + 1 : 1);
 
   // B operands Q'_a^T of the score product, one per kv head a of the wave:
   // column lr < NQ holds the hi part of query head lr of the wave, column
@@ -1999,7 +2047,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // Every field is uniform over the wave (scalar registers).
   struct Item {
     int64_t qi, len, tok1;
-    int part, np, b0, b1;
+    int part, np, b0, b1;  // part: the partition of tile b (the item's first one at the start)
+    int p0, plast, pt_tiles;  // the item's first and last partitions; tiles per partition
     const int32_t *tab;
     int b_new, r_new;  // fused new row: its tile and row (b_new -1: none)
     int32_t cell;      // ... and its pool cell
@@ -2036,13 +2085,19 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
     const int pt = partition_tokens(len, part_tokens) / split;
     const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+    // the item's partitions: run of them from part * run (run 1 without order)
+    part *= run;
     if (part >= np) return;
-    const int64_t tok0 = (int64_t)part * pt;
+    const int plast = part + run - 1 < np - 1 ? part + run - 1 : np - 1;
+    const int64_t tok0 = (int64_t)part * pt, tend = (int64_t)(plast + 1) * pt;
     it.qi = qi;
     it.len = len;
     it.part = part;
+    it.p0 = part;
+    it.plast = plast;
+    it.pt_tiles = pt >> 4;  // partitions are multiples of 32 tokens
     it.np = np;
-    it.tok1 = len < tok0 + pt ? len : tok0 + pt;
+    it.tok1 = len < tend ? len : tend;
     it.b0 = (int)(tok0 >> 4);
     it.b1 = (int)((it.tok1 + 15) >> 4);
     // A resident row outside the tables reads row 0 and is a fault when the
@@ -2070,7 +2125,7 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     it.cell = -1;
     kr[0] = kr[1] = vr[0] = vr[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (!Q8) {
-      if (new_slots && part == np - 1 && len > 0) {  // uniform
+      if (new_slots && plast == np - 1 && len > 0) {  // uniform
         const int32_t cell = scalar_read(new_slots, qi);
         // The cell must be position len - 1 of the query's table (what the
         // claim returned for it); otherwise write-then-attend would differ.
@@ -2300,17 +2355,15 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     }
   };
 
-  // The item's result: the output (one partition) or its partial.
-  auto finish = [&](const Item &it) __attribute__((always_inline)) {
-    // The lane's own head's accumulators.
-    f32x4 o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = oacc[0][dt];
+  // The lane's own head's column sums, in place (the accumulators are reset
+  // or dead afterwards): oacc[0] holds the numerators of rows d = 16 dt +
+  // 4 lq + i of query head lr (the hi lanes), l_run the column's sum.
+  auto reduce_acc = [&]() __attribute__((always_inline)) {
     if constexpr (OS > 1) {
 #pragma unroll
       for (int a = 1; a < OS; ++a)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] = a == my_head ? oacc[a][dt] : o[dt];
+        for (int dt = 0; dt < DT; ++dt) oacc[0][dt] = a == my_head ? oacc[a][dt] : oacc[0][dt];
     }
     // Column sums over the four lane rows; hi + lo parts of the numerators.
     l_run += __shfl_xor(l_run, 16);
@@ -2318,68 +2371,83 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[dt][i] += dpp<0x140>(o[dt][i]);
-    if (!hi_lane) return;  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
+      for (int i = 0; i < 4; ++i) oacc[0][dt][i] += dpp<0x140>(oacc[0][dt][i]);
+  };
+  // Partial (numerators, reference, sum) of partition it.part, after reduce_acc.
+  auto write_partial = [&](const Item &it) __attribute__((always_inline)) {
+    if (!hi_lane) return;
     const int64_t qh = it.qi * n_heads + (int64_t)kvh0 * G + lr;
-    if (it.np == 1) {  // one partition: this wave writes the output
-      const int npre = pre_parts ? pre_parts[it.qi] : 0;
-      if (npre > 0) {
-        // Fold the query's group partials (numerator, reference, sum) into
-        // the wave's own, four partials per round (indices clamped to the
-        // last partial, with weight 0 past it): one round of loads brings
-        // their references, sums and numerators together, and the running
-        // reference is raised to the round's maximum as it goes (the
-        // accumulators rescaled), so no separate pass finds the maximum.
-        const float *pml = pre_ml + qh * max_pre_parts * 2;
-        float mref = m_ref;
-        for (int p0 = 0; p0 < npre; p0 += 4) {
-          f32x4 po[4][DT];
-          float pm[4], pl[4];
+    const int64_t pi = qh * max_parts + it.part;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int pc = p0 + u < npre ? p0 + u : npre - 1;
-            const float *src = pre_o + (qh * max_pre_parts + pc) * HD + 4 * lq;
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4 *>(part_o + pi * HD + 16 * dt + 4 * lq) = oacc[0][dt];
+    if (lq == 0) {
+      part_ml[2 * pi] = m_ref;
+      part_ml[2 * pi + 1] = l_run;
+    }
+  };
+
+  // The item's result: the output (one partition) or the partial of its last
+  // partition.
+  auto finish = [&](const Item &it) __attribute__((always_inline)) {
+    reduce_acc();
+    if (!hi_lane) return;  // lane (j, lq) holds rows d = 16 dt + 4 lq + i of the wave's query head j
+    if (it.np > 1) {
+      write_partial(it);
+      return;
+    }
+    auto &o = oacc[0];
+    const int64_t qh = it.qi * n_heads + (int64_t)kvh0 * G + lr;
+    // one partition: this wave writes the output
+    const int npre = pre_parts ? pre_parts[it.qi] : 0;
+    if (npre > 0) {
+      // Fold the query's group partials (numerator, reference, sum) into
+      // the wave's own, four partials per round (indices clamped to the
+      // last partial, with weight 0 past it): one round of loads brings
+      // their references, sums and numerators together, and the running
+      // reference is raised to the round's maximum as it goes (the
+      // accumulators rescaled), so no separate pass finds the maximum.
+      const float *pml = pre_ml + qh * max_pre_parts * 2;
+      float mref = m_ref;
+      for (int p0 = 0; p0 < npre; p0 += 4) {
+        f32x4 po[4][DT];
+        float pm[4], pl[4];
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) po[u][dt] = *reinterpret_cast<const f32x4 *>(src + 16 * dt);
-            pm[u] = pml[2 * pc];
-            pl[u] = pml[2 * pc + 1];
-          }
-          float mx = mref;
+        for (int u = 0; u < 4; ++u) {
+          const int pc = p0 + u < npre ? p0 + u : npre - 1;
+          const float *src = pre_o + (qh * max_pre_parts + pc) * HD + 4 * lq;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pm[u]);  // clamped: a repeat, harmless
-          // While every reference seen is -inf (empty partials, empty own
-          // range) the running reference stays -inf and nothing is added; it
-          // never takes a finite placeholder that later rounds would use as a
-          // floor.
-          const bool any = mx != -INFINITY;
-          const float a0 = any ? __builtin_amdgcn_exp2f(mref - mx) : 1.f;
-          l_run *= a0;
+          for (int dt = 0; dt < DT; ++dt) po[u][dt] = *reinterpret_cast<const f32x4 *>(src + 16 * dt);
+          pm[u] = pml[2 * pc];
+          pl[u] = pml[2 * pc + 1];
+        }
+        float mx = mref;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
-          mref = any ? mx : mref;
+        for (int u = 0; u < 4; ++u) mx = __builtin_fmaxf(mx, pm[u]);  // clamped: a repeat, harmless
+        // While every reference seen is -inf (empty partials, empty own
+        // range) the running reference stays -inf and nothing is added; it
+        // never takes a finite placeholder that later rounds would use as a
+        // floor.
+        const bool any = mx != -INFINITY;
+        const float a0 = any ? __builtin_amdgcn_exp2f(mref - mx) : 1.f;
+        l_run *= a0;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float a = p0 + u < npre && any ? __builtin_amdgcn_exp2f(pm[u] - mref) : 0.f;
-            l_run += pl[u] * a;
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
+        mref = any ? mx : mref;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a;
-          }
+        for (int u = 0; u < 4; ++u) {
+          const float a = p0 + u < npre && any ? __builtin_amdgcn_exp2f(pm[u] - mref) : 0.f;
+          l_run += pl[u] * a;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[dt] += po[u][dt] * a;
         }
       }
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<f32x4 *>(out + qh * HD + 16 * dt + 4 * lq) =
-            l_run > 0.f ? o[dt] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
-    } else {
-      const int64_t pi = qh * max_parts + it.part;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(part_o + pi * HD + 16 * dt + 4 * lq) = o[dt];
-      if (lq == 0) {
-        part_ml[2 * pi] = m_ref;
-        part_ml[2 * pi + 1] = l_run;
-      }
     }
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4 *>(out + qh * HD + 16 * dt + 4 * lq) =
+          l_run > 0.f ? o[dt] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
   // STAGES - 1 tiles in flight while one is computed; loads past the last
@@ -2405,6 +2473,47 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     else if (left > 24) __builtin_amdgcn_s_setprio(1);
     else __builtin_amdgcn_s_setprio(0);
   };
+  // The tile loop stops at `stop`: the item's end or, inside a run, the end
+  // of the current partition. There the partition's partial goes to the
+  // wave's LDS slot cur.part - cur.p0 (fewer than kRunSlots: runs are at
+  // most kRunSlots + 1 partitions) and the next partition starts from empty
+  // accumulators (the tiles in flight are the next partition's). One test
+  // per tile, as for the item's end alone: a separate test per tile cost the
+  // Qwen2.5-7B step 3% (the tiles' work no longer overlapped across it).
+  auto part_stop = [&]() __attribute__((always_inline)) {
+    const int e = (cur.part + 1) * cur.pt_tiles;
+    return e < cur.b1 ? e : cur.b1;
+  };
+  int stop = part_stop();
+  auto next_part = [&]() __attribute__((always_inline)) {
+    if constexpr (RUNS) {
+      reduce_acc();
+      const int slot = cur.part - cur.p0;
+      if (hi_lane) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) srun_o[wv][slot][dt][lq * NQ + lr] = oacc[0][dt];
+        if (lq == 0) {
+          srun_ml[wv][slot][lr][0] = m_ref;
+          srun_ml[wv][slot][lr][1] = l_run;
+        }
+      }
+      reset();
+      ++cur.part;
+      stop = part_stop();
+    }
+  };
+  // After tile b - 1 (b incremented): false when the item is done.
+  auto more = [&]() __attribute__((always_inline)) {
+    if constexpr (RUNS) {
+      if (b >= stop) {
+        if (b >= cur.b1) return false;
+        next_part();
+      }
+      return true;
+    } else {
+      return b < cur.b1;
+    }
+  };
   if (b < cur.b1) {
     if constexpr (STAGES == 3) {
       Stage s0, s1, s2;
@@ -2421,15 +2530,18 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         load_b(b + 2, en, s2);
         compute_tile(b, s0);
         LTKV_STAMP_ONCE(3);
-        if (++b >= cur.b1) break;
+        ++b;
+        if (!more()) break;
         en = entry_of(b + 3);
         load_b(b + 2, ea, s0);
         compute_tile(b, s1);
-        if (++b >= cur.b1) break;
+        ++b;
+        if (!more()) break;
         ea = entry_of(b + 3);
         load_b(b + 2, en, s1);
         compute_tile(b, s2);
-        if (++b >= cur.b1) break;
+        ++b;
+        if (!more()) break;
         en = ea;
       }
     } else {
@@ -2446,16 +2558,32 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
         load_b(b + 1, en, s1);
         compute_tile(b, s0);
         LTKV_STAMP_ONCE(3);
-        if (++b >= cur.b1) break;
+        ++b;
+        if (!more()) break;
         en = entry_of(b + 2);
         load_b(b + 1, ea, s0);
         compute_tile(b, s1);
-        if (++b >= cur.b1) break;
+        ++b;
+        if (!more()) break;
       }
     }
   }
   LTKV_STAMP(4);
   finish(cur);
+  // The run's staged partials (partitions p0 .. part - 1).
+  if (RUNS && hi_lane) {
+    const int64_t qh = cur.qi * n_heads + (int64_t)kvh0 * G + lr;
+    for (int slot = 0; slot < cur.part - cur.p0; ++slot) {  // uniform
+      const int64_t pi = qh * max_parts + cur.p0 + slot;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4 *>(part_o + pi * HD + 16 * dt + 4 * lq) = srun_o[wv][slot][dt][lq * NQ + lr];
+      if (lq == 0) {
+        part_ml[2 * pi] = srun_ml[wv][slot][lr][0];
+        part_ml[2 * pi + 1] = srun_ml[wv][slot][lr][1];
+      }
+    }
+  }
 #ifdef LTKV_TIMELINE
   LTKV_STAMP(5);
   tl_[6] = (unsigned long long)(cur.b1 - cur.b0);
@@ -2476,19 +2604,43 @@ inline bool decode_ordered(const AttnArgs &a) {
 // One wave per item (a partition of NH kv heads of one query), kDecodeWaves
 // consecutive items per work-group; the grid is rounded up to whole
 // work-groups and the waves past the last item leave at once.
-template <typename T, int HD, int G, int NH>
-hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+template <typename T, int HD, int G, int NH, bool RUNS>
+hipError_t launch_attn_mfma_k(const PoolGeom &g, const AttnArgs &a, int slots, hipStream_t s) {
   constexpr int nw = kDecodeWaves;
   const unsigned grid = (unsigned)((a.n * (a.n_kv_heads / NH) * a.max_parts + nw - 1) / nw);
-  attn_mfma_kernel<T, HD, G, NH><<<grid, 64 * nw, 0, s>>>(
+  attn_mfma_kernel<T, HD, G, NH, RUNS><<<grid, 64 * nw, 0, s>>>(
       static_cast<const T *>(a.k_layer), static_cast<const T *>(a.v_layer), a.q, a.tables, a.table_stride,
       a.lens, a.out, a.part_o, a.part_ml, a.n_kv_heads, g.n_blocks, g.block_stride, g.slot_stride,
       g.head_stride, a.scale * kLog2e, a.part_tokens, a.split, a.max_parts, a.pre_parts, a.qmap,
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
       a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts, a.new_slots, a.new_k, a.new_v, a.new_stride,
       static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)), a.n,
-      decode_ordered(a) ? 1 : 0, a.status);
+      decode_ordered(a) ? 1 : 0, slots, a.status);
   return launch_merge<HD>(a, s, true);
+}
+
+// Ordered launches of f16 two-head waves whose grid holds at least twice the
+// waves the chip holds at once take the kernel with runs of partitions (the
+// lengths then decide the run length; it may still be 1); the others the
+// kernel without. Both give the same bits.
+template <typename T, int HD, int G, int NH>
+hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t s) {
+  constexpr int nw = kDecodeWaves;
+  if constexpr (NH == 2 && !std::is_same_v<T, int8_t>) {
+    // Waves the chip holds at once (work-groups per CU from the kernel's
+    // registers and LDS).
+    static const int per_cu = [] {
+      int blocks = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, attn_mfma_kernel<T, HD, G, NH, true>, 64 * nw,
+                                                       0) != hipSuccess)
+        blocks = 0;
+      return blocks * nw;
+    }();
+    const int64_t slots = (int64_t)per_cu * a.cu_count;
+    if (decode_ordered(a) && slots > 0 && a.n * (a.n_kv_heads / NH) * a.max_parts >= 2 * slots)
+      return launch_attn_mfma_k<T, HD, G, NH, true>(g, a, (int)slots, s);
+  }
+  return launch_attn_mfma_k<T, HD, G, NH, false>(g, a, 0, s);
 }
 
 template <typename T, int HD, int G>

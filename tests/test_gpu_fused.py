@@ -84,6 +84,13 @@ def test_fused_step_fixed_partitions(gpu, partition):
     _step(gpu, "f16", 128, 4, 8, [5, 64, 65, 700, 2049], partition=partition, seed=partition)
 
 
+def test_fused_step_partition_runs(gpu):
+    # 16 queries of ~2k tokens in 64-token partitions: more than twice the
+    # wave slots in partition items, so waves take runs of partitions and the
+    # one whose run ends the query writes the new row
+    _step(gpu, "f16", 128, 4, 8, [1990 + 37 * i for i in range(16)], partition=64, seed=9)
+
+
 def test_fused_step_skipped_cells(gpu):
     _step(gpu, "f16", 128, 4, 8, [10, 40, 300], seed=3, skip=(1,))
 

@@ -558,6 +558,36 @@ def test_attention_batch_independence(gpu, dtype, n_batch):
         np.testing.assert_array_equal(one[0].view(np.uint32), full[i].view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+def test_attention_partition_runs_match_single_partitions(gpu, dtype):
+    """A batch with at least twice as many partition items as the chip holds
+    waves (fixed 64-token partitions, 24 queries of 1.5-3k tokens: ~4k-7k
+    items times the kv-head groups on 1024 or 2048 wave slots) has each wave
+    stream a run of consecutive partitions, writing each partition's partial
+    as it passes; every query's output equals, bit for bit, the one it gets
+    alone (a wave per partition), and the batch is within the tolerance of
+    the oracle."""
+    import torch
+
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(1500, 3000, size=24)]
+    lens[3] = 1  # a one-token query among them
+    blocks = sum(-(-n // BLOCK) for n in lens) + 8
+    g, o = _caches(1, 1024, blocks * BLOCK, dtype, rng.permutation(blocks))
+    g.set_attention_partition(64)
+    fill_sequences([("gpu", g), ("oracle", o)], dict(enumerate(lens)), rng, 1024)
+    q = rng.standard_normal((len(lens), 32 * 128), dtype=np.float32)
+    tables, la = tables_and_lens(g, range(len(lens)), lens)
+    dq, dt, dl = (torch.from_numpy(x).to(gpu) for x in (q, tables, la))
+    full = g.decode_attention(0, dq, dt, dl, 32, 128).cpu().numpy()
+    for i in (0, 3, 11, 23):
+        one = g.decode_attention(0, dq[i:i + 1].contiguous(), dt[i:i + 1].contiguous(),
+                                 dl[i:i + 1].contiguous(), 32, 128).cpu().numpy()
+        np.testing.assert_array_equal(one[0].view(np.uint32), full[i].view(np.uint32))
+    want = o.attention_tables(0, tables, la, q, 32, 128, threads=8)
+    attention_close(full, want, dtype)
+
+
 def test_attention_workspace_reuse_across_shapes(gpu):
     """Calls of different batch sizes and table widths alternate on one cache
     (its partition workspace and counters are reused); each must match."""
