@@ -1693,14 +1693,14 @@ struct OrderShapes {
   int key[kOrderChunks], keyl[kOrderChunks], items[kOrderChunks], len[kOrderChunks];
 };
 
-template <bool FIRST_WAVE_COUNTS = false>
+template <bool FIRST_WAVE_COUNTS = false, bool RUNS = false>
 __device__ __forceinline__ int decode_order_setup(const int32_t *__restrict__ lens, int64_t n, int64_t max_len,
                                                   int part_tokens, int split, int lane, int32_t *hist,
                                                   OrderShapes &sh, int n_groups, int slots, int max_run) {
   if (lane < kOrderClasses) hist[lane] = 0;
   __syncthreads();
   int pt[kOrderChunks];
-  int total = 0;
+  int k = 1;
 #pragma unroll
   for (int c = 0; c < kOrderChunks; ++c) {
     sh.key[c] = 0;
@@ -1708,17 +1708,24 @@ __device__ __forceinline__ int decode_order_setup(const int32_t *__restrict__ le
     sh.items[c] = 0;
     sh.len[c] = 0;
     pt[c] = 1;
-    if ((int64_t)c * 64 + lane < n) {
+    if ((int64_t)c * 64 + lane < n)
       decode_query_parts(lens, (int64_t)c * 64 + lane, max_len, part_tokens, split, sh.len[c], pt[c],
                          sh.items[c]);
-      total += sh.items[c];
-    }
   }
+  if constexpr (RUNS) {  // the run length from the batch's partition items (a wave-wide sum)
+    int total = 0;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
-  const int64_t waves = (int64_t)__builtin_amdgcn_readfirstlane(total) * n_groups;
-  int k = slots > 0 && waves >= 2 * (int64_t)slots ? (int)(waves / slots) : 1;
-  k = k < max_run ? k : max_run;
+    for (int c = 0; c < kOrderChunks; ++c) total += sh.items[c];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+    const int64_t waves = (int64_t)__builtin_amdgcn_readfirstlane(total) * n_groups;
+    k = slots > 0 && waves >= 2 * (int64_t)slots ? (int)(waves / slots) : 1;
+    k = k < max_run ? k : max_run;
+  } else {
+    (void)n_groups;
+    (void)slots;
+    (void)max_run;
+  }
 #pragma unroll
   for (int c = 0; c < kOrderChunks; ++c) {
     if ((int64_t)c * 64 + lane < n) {
@@ -1859,7 +1866,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
                  int64_t max_len, const float *__restrict__ pre_o, const float *__restrict__ pre_ml,
                  int max_pre_parts, const int32_t *__restrict__ new_slots,
                  const float *__restrict__ new_k, const float *__restrict__ new_v, int64_t new_stride,
-                 T *kdst, T *vdst, int64_t n_queries, int order, int slots, int32_t *__restrict__ status) {
+                 T *kdst, T *vdst, int64_t n_queries, int order, int slots, int pair_items,
+                 int32_t *__restrict__ status) {
 #ifdef LTKV_TIMELINE
   unsigned long long tl_[8] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0, 0, 0};
 #endif
@@ -1930,12 +1938,24 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   const int lane = threadIdx.x & 63;
   const int lr = lane & 15, lq = lane >> 4;
   const int n_heads = n_kv_heads * G;
-  const int64_t wave_idx = gw / n_groups;
+  int64_t wave_idx = gw / n_groups;
+  // Two work-groups per CU (pair_items > 0: the items of the chip's first
+  // round of work-groups): the grid's first pair_items / 2 items and the
+  // next ones share CUs, so the second half takes its items in reverse (the
+  // longest item with the shortest of the round) and the pairs a CU's SIMDs
+  // hold add up to about the same tiles (q8_0 decode 87.5 -> 85.7 us). The
+  // reversal is a permutation of the grid's complete items [p / 2, p), so
+  // every item of the list still has its wave.
+  if (order && pair_items > 0) {
+    const int64_t w_items = (int64_t)gridDim.x * NW / n_groups;
+    const int64_t p = pair_items < w_items ? pair_items : w_items;
+    if (wave_idx >= p / 2 && wave_idx < p) wave_idx = p / 2 + (p - 1 - wave_idx);
+  }
   OrderShapes osh;
   int run = 1;
   if (order)
-    run = decode_order_setup<(NW > 1)>(lens, n_queries, max_len, part_tokens, split, lane, shist, osh, n_groups,
-                                       slots, RUNS ? kRunSlots + 1 : 1);
+    run = decode_order_setup<(NW > 1), RUNS>(lens, n_queries, max_len, part_tokens, split, lane, shist, osh,
+                                             n_groups, slots, kRunSlots + 1);
 
   // B operands Q'_a^T of the score product, one per kv head a of the wave:
   // column lr < NQ holds the hi part of query head lr of the wave, column
@@ -2605,7 +2625,7 @@ inline bool decode_ordered(const AttnArgs &a) {
 // consecutive items per work-group; the grid is rounded up to whole
 // work-groups and the waves past the last item leave at once.
 template <typename T, int HD, int G, int NH, bool RUNS>
-hipError_t launch_attn_mfma_k(const PoolGeom &g, const AttnArgs &a, int slots, hipStream_t s) {
+hipError_t launch_attn_mfma_k(const PoolGeom &g, const AttnArgs &a, int slots, int pair_items, hipStream_t s) {
   constexpr int nw = kDecodeWaves;
   const unsigned grid = (unsigned)((a.n * (a.n_kv_heads / NH) * a.max_parts + nw - 1) / nw);
   attn_mfma_kernel<T, HD, G, NH, RUNS><<<grid, 64 * nw, 0, s>>>(
@@ -2615,7 +2635,7 @@ hipError_t launch_attn_mfma_k(const PoolGeom &g, const AttnArgs &a, int slots, h
       static_cast<const uint16_t *>(a.k_scale), static_cast<const uint16_t *>(a.v_scale), a.rows, a.n_rows,
       a.max_len, a.pre_o, a.pre_ml, a.max_pre_parts, a.new_slots, a.new_k, a.new_v, a.new_stride,
       static_cast<T *>(const_cast<void *>(a.k_layer)), static_cast<T *>(const_cast<void *>(a.v_layer)), a.n,
-      decode_ordered(a) ? 1 : 0, slots, a.status);
+      decode_ordered(a) ? 1 : 0, slots, pair_items, a.status);
   return launch_merge<HD>(a, s, true);
 }
 
@@ -2638,9 +2658,19 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
     }();
     const int64_t slots = (int64_t)per_cu * a.cu_count;
     if (decode_ordered(a) && slots > 0 && a.n * (a.n_kv_heads / NH) * a.max_parts >= 2 * slots)
-      return launch_attn_mfma_k<T, HD, G, NH, true>(g, a, (int)slots, s);
+      return launch_attn_mfma_k<T, HD, G, NH, true>(g, a, (int)slots, 0, s);
   }
-  return launch_attn_mfma_k<T, HD, G, NH, false>(g, a, 0, s);
+  // Work-groups per CU of the kernel without runs; with two, the first
+  // round's items are paired longest with shortest.
+  static const int wg_per_cu = [] {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, attn_mfma_kernel<T, HD, G, NH, false>, 64 * nw, 0) !=
+        hipSuccess)
+      blocks = 0;
+    return blocks;
+  }();
+  const int pair_items = wg_per_cu == 2 ? 2 * a.cu_count * nw / (a.n_kv_heads / NH) : 0;
+  return launch_attn_mfma_k<T, HD, G, NH, false>(g, a, 0, pair_items, s);
 }
 
 template <typename T, int HD, int G>
