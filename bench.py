@@ -1419,7 +1419,7 @@ def bench_decode_q8(args):
 def main():
     args = _args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+        print(json.dumps({"error": "ltkv's bench runs on exactly one GPU; --gpus must be 1 "
                           "(the path shards by sequence across GPUs with no exchange)"}))
         sys.exit(2)
     import torch
