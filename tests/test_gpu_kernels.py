@@ -584,6 +584,10 @@ def test_attention_partition_runs_match_single_partitions(gpu, dtype):
         one = g.decode_attention(0, dq[i:i + 1].contiguous(), dt[i:i + 1].contiguous(),
                                  dl[i:i + 1].contiguous(), 32, 128).cpu().numpy()
         np.testing.assert_array_equal(one[0].view(np.uint32), full[i].view(np.uint32))
+    # the same batch by resident rows (the runs read the same table entries)
+    rows = torch.from_numpy(g.seq_rows(list(range(len(lens)))).astype(np.int32)).to(gpu)
+    by_rows = g.decode_attention_rows(0, dq, rows, dl, 32, 128).cpu().numpy()
+    np.testing.assert_array_equal(by_rows.view(np.uint32), full.view(np.uint32))
     want = o.attention_tables(0, tables, la, q, 32, 128, threads=8)
     attention_close(full, want, dtype)
 

@@ -43,6 +43,7 @@ def _filled(dtype, n_kv, hd, ctx, seed):
     ("f16", 32, 8, 128, 2048, 4097),   # Llama-3-8B decode shape, two kv heads per wave
     ("q8_0", 32, 8, 128, 3000, 9000),  # partitions cut in two; some queries beyond 4096 tokens
     ("f16", 28, 4, 128, 512, 8193),    # Qwen2.5-7B, one kv head per wave, up to 9 partitions
+    ("f16", 32, 8, 128, 11000, 13001),  # over twice the wave slots in partitions: runs per wave
     ("f32", 32, 4, 64, 128, 513),      # TinyLlama shape, vector-ALU kernel
 ])
 def test_noalloc_equals_decode_attention(gpu, dtype, n_heads, n_kv, hd, lo, hi):
