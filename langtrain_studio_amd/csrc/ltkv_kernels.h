@@ -173,6 +173,19 @@ __host__ __device__ inline int partition_tokens(int64_t len, int fixed) {
   return p < 64 ? 64 : (int)p;
 }
 
+// ceil(len / pt) for 0 <= len < 2^31 and pt > 0, in 32-bit arithmetic (a
+// 64-bit division is a long instruction sequence on the vector ALU, on the
+// path from a wave's start to its first loads).
+__host__ __device__ inline int div_up_tokens(int64_t len, int pt) {
+  return (int)(((uint32_t)len + (uint32_t)pt - 1u) / (uint32_t)pt);
+}
+
+// A query's partition size with the matrix-core kernel's cut (split 1 or 2).
+__host__ __device__ inline int split_partition(int64_t len, int part_tokens, int split) {
+  const int pt = partition_tokens(len, part_tokens);
+  return split == 1 ? pt : (split == 2 ? pt >> 1 : pt / split);
+}
+
 // Upper bound of partitions per query for contexts up to max_tokens (the
 // same for both per-query policies: at most four up to 4096 tokens).
 inline int max_partitions(int64_t max_tokens, int fixed) {

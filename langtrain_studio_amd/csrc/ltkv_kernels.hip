@@ -1009,13 +1009,13 @@ attn_merge_kernel(const float *__restrict__ part_o, const float *__restrict__ pa
   int64_t len = lens[qi];
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
-  const int pt = partition_tokens(len, part_tokens) / split;
+  const int pt = split_partition(len, part_tokens, split);
   const int npre = pre_parts ? pre_parts[qi] : 0;
   if (npre < 0) return;  // its group wrote the output
   // A single partition wrote its output directly; with group partials too
   // when the context kernel folds them (`folded`), else it wrote a partial.
   // An empty remainder (np == 0) leaves the group partials to this kernel.
-  const int np = (int)((len + pt - 1) / pt);
+  const int np = div_up_tokens(len, pt);
   if (np <= 1 && npre == 0) return;
   if (np == 1 && folded) return;
   if (npre == 0 && np <= NF) {
@@ -1678,8 +1678,8 @@ __device__ __forceinline__ void decode_query_parts(const int32_t *__restrict__ l
   if (len < 0) len = 0;
   if (len > max_len) len = max_len;
   clen = (int)len;
-  pt = partition_tokens(len, part_tokens) / split;
-  np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+  pt = split_partition(len, part_tokens, split);
+  np = len > 0 ? div_up_tokens(len, pt) : 1;
 }
 
 // Size classes and item counts of queries lane, 64 + lane, ... (n <=
@@ -2103,8 +2103,8 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
     // A query with group partials and nothing else to read (or whose group
     // wrote its output) has no work here.
     if (pre_parts && (pre_parts[qi] < 0 || (pre_parts[qi] > 0 && len == 0))) return;
-    const int pt = partition_tokens(len, part_tokens) / split;
-    const int np = len > 0 ? (int)((len + pt - 1) / pt) : 1;
+    const int pt = split_partition(len, part_tokens, split);
+    const int np = len > 0 ? div_up_tokens(len, pt) : 1;
     // the item's partitions: run of them from part * run (run 1 without order)
     part *= run;
     if (part >= np) return;
