@@ -1271,8 +1271,8 @@ def bench_decode_timeline(args):
     64 queries x U[2048, 4096]) from the profiling build: when each wave found
     its item, issued its first loads, computed its first tile and finished,
     and how many waves stream at each 10 µs. One line per launch of the last
-    `--steps` steps (at most 5), then the prefix-cow planned step's per-query
-    pass."""
+    `--steps` steps (at most 5), then the same launch on a q8_0 pool, one at
+    the Qwen2.5-7B shape and the prefix-cow planned step's per-query pass."""
     import torch
 
     read = _use_timeline_library()
@@ -1292,6 +1292,18 @@ def bench_decode_timeline(args):
         print(json.dumps({"workload": "decode-timeline llama3-8b-layer decode, 64 seqs ctx U[2048,4096], f16, "
                                       "unfused attention launch", "step": s, **_timeline_stats(read())}),
               flush=True)
+    del w
+    torch.cuda.synchronize()
+    # the same launch on a q8_0 pool (half partitions: two waves per SIMD)
+    w = Llama3Decode(1, args.seed, args.partition, dtype="q8_0")
+    w.append(0)
+    w.attend(0)
+    torch.cuda.synchronize()
+    read()
+    for _ in range(5):
+        w.attend(0)
+    print(json.dumps({"workload": "decode-timeline llama3-8b-layer decode, 64 seqs ctx U[2048,4096], q8_0, "
+                                  "unfused attention launch", **_timeline_stats(read())}), flush=True)
     del w
     torch.cuda.synchronize()
     _timeline_qwen_decode(read, args.seed)
