@@ -221,12 +221,18 @@ def test_long_context_full_size(gpu):
     del k_out, v_out
 
     q = torch.randn((B, N_HEADS * HD), generator=torch.Generator(device="cuda").manual_seed(8), device="cuda")
+    # 32 partitions of 1024 tokens per query, 4096 items x head pairs on the
+    # chip's wave slots: each wave streams a run of four partitions
     out = kv.decode_attention(0, q, d_tables, lens, N_HEADS, HD).cpu().numpy()
     o = _oracle_with_pool(kv, n_blocks)
     want = o.attention_tables(0, tables, lens.cpu().numpy(), q.cpu().numpy(), N_HEADS, HD, threads=16)
     attention_close(out, want, "f16")
-    # the same step with 4096-token partitions fixed (8 a query instead of 32),
-    # the setting an engine running dozens of long queries would choose
+    # a query alone (a wave per partition) gives the bits it gets in the batch
+    for i in (0, 17):
+        one = kv.decode_attention(0, q[i:i + 1].contiguous(), d_tables[i:i + 1].contiguous(),
+                                  lens[i:i + 1].contiguous(), N_HEADS, HD).cpu().numpy()
+        np.testing.assert_array_equal(one[0].view(np.uint32), out[i].view(np.uint32))
+    # the same step with 4096-token partitions fixed (8 a query instead of 32)
     kv.set_attention_partition(4096)
     out4 = kv.decode_attention(0, q, d_tables, lens, N_HEADS, HD).cpu().numpy()
     kv.set_attention_partition(0)
