@@ -2660,8 +2660,8 @@ hipError_t launch_attn_mfma_t(const PoolGeom &g, const AttnArgs &a, hipStream_t 
     if (decode_ordered(a) && slots > 0 && a.n * (a.n_kv_heads / NH) * a.max_parts >= 2 * slots)
       return launch_attn_mfma_k<T, HD, G, NH, true>(g, a, (int)slots, 0, s);
   }
-  // Work-groups per CU of the kernel without runs; with two, the first
-  // round's items are paired longest with shortest.
+  // Work-groups per CU of the kernel without runs; with two, the items of
+  // the work-groups the chip starts with are paired longest with shortest.
   static const int wg_per_cu = [] {
     int blocks = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, attn_mfma_kernel<T, HD, G, NH, false>, 64 * nw, 0) !=
