@@ -325,6 +325,47 @@ def test_gather_ragged_matches_rows(gpu, dtype):
     assert (kh[total:] == -1).all() and (vh[total:] == -1).all()
 
 
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+def test_empty_batches_change_nothing(gpu, dtype):
+    """Every device op with an empty batch (n = 0: empty tensors, so null
+    device pointers) succeeds, launches nothing and leaves the pools and the
+    fault word as they were, as the reference's loops over an empty batch do
+    (model.rs:380-475 with no tokens)."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    kv_dim, head_dim, n_heads = 256, 64, 8
+    g, o = _caches(1, kv_dim, 32 * BLOCK, dtype, rng.permutation(32))
+    fill_sequences([("gpu", g), ("oracle", o)], {0: 40, 1: 7}, rng, kv_dim)
+    g.synchronize()
+    before = [p.copy() for p in g.read_pool(0)]
+    i32 = torch.zeros(0, dtype=torch.int32, device=gpu)
+    f32 = torch.zeros((0, kv_dim), dtype=torch.float32, device=gpu)
+    q = torch.zeros((0, n_heads * head_dim), dtype=torch.float32, device=gpu)
+    tables = torch.zeros((0, 4), dtype=torch.int32, device=gpu)
+    assert g.append_batch(np.zeros(0, np.uint32), np.zeros(0, np.uint64)).size == 0
+    g.write_batch(0, i32, f32, f32)
+    g.write_batch_ordered(0, i32, f32, f32, i32)
+    g.rope_init(10000.0, head_dim, head_dim, False, 64)
+    g.write_rope(0, i32, i32, f32, f32, q, n_heads)
+    g.copy_blocks(torch.zeros((0, 2), dtype=torch.int32, device=gpu))
+    assert g.decode_attention(0, q, tables, i32, n_heads, head_dim).numel() == 0
+    assert g.decode_attention(0, q, tables, i32, n_heads, head_dim, noalloc=True).numel() == 0
+    assert g.decode_attention_rows(0, q, i32, i32, n_heads, head_dim).numel() == 0
+    assert g.slot_mapping(i32, torch.zeros(0, dtype=torch.int64, device=gpu)).numel() == 0
+    if dtype == "f16":
+        assert g.append_decode_attention(0, i32, f32, f32, q, tables, i32, n_heads, head_dim).numel() == 0
+        g.gather(0, tables, i32, torch.zeros(0, dtype=torch.int64, device=gpu),
+                 torch.zeros((1, kv_dim), dtype=torch.float16, device=gpu),
+                 torch.zeros((1, kv_dim), dtype=torch.float16, device=gpu))
+    g.plan_attention([], [], n_heads, head_dim)
+    assert g.planned_attention(0, q).numel() == 0
+    g.synchronize()  # no fault recorded
+    after = g.read_pool(0)
+    for b, a in zip(before, after):
+        np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
 def test_rows_host_convenience(gpu):
     rng = np.random.default_rng(6)
     g, o = _caches(2, 128, 64 * BLOCK, "f16", rng.permutation(64))
