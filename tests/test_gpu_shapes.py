@@ -74,7 +74,7 @@ def test_write_gather_rows_any_kv_dim(gpu, dtype, kv_dim):
 
 @pytest.mark.parametrize("dtype", ["f16", "f32", "q8_0"])
 @pytest.mark.parametrize("head_dim,group,n_kv", [(32, 4, 2), (96, 5, 1), (80, 16, 2), (256, 8, 1),
-                                                 (128, 12, 1), (64, 32, 1), (160, 2, 2)])
+                                                 (128, 12, 1), (64, 32, 1), (160, 2, 2), (1024, 2, 1)])
 def test_attention_any_shape(gpu, dtype, head_dim, group, n_kv):
     import torch
 
@@ -98,6 +98,23 @@ def test_attention_any_shape(gpu, dtype, head_dim, group, n_kv):
     one = g.decode_attention(0, torch.from_numpy(q[5:6]).to(gpu), torch.from_numpy(tables[5:6]).to(gpu),
                              torch.from_numpy(la[5:6]).to(gpu), n_heads, head_dim).cpu().numpy()
     np.testing.assert_array_equal(one[0].view(np.uint32), out[5].view(np.uint32))
+    g.synchronize()
+
+
+def test_attention_head_dim_beyond_limit_is_refused(gpu):
+    """head_dim 1024 is the largest the kernels take; 1056 (a multiple of 32
+    past it) is refused with LTKV_ERR_ARG before anything is launched."""
+    import torch
+
+    from langtrain_studio_amd import KvError
+
+    rng = np.random.default_rng(3)
+    g, o = _caches(1056, 4, "f16", rng)
+    fill_sequences([("gpu", g), ("oracle", o)], {0: 5}, rng, 1056)
+    tables, la = tables_and_lens(g, [0], [5])
+    q = torch.zeros((1, 1056), dtype=torch.float32, device=gpu)
+    with pytest.raises(KvError, match="at most 1024"):
+        g.decode_attention(0, q, torch.from_numpy(tables).to(gpu), torch.from_numpy(la).to(gpu), 1, 1056)
     g.synchronize()
 
 
