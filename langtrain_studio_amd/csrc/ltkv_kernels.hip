@@ -2816,8 +2816,11 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   constexpr int DT = HD / 16;                // 16-wide d tiles of the output
   // LDS bytes per staged row, f16. The pads keep the score product's K
   // reads (16 bytes a lane) and the transposing V reads (8 bytes a lane,
-  // four rows x four columns per 16 lanes) free of bank conflicts.
-  constexpr int ROWK = HD * 2 + 16;
+  // four rows x four columns per 16 lanes) free of bank conflicts: 0
+  // SQ_LDS_BANK_CONFLICT cycles with these pitches, 12.4 M per prefill
+  // 8 x 512 dispatch with K rows padded by 16 bytes (prefill 1-2% slower),
+  // 25 M with V rows padded by 16 or 48, 87-99 M with either unpadded.
+  constexpr int ROWK = HD * 2 + 32;
   constexpr int ROWV = HD * 2 + 32;
   constexpr int VPR = HD * (int)sizeof(T) / 16;  // 16-byte vectors per pool row
   constexpr int NT = 64 * kMqWaves;  // threads
