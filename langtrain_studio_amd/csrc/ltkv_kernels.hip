@@ -1890,8 +1890,13 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   constexpr int RPI = 64 / LPR;            // rows per load instruction
   constexpr int NLD = 16 / RPI;            // load instructions per tile, K or V
   constexpr int KB = 8 * (int)sizeof(T);   // bytes of an A slice of the score product
-  constexpr int KPITCH = RB + 16;          // LDS bytes per staged K row
-  constexpr int VPITCH = HD * 2 + 16;      // LDS bytes per staged V row (f16)
+  // LDS bytes per staged K row (as loaded) and V row (f16). f16 rows of 128
+  // elements take 32 bytes of pad: SQ_LDS_BANK_CONFLICT per launch 3.2 M ->
+  // 0.02 M at the Llama-3-8B shape (time unchanged) and 4.2 M -> 0.07 M at
+  // the Qwen2.5-7B step (1% faster) against 16; q8_0 rows keep 16 (32 gave
+  // it more conflicts, 8.0 M -> 9.5 M, and 1% more time).
+  constexpr int KPITCH = RB + (!Q8 && HD == 128 ? 32 : 16);
+  constexpr int VPITCH = HD * 2 + (!Q8 && HD == 128 ? 32 : 16);
   constexpr int NQ = NH * G;               // query heads of the wave
   constexpr int NSC = NH * KS * 16;        // q8_0 scale entries of a tile, K or V
   constexpr int STAGES = NH == 2 && Q8 ? 2 : 3;  // tiles in flight + 1
@@ -2816,11 +2821,12 @@ mq_attn_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
   constexpr int DT = HD / 16;                // 16-wide d tiles of the output
   // LDS bytes per staged row, f16. The pads keep the score product's K
   // reads (16 bytes a lane) and the transposing V reads (8 bytes a lane,
-  // four rows x four columns per 16 lanes) free of bank conflicts: 0
-  // SQ_LDS_BANK_CONFLICT cycles with these pitches, 12.4 M per prefill
-  // 8 x 512 dispatch with K rows padded by 16 bytes (prefill 1-2% slower),
-  // 25 M with V rows padded by 16 or 48, 87-99 M with either unpadded.
-  constexpr int ROWK = HD * 2 + 32;
+  // four rows x four columns per 16 lanes) free of bank conflicts: at
+  // head_dim 128, 0 SQ_LDS_BANK_CONFLICT cycles with these pitches, 12.4 M
+  // per prefill 8 x 512 dispatch with K rows padded by 16 bytes (prefill
+  // 1-2% slower), 25 M with V rows padded by 16 or 48, 87-99 M with either
+  // unpadded. head_dim 64 keeps its K pad of 16 bytes.
+  constexpr int ROWK = HD * 2 + (HD == 128 ? 32 : 16);
   constexpr int ROWV = HD * 2 + 32;
   constexpr int VPR = HD * (int)sizeof(T) / 16;  // 16-byte vectors per pool row
   constexpr int NT = 64 * kMqWaves;  // threads
