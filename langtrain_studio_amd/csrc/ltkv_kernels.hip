@@ -1893,8 +1893,9 @@ attn_mfma_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool, const
   // LDS bytes per staged K row (as loaded) and V row (f16). f16 rows of 128
   // elements take 32 bytes of pad: SQ_LDS_BANK_CONFLICT per launch 3.2 M ->
   // 0.02 M at the Llama-3-8B shape (time unchanged) and 4.2 M -> 0.07 M at
-  // the Qwen2.5-7B step (1% faster) against 16; q8_0 rows keep 16 (32 gave
-  // it more conflicts, 8.0 M -> 9.5 M, and 1% more time).
+  // the Qwen2.5-7B step (1% faster) against 16; q8_0 rows keep 16 (a K pad
+  // of 32 gave more conflicts, 8.0 M -> 9.5 M, and 1% more time; a V pad
+  // of 32 fewer, 6.4 M, at the same time).
   constexpr int KPITCH = RB + (!Q8 && HD == 128 ? 32 : 16);
   constexpr int VPITCH = HD * 2 + (!Q8 && HD == 128 ? 32 : 16);
   constexpr int NQ = NH * G;               // query heads of the wave
